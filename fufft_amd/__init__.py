@@ -1,0 +1,197 @@
+"""fuFFT for MI355X: Python binding of the C ABI in include/fufft/fufft.h.
+
+The compute path is the in-tree HIP library ``libfufft_amd.so`` (built by
+``fufft_amd.build``).  There is no fallback: if the library is missing, import
+fails loudly.  Device memory is whatever the caller passes -- torch tensors on
+``cuda`` (ROCm) or raw device pointers.
+
+torch is imported before the library is loaded so that both share torch's HIP
+runtime (torch bundles its own ``libamdhip64.so.7``; the loader then resolves
+the library's dependency to that same copy).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+try:  # must precede loading the HIP library, see module docstring
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - torch is part of the image
+    torch = None
+
+_LIB_PATH = Path(__file__).resolve().parent / "libfufft_amd.so"
+
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN = 0, -1, -2, -3, -4
+MID = {"mul": 0, "conj": 1, "none": 2}
+VARIANT = {"v16": 0, "r8": 1}
+LAYOUT = {"dr": 0, "lane": 1}
+FILTER_SPECTRUM, FILTER_TAPS = 0, 1
+BFP_BLOCK = 64
+VALUES_PER_LANE = {"v16": 16, "r8": 8}
+
+
+class FufftError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: {lib.fufft_status_string(status).decode()} ({status})")
+
+
+def _load() -> C.CDLL:
+    if not _LIB_PATH.exists():
+        raise FileNotFoundError(
+            f"{_LIB_PATH} is missing: build it with `python -m fufft_amd.build` "
+            "(there is no CPU fallback)")
+    L = C.CDLL(str(_LIB_PATH))
+    i64, i32, vp, fp = C.c_int64, C.c_int, C.c_void_p, C.POINTER(C.c_float)
+    sig = {
+        "fufft_init": ([i32], i32),
+        "fufft_status_string": ([i32], C.c_char_p),
+        "fufft_supported": ([i64, i32], i32),
+        "fufft_plan_radices": ([i64, i32, C.POINTER(C.c_int)], i32),
+        "fufft_digit_order": ([i64, i32, C.POINTER(C.c_int32)], i32),
+        "fufft_plan_filter_f32": ([i64, i32, i32, i32, i32, vp, vp], i32),
+        "fufft_twiddle_table_host": ([i32, vp], i32),
+        "fufft_conv_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp], i32),
+        "fufft_fwd_f32": ([vp, vp, i64, i64, i32, vp], i32),
+        "fufft_apply_f32": ([vp, i64, vp, i64, vp, i64, i64, i32, i32, i32, vp], i32),
+        "fufft_conv_r2_f32": ([vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_bfp_exponent": ([C.c_float], i32),
+        "fufft_bfp_quantize": ([vp, i64, vp, vp], i32),
+        "fufft_bfp_dequantize": ([vp, vp, i64, vp], i32),
+        "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_large_plan": ([i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
+        "fufft_large_digit_order": ([i64, C.POINTER(C.c_int32)], i32),
+        "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
+        "fufft_conv_large_f32": ([vp, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, vp, vp], i32),
+        "fufft_conv2d_f32": ([vp, vp, i64, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp], i32),
+        "fufft_fwd2d_f32": ([vp, vp, i64, i64, i64, vp], i32),
+        "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name, None)
+        if f is None:
+            continue
+        f.argtypes, f.restype = args, res
+    return L
+
+
+lib = _load()
+
+
+def check(status: int, where: str) -> None:
+    if status != OK:
+        raise FufftError(status, where)
+
+
+def _ptr(x) -> int | None:
+    """Device (or host) address of a tensor / numpy array / int / None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if isinstance(x, np.ndarray):
+        return x.ctypes.data
+    return x.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+# ---- host planning ---------------------------------------------------------------
+
+def init(device: int = 0) -> None:
+    check(lib.fufft_init(device), "fufft_init")
+
+
+def supported(n: int, variant: str = "v16") -> bool:
+    return bool(lib.fufft_supported(n, VARIANT[variant]))
+
+
+def plan_radices(n: int, variant: str = "v16") -> list[int]:
+    buf = (C.c_int * 64)()
+    np_ = lib.fufft_plan_radices(n, VARIANT[variant], buf)
+    if np_ < 0:
+        raise FufftError(np_, "fufft_plan_radices")
+    return list(buf[:np_])
+
+
+def digit_order(n: int, variant: str = "v16") -> np.ndarray:
+    perm = np.empty(n, dtype=np.int32)
+    check(lib.fufft_digit_order(n, VARIANT[variant], perm.ctypes.data_as(C.POINTER(C.c_int32))),
+          "fufft_digit_order")
+    return perm
+
+
+def plan_filter(x: np.ndarray, n: int, variant: str = "v16", layout: str = "dr",
+                kind: int = FILTER_SPECTRUM, fold_inv_n: bool = True) -> np.ndarray:
+    """Filter as the conv kernels read it, from a natural-order spectrum or taps."""
+    src = np.ascontiguousarray(x, dtype=np.complex64)
+    assert src.size == n
+    out = np.empty(n, dtype=np.complex64)
+    check(lib.fufft_plan_filter_f32(n, VARIANT[variant], LAYOUT[layout], kind, int(fold_inv_n),
+                                    src.ctypes.data, out.ctypes.data), "fufft_plan_filter_f32")
+    return out
+
+
+def twiddle_table_host(log_max: int) -> np.ndarray:
+    out = np.empty(2 << log_max, dtype=np.complex64)
+    check(lib.fufft_twiddle_table_host(log_max, out.ctypes.data), "fufft_twiddle_table_host")
+    return out
+
+
+# ---- launches ------------------------------------------------------------------------
+
+def conv(inp, filt, out, n: int, batch: int, filt_stride: int = 0, mid: str = "mul",
+         variant: str = "v16", layout: str = "dr", stream=None) -> None:
+    check(lib.fufft_conv_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), n, batch, MID[mid],
+                             VARIANT[variant], LAYOUT[layout], _stream(stream)), "fufft_conv_f32")
+
+
+def fwd(inp, spec, n: int, batch: int, variant: str = "v16", stream=None) -> None:
+    check(lib.fufft_fwd_f32(_ptr(inp), _ptr(spec), n, batch, VARIANT[variant], _stream(stream)),
+          "fufft_fwd_f32")
+
+
+def apply(spec, filt, out, n: int, batch: int, spec_stride: int = 0, filt_stride: int = 0,
+          mid: str = "mul", variant: str = "v16", layout: str = "dr", stream=None) -> None:
+    check(lib.fufft_apply_f32(_ptr(spec), spec_stride, _ptr(filt), filt_stride, _ptr(out), n,
+                              batch, MID[mid], VARIANT[variant], LAYOUT[layout], _stream(stream)),
+          "fufft_apply_f32")
+
+
+def conv_r2(x, y, filt, u, v, n: int, batch: int, filt_stride: int = 0, variant: str = "v16",
+            layout: str = "dr", stream=None) -> None:
+    check(lib.fufft_conv_r2_f32(_ptr(x), _ptr(y), _ptr(filt), filt_stride, _ptr(u), _ptr(v), n,
+                                batch, VARIANT[variant], LAYOUT[layout], _stream(stream)),
+          "fufft_conv_r2_f32")
+
+
+def bfp_exponent(absmax: float) -> int:
+    return lib.fufft_bfp_exponent(absmax)
+
+
+def bfp_quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
+    q = np.empty(2 * src.size, dtype=np.int16)
+    e = np.empty(src.size // BFP_BLOCK, dtype=np.int8)
+    check(lib.fufft_bfp_quantize(src.ctypes.data, src.size, q.ctypes.data, e.ctypes.data),
+          "fufft_bfp_quantize")
+    return q, e
+
+
+def bfp_dequantize(q: np.ndarray, e: np.ndarray) -> np.ndarray:
+    npts = q.size // 2
+    x = np.empty(npts, dtype=np.complex64)
+    check(lib.fufft_bfp_dequantize(np.ascontiguousarray(q).ctypes.data,
+                                   np.ascontiguousarray(e).ctypes.data, npts, x.ctypes.data),
+          "fufft_bfp_dequantize")
+    return x

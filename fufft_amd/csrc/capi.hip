@@ -1,0 +1,383 @@
+// C-ABI layer: argument checking, host planning, the device twiddle table and
+// dispatch to the kernel translation units.  Declarations and the reference
+// interfaces each entry point replaces are in include/fufft/fufft.h.
+#include "fufft_internal.hpp"
+#include "fufft_plan.hpp"
+#include "../../include/fufft/fufft.h"
+
+#include <atomic>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+namespace fufft {
+
+// ---- twiddle table ----------------------------------------------------------------
+// Static device memory: every GPU the library runs on holds one copy, filled
+// once by fufft_init.  Level P = 2^p (1 <= p <= FUFFT_TW_LOG_MAX) occupies
+// entries [P, 2P): (cos, sin)(2*pi*t/P) rounded to fp32.
+__device__ float2 g_twiddle[FUFFT_TW_ENTRIES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceState {
+   std::atomic<int> ready{0};
+   const float2*    tw = nullptr;
+};
+DeviceState g_dev[kMaxDevices];
+std::mutex  g_init_mutex;
+
+// (cos, sin)(2*pi*t/P) in double, rounded to float.  The CPU oracle
+// (oracle/oracle.c: table_cs) evaluates this same expression.
+void table_entry(int P, int64_t t, float* c, float* s)
+{
+   const double th = 6.283185307179586476925286766559 * (double)t / (double)P;
+   *c = (float)cos(th);
+   *s = (float)sin(th);
+}
+
+void fill_table(int log_max, float* out)
+{
+   out[0] = out[1] = out[2] = out[3] = 0.0f;
+   for(int p = 1; p <= log_max; p++) {
+      const int P = 1 << p;
+      for(int t = 0; t < P; t++) table_entry(P, t, &out[2 * (P + t)], &out[2 * (P + t) + 1]);
+   }
+}
+
+int lds_layout()
+{
+   static const int layout = [] {
+      const char* e = std::getenv("FUFFT_LDS_LAYOUT");
+      return (e && std::strcmp(e, "pad") == 0) ? LAYOUT_PAD : LAYOUT_XOR;
+   }();
+   return layout;
+}
+
+int init_device(int dev)
+{
+   if(dev < 0 || dev >= kMaxDevices) return FUFFT_ERR_INVALID;
+   DeviceState& d = g_dev[dev];
+   if(d.ready.load(std::memory_order_acquire)) return FUFFT_OK;
+   std::lock_guard<std::mutex> lock(g_init_mutex);
+   if(d.ready.load(std::memory_order_relaxed)) return FUFFT_OK;
+
+   int prev = 0;
+   if(hipGetDevice(&prev) != hipSuccess) return FUFFT_ERR_HIP;
+   if(prev != dev && hipSetDevice(dev) != hipSuccess) return FUFFT_ERR_HIP;
+   std::vector<float> host(2 * (size_t)FUFFT_TW_ENTRIES);
+   fill_table(FUFFT_TW_LOG_MAX, host.data());
+   int status = FUFFT_OK;
+   void* addr = nullptr;
+   if(hipMemcpyToSymbol(HIP_SYMBOL(g_twiddle), host.data(), host.size() * sizeof(float), 0,
+                        hipMemcpyHostToDevice) != hipSuccess ||
+      hipGetSymbolAddress(&addr, HIP_SYMBOL(g_twiddle)) != hipSuccess || addr == nullptr)
+      status = FUFFT_ERR_HIP;
+   if(prev != dev) (void)hipSetDevice(prev);
+   if(status != FUFFT_OK) return status;
+   d.tw = static_cast<const float2*>(addr);
+   d.ready.store(1, std::memory_order_release);
+   return FUFFT_OK;
+}
+
+// twiddle table of the current device, initialising it on first use
+int current_table(const float2** tw)
+{
+   int dev = 0;
+   if(hipGetDevice(&dev) != hipSuccess) return FUFFT_ERR_HIP;
+   const int st = init_device(dev);
+   if(st != FUFFT_OK) return st;
+   *tw = g_dev[dev].tw;
+   return FUFFT_OK;
+}
+
+int status_of(hipError_t e) { return e == hipSuccess ? FUFFT_OK : FUFFT_ERR_HIP; }
+
+bool pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+int values_per_lane(int variant)
+{
+   return variant == FUFFT_V16 ? 16 : variant == FUFFT_R8 ? 8 : 0;
+}
+
+// factorisation lead * V^k, lead first (cpu_mixed.cpp:36-49)
+int factor(int64_t n, int v, int* radices)
+{
+   int m = 0;
+   while(((int64_t)1 << m) < n) m++;
+   int vb = 0;
+   while((1 << vb) < v) vb++;
+   const int a = m / vb, r = m % vb;
+   int p = 0;
+   if(r) radices[p++] = 1 << r;
+   for(int i = 0; i < a; i++) radices[p++] = v;
+   return p;
+}
+
+// bit-group reversal over the radix widths in pass order
+// (mixedrev_host, bench_fufft.cu:63-82)
+int32_t group_reverse(int32_t idx, const int* radices, int np)
+{
+   int w[64], m = 0;
+   for(int i = 0; i < np; i++) {
+      w[i] = 0;
+      while((1 << w[i]) < radices[i]) w[i]++;
+      m += w[i];
+   }
+   int32_t d[64];
+   int pos = m;
+   for(int i = 0; i < np; i++) { pos -= w[i]; d[i] = (idx >> pos) & ((1 << w[i]) - 1); }
+   int32_t out = 0;
+   int op = m;
+   for(int i = np - 1; i >= 0; i--) { op -= w[i]; out |= d[i] << op; }
+   return out;
+}
+
+// in-place iterative radix-2 DFT in double (natural order), sign -1 = forward
+void dft_f64(std::vector<double>& x, int64_t n, int sign)
+{
+   for(int64_t i = 1, j = 0; i < n; i++) {
+      int64_t bit = n >> 1;
+      for(; j & bit; bit >>= 1) j ^= bit;
+      j ^= bit;
+      if(i < j) { std::swap(x[2 * i], x[2 * j]); std::swap(x[2 * i + 1], x[2 * j + 1]); }
+   }
+   for(int64_t len = 2; len <= n; len <<= 1) {
+      const int64_t half = len / 2;
+      for(int64_t k = 0; k < half; k++) {
+         const double th = 6.283185307179586476925286766559 * (double)k / (double)len;
+         const double wr = cos(th), wi = sign * sin(th);
+         for(int64_t i = 0; i < n; i += len) {
+            const int64_t a = i + k, b = i + k + half;
+            const double br = x[2 * b] * wr - x[2 * b + 1] * wi;
+            const double bi = x[2 * b] * wi + x[2 * b + 1] * wr;
+            x[2 * b]     = x[2 * a] - br;  x[2 * b + 1] = x[2 * a + 1] - bi;
+            x[2 * a]     = x[2 * a] + br;  x[2 * a + 1] = x[2 * a + 1] + bi;
+         }
+      }
+   }
+}
+
+// natural-order spectrum in double from taps or a given spectrum, 1/n folded
+std::vector<double> spectrum_of(int64_t n, int filter_kind, int fold_inv_n, const float* in)
+{
+   std::vector<double> s(2 * (size_t)n);
+   for(int64_t i = 0; i < 2 * n; i++) s[i] = in[i];
+   if(filter_kind == FUFFT_FILTER_TAPS) dft_f64(s, n, -1);
+   if(fold_inv_n)
+      for(auto& v : s) v /= (double)n;
+   return s;
+}
+
+}  // namespace
+}  // namespace fufft
+
+using namespace fufft;
+
+extern "C" {
+
+int fufft_init(int device) { return init_device(device); }
+
+const char* fufft_status_string(int status)
+{
+   switch(status) {
+      case FUFFT_OK:              return "ok";
+      case FUFFT_ERR_INVALID:     return "invalid argument";
+      case FUFFT_ERR_UNSUPPORTED: return "unsupported size or variant";
+      case FUFFT_ERR_HIP:         return "HIP runtime error";
+      case FUFFT_ERR_ALIGN:       return "pointer not 16-byte aligned";
+      default:                    return "unknown status";
+   }
+}
+
+int fufft_supported(int64_t n, int variant)
+{
+   const int v = values_per_lane(variant);
+   return (v && pow2(n) && n <= 16384 && conv1d_supported((int)n, v)) ? 1 : 0;
+}
+
+int fufft_plan_radices(int64_t n, int variant, int* radices)
+{
+   const int v = values_per_lane(variant);
+   if(!v || !radices || !pow2(n) || n < 2) return FUFFT_ERR_INVALID;
+   return factor(n, v, radices);
+}
+
+int fufft_digit_order(int64_t n, int variant, int32_t* perm)
+{
+   int r[64];
+   const int np = fufft_plan_radices(n, variant, r);
+   if(np < 0) return np;
+   if(!perm || n > ((int64_t)1 << 30)) return FUFFT_ERR_INVALID;
+   for(int64_t i = 0; i < n; i++) perm[i] = group_reverse((int32_t)i, r, np);
+   return FUFFT_OK;
+}
+
+int fufft_plan_filter_f32(int64_t n, int variant, int layout, int filter_kind,
+                          int fold_inv_n, const float* in, float* out)
+{
+   const int v = values_per_lane(variant);
+   if(!v || !in || !out || !pow2(n) || n < v) return FUFFT_ERR_INVALID;
+   if(layout != FUFFT_LAYOUT_DR && layout != FUFFT_LAYOUT_LANE) return FUFFT_ERR_INVALID;
+   if(filter_kind != FUFFT_FILTER_SPECTRUM && filter_kind != FUFFT_FILTER_TAPS) return FUFFT_ERR_INVALID;
+   int r[64];
+   const int np = factor(n, v, r);
+   const std::vector<double> s = spectrum_of(n, filter_kind, fold_inv_n, in);
+   const int64_t T = n / v;
+   for(int64_t i = 0; i < n; i++) {
+      const int32_t bin = group_reverse((int32_t)i, r, np);
+      // digit-order slot i; lane-major moves slot V*L + k to L + k*T
+      const int64_t dst = (layout == FUFFT_LAYOUT_DR) ? i : (i / v) + (i % v) * T;
+      out[2 * dst]     = (float)s[2 * bin];
+      out[2 * dst + 1] = (float)s[2 * bin + 1];
+   }
+   return FUFFT_OK;
+}
+
+int fufft_twiddle_table_host(int log_max, float* out)
+{
+   if(!out || log_max < 1 || log_max > FUFFT_TW_LOG_MAX) return FUFFT_ERR_INVALID;
+   fill_table(log_max, out);
+   return FUFFT_OK;
+}
+
+// ---- 1D fp32 --------------------------------------------------------------------------
+
+static int check_1d(int64_t n, int64_t batch, int variant, int mid, int layout, int* v)
+{
+   *v = values_per_lane(variant);
+   if(!*v) return FUFFT_ERR_INVALID;
+   if(mid < FUFFT_MID_MUL || mid > FUFFT_MID_NONE) return FUFFT_ERR_INVALID;
+   if(layout != FUFFT_LAYOUT_DR && layout != FUFFT_LAYOUT_LANE) return FUFFT_ERR_INVALID;
+   if(batch < 0 || batch > 0xffffffffll) return FUFFT_ERR_INVALID;
+   if(!pow2(n) || !fufft_supported(n, variant)) return FUFFT_ERR_UNSUPPORTED;
+   return FUFFT_OK;
+}
+
+static int filter_count(int64_t filt_stride, int64_t n, int64_t batch, uint32_t* fcount)
+{
+   if(filt_stride == 0) { *fcount = 1; return FUFFT_OK; }
+   if(filt_stride == n) { *fcount = (uint32_t)(batch > 0 ? batch : 1); return FUFFT_OK; }
+   return FUFFT_ERR_INVALID;
+}
+
+static int run_conv1d(int kind, int n, int v, const Conv1dParams& p, void* stream)
+{
+   if(p.ntrans == 0) return FUFFT_OK;
+   return status_of(launch_conv1d(kind, n, v, lds_layout(), p, static_cast<hipStream_t>(stream)));
+}
+
+int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
+                   void* out, int64_t n, int64_t batch, int mid, int variant,
+                   int layout, void* stream)
+{
+   int v = 0;
+   int st = check_1d(n, batch, variant, mid, layout, &v);
+   if(st != FUFFT_OK) return st;
+   if(!in || !out || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   Conv1dParams p{};
+   if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.in0 = in; p.filt = filt; p.out0 = out;
+   p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
+   return run_conv1d(K_CONV, (int)n, v, p, stream);
+}
+
+int fufft_fwd_f32(const void* in, void* spec, int64_t n, int64_t batch,
+                  int variant, void* stream)
+{
+   int v = 0;
+   int st = check_1d(n, batch, variant, FUFFT_MID_NONE, FUFFT_LAYOUT_DR, &v);
+   if(st != FUFFT_OK) return st;
+   if(!in || !spec) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(spec)) return FUFFT_ERR_ALIGN;
+   Conv1dParams p{};
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.in0 = in; p.out0 = spec; p.ntrans = (uint32_t)batch;
+   p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR;
+   return run_conv1d(K_FWD, (int)n, v, p, stream);
+}
+
+int fufft_apply_f32(const void* spec, int64_t spec_stride, const void* filt,
+                    int64_t filt_stride, void* out, int64_t n, int64_t batch,
+                    int mid, int variant, int layout, void* stream)
+{
+   int v = 0;
+   int st = check_1d(n, batch, variant, mid, layout, &v);
+   if(st != FUFFT_OK) return st;
+   if(!spec || !out || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(!aligned16(spec) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   Conv1dParams p{};
+   if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   if((st = filter_count(spec_stride, n, batch, &p.scount)) != FUFFT_OK) return st;
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.spec = spec; p.filt = filt; p.out0 = out;
+   p.ntrans = (uint32_t)batch; p.mid = mid; p.fl = layout;
+   return run_conv1d(K_APPLY, (int)n, v, p, stream);
+}
+
+int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
+                      int64_t filt_stride, float* u, float* v, int64_t n,
+                      int64_t batch, int variant, int layout, void* stream)
+{
+   int vl = 0;
+   int st = check_1d(n, batch, variant, FUFFT_MID_MUL, layout, &vl);
+   if(st != FUFFT_OK) return st;
+   if(!x || !y || !filt || !u || !v) return FUFFT_ERR_INVALID;
+   if(!aligned4(x) || !aligned4(y) || !aligned4(u) || !aligned4(v) || !aligned16(filt))
+      return FUFFT_ERR_ALIGN;
+   Conv1dParams p{};
+   if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.in0 = x; p.in1 = y; p.filt = filt; p.out0 = u; p.out1 = v;
+   p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = FUFFT_MID_MUL; p.fl = layout;
+   return run_conv1d(K_CONV_R2, (int)n, vl, p, stream);
+}
+
+// ---- BFP host codec -----------------------------------------------------------------
+
+int fufft_bfp_exponent(float absmax)
+{
+   uint32_t bits;
+   std::memcpy(&bits, &absmax, sizeof bits);
+   bits &= 0x7fffffffu;
+   const uint32_t xb = bits >> 23;
+   if(xb == 0) return -128;
+   // absmax = m * 2^(xb-126), m in [0.5, 1); 32767 * 2^(xb-141) >= absmax
+   // exactly when the 23 fraction bits are <= 0x7ffe00
+   const int e = (int)xb - 141 + ((bits & 0x7fffffu) > 0x7ffe00u ? 1 : 0);
+   return e < -128 ? -128 : e;
+}
+
+int fufft_bfp_quantize(const float* x, int64_t npts, int16_t* q, int8_t* e)
+{
+   if(!x || !q || !e || npts < 0 || npts % FUFFT_BFP_BLOCK) return FUFFT_ERR_INVALID;
+   for(int64_t b = 0; b < npts / FUFFT_BFP_BLOCK; b++) {
+      const float* xb = x + 2 * b * FUFFT_BFP_BLOCK;
+      float m = 0.0f;
+      for(int i = 0; i < 2 * FUFFT_BFP_BLOCK; i++) m = std::fmax(m, std::fabs(xb[i]));
+      const int ex = fufft_bfp_exponent(m);
+      e[b] = (int8_t)ex;
+      for(int i = 0; i < 2 * FUFFT_BFP_BLOCK; i++)
+         q[2 * b * FUFFT_BFP_BLOCK + i] = (int16_t)std::rint(std::ldexp(xb[i], -ex));
+   }
+   return FUFFT_OK;
+}
+
+int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float* x)
+{
+   if(!x || !q || !e || npts < 0 || npts % FUFFT_BFP_BLOCK) return FUFFT_ERR_INVALID;
+   for(int64_t b = 0; b < npts / FUFFT_BFP_BLOCK; b++)
+      for(int i = 0; i < 2 * FUFFT_BFP_BLOCK; i++)
+         x[2 * b * FUFFT_BFP_BLOCK + i] = std::ldexp((float)q[2 * b * FUFFT_BFP_BLOCK + i], e[b]);
+   return FUFFT_OK;
+}
+
+}  // extern "C"

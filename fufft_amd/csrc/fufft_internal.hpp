@@ -1,0 +1,67 @@
+// Internal interface between the C-ABI layer (capi.hip) and the kernel
+// translation units.  Not installed; the public contract is include/fufft/fufft.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fufft {
+
+// ---- 1D fused pipeline (conv1d.hip) ------------------------------------------------
+enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3 };
+
+struct Conv1dParams {
+   const void*   in0;      // complex input, or real x (K_CONV_R2)
+   const void*   in1;      // real y (K_CONV_R2)
+   const void*   spec;     // digit-order spectrum (K_APPLY)
+   const void*   filt;     // filter, digit order or lane-major
+   void*         out0;     // complex output / spectrum (K_FWD) / real u
+   void*         out1;     // real v (K_CONV_R2)
+   const float2* tw;       // device twiddle table
+   uint32_t      ntrans;   // transforms in the launch
+   uint32_t      fcount;   // transform t uses filter (t % fcount)
+   uint32_t      scount;   // transform t uses spectrum (t % scount)
+   int32_t       mid;      // MID_MUL / MID_CONJ / MID_NONE
+   int32_t       fl;       // FLT_DR / FLT_LANE
+};
+
+bool       conv1d_supported(int n, int v);
+hipError_t launch_conv1d(int kind, int n, int v, int layout, const Conv1dParams& p, hipStream_t s);
+
+// ---- int16 block floating point (bfp.hip) ---------------------------------------------
+struct BfpParams {
+   const void*   qin;      // int16 pairs
+   const int8_t* ein;      // one exponent per block
+   const void*   filt;     // fp32 filter
+   void*         qout;
+   int8_t*       eout;
+   const float2* tw;
+   uint32_t      ntrans;
+   uint32_t      fcount;
+   int32_t       mid;
+   int32_t       fl;
+};
+
+bool       bfp_supported(int n);
+hipError_t launch_bfp(int n, int layout, const BfpParams& p, hipStream_t s);
+
+// ---- four-step outer levels (large.hip) -------------------------------------------
+hipError_t launch_outer_pass(float2* buf, int64_t total, int R, int M, int sign, int dit,
+                             const float2* tw, hipStream_t s);
+
+// ---- 2D column kernels (conv2d.hip) -------------------------------------------------
+struct ColParams {
+   const void*   in;       // h x w complex images (rows contiguous)
+   void*         out;
+   const void*   filt;     // 2D filter, digit order per dimension
+   const float2* tw;
+   uint32_t      nimg;
+   uint32_t      fcount;
+   int32_t       mid;
+   int32_t       w;        // row length
+};
+enum { COL_CONV = 0, COL_FWD = 1, COL_APPLY = 2 };
+bool       col_supported(int h, int w);
+hipError_t launch_col(int kind, int h, const ColParams& p, hipStream_t s);
+
+}  // namespace fufft

@@ -1,0 +1,232 @@
+// Compile-time pass plan and LDS layouts shared by the 1D, BFP and 2D kernels.
+//
+// A transform of N = LEAD * V^NR points is held by T = N/V lanes, V values per
+// lane.  DIF pass p has radix R_p (LEAD first when LEAD > 1, then V) and stride
+// M_p = N / (R_0 ... R_p); DIT runs the same passes in reverse.  In pass p lane
+// L owns the G = V/R groups gidx = L + g*T, j = gidx % M, b = gidx / M, whose
+// taps sit at b*R*M + j + k*M (fufft.cuh:722-756); tap k of group g lives in
+// register g + k*G.  With that convention:
+//   - pass 0 reads position L + q*T into register q, so the first DIF pass
+//     loads straight from HBM and the last DIT pass stores straight to HBM
+//     (coalesced across lanes for every q);
+//   - the last DIF pass and the first DIT pass run at M = 1 with lane L owning
+//     positions L*V .. L*V + V-1 in registers, so the pointwise mid operation
+//     happens in registers between them (fufft.cuh:1435-1443);
+//   - every other pass boundary is one exchange through LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <utility>
+
+#include "fufft_device.hpp"
+
+namespace fufft {
+
+constexpr int ilog2c(int x) { int r = 0; while((1 << r) < x) r++; return r; }
+
+template<int N_, int V_>
+struct Plan {
+   static constexpr int N = N_, V = V_;
+   static constexpr int LOGN = ilog2c(N), LOGV = ilog2c(V);
+   static constexpr int NR   = LOGN / LOGV;
+   static constexpr int LEAD = 1 << (LOGN % LOGV);
+   static constexpr int NP   = NR + (LEAD > 1 ? 1 : 0);
+   static constexpr int T    = N / V;
+   static_assert((1 << LOGN) == N && (1 << LOGV) == V, "power-of-two sizes only");
+   static_assert(NR >= 1, "N must hold at least one radix-V pass");
+
+   static constexpr int radix(int p) { return (LEAD > 1 && p == 0) ? LEAD : V; }
+   static constexpr int stride(int p)
+   {
+      int M = N;
+      for(int i = 0; i <= p; i++) M /= radix(i);
+      return M;
+   }
+};
+
+// ---- compile-time loop --------------------------------------------------------
+template<class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>)
+{
+   (f(std::integral_constant<int, Is>{}), ...);
+}
+template<int COUNT, class F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+   static_for_impl(f, std::make_integer_sequence<int, COUNT>{});
+}
+
+// ---- LDS layouts ------------------------------------------------------------------
+// phys(i) maps logical position i of a transform to its float2 slot.  Every
+// pass touches positions base(L) + k*M; with 8-byte accesses a bank conflict
+// arises when lanes serviced in the same cycle hit equal slot numbers modulo
+// 16 (32 banks x 4 B, 16 lanes per cycle) or modulo 32 (64 banks, 32 lanes per
+// cycle).  Both layouts below are bijections; tests/test_lds_audit.py checks
+// every access pattern of every plan against both models.
+//
+// Xor: bits [0, v) ^= bits [v, 2v), bits [v, 5) ^= bits [2v, v+5).  Conflict
+// free under both models; costs about one v_xor per access in the M = 1 and
+// M = V passes.
+// Pad: one spare slot after every 16 (phys = i + i/16).  Every access of a pass
+// becomes base(L) + compile-time offset; 6.25% more LDS.
+enum { LAYOUT_XOR = 0, LAYOUT_PAD = 1 };
+
+template<int V, int LAYOUT>
+struct Lds;
+
+template<int V>
+struct Lds<V, LAYOUT_XOR> {
+   static constexpr int LOGV = ilog2c(V);
+   static constexpr int HI   = 5 - LOGV;      // bits folded into [v, 5)
+   static constexpr int size(int n) { return n; }
+   __device__ __forceinline__ static int phys(int i)
+   {
+      return i ^ ((i >> LOGV) & (V - 1)) ^ (((i >> (2 * LOGV)) & ((1 << HI) - 1)) << LOGV);
+   }
+};
+
+template<int V>
+struct Lds<V, LAYOUT_PAD> {
+   static constexpr int size(int n) { return n + n / 16; }
+   __device__ __forceinline__ static int phys(int i) { return i + (i >> 4); }
+};
+
+// ---- pass machinery ---------------------------------------------------------------
+template<class PL, int P>
+__device__ __forceinline__ int tap_pos(int L, int g, int k)
+{
+   constexpr int R = PL::radix(P), M = PL::stride(P), T = PL::T;
+   const int gidx = L + g * T;
+   const int j = gidx & (M - 1), b = gidx / M;
+   return b * R * M + j + k * M;
+}
+
+template<class PL, int P, class LD>
+__device__ __forceinline__ void lds_gather(float2 (&r)[PL::V], const float2* A, int L)
+{
+   constexpr int R = PL::radix(P), G = PL::V / R;
+#pragma unroll
+   for(int g = 0; g < G; g++)
+#pragma unroll
+      for(int k = 0; k < R; k++) r[g + k * G] = A[LD::phys(tap_pos<PL, P>(L, g, k))];
+}
+
+template<class PL, int P, class LD>
+__device__ __forceinline__ void lds_scatter(const float2 (&r)[PL::V], float2* A, int L)
+{
+   constexpr int R = PL::radix(P), G = PL::V / R;
+#pragma unroll
+   for(int g = 0; g < G; g++)
+#pragma unroll
+      for(int k = 0; k < R; k++) A[LD::phys(tap_pos<PL, P>(L, g, k))] = r[g + k * G];
+}
+
+// ---- stage twiddles --------------------------------------------------------------
+// The base twiddle W^j of every group depends only on the lane, so all of them
+// are read once at kernel start and kept in registers: (cos, sin)(2*pi*j/P)
+// serves the forward pass as (c, -s) and the inverse pass as (c, s).  Slot
+// numbering: passes with M > 1 in order, G_p slots each.
+template<class PL>
+struct Twiddles {
+   static constexpr int slots_before(int p)
+   {
+      int n = 0;
+      for(int i = 0; i < p; i++)
+         if(PL::stride(i) > 1) n += PL::V / PL::radix(i);
+      return n;
+   }
+   static constexpr int COUNT = slots_before(PL::NP) > 0 ? slots_before(PL::NP) : 1;
+   float2 w[COUNT];
+
+   __device__ __forceinline__ void load(const float2* __restrict__ tw, int L)
+   {
+      static_for<PL::NP>([&](auto pi) {
+         constexpr int p = decltype(pi)::value;
+         constexpr int R = PL::radix(p), M = PL::stride(p), G = PL::V / R;
+         if constexpr(M > 1) {
+#pragma unroll
+            for(int g = 0; g < G; g++)
+               w[slots_before(p) + g] = tw[R * M + ((L + g * PL::T) & (M - 1))];
+         }
+      });
+   }
+};
+
+// Butterflies + stage twiddles of pass P for all groups of lane L.  Lead
+// passes use the single twiddle chain, radix-16 passes the even/odd chains
+// (fufft.cuh:743-746).
+template<class PL, int P, int SIGN, bool DIT>
+__device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<PL>& tw)
+{
+   constexpr int R = PL::radix(P), M = PL::stride(P), G = PL::V / R;
+   static_for<G>([&](auto gi) {
+      constexpr int g = decltype(gi)::value;
+      if constexpr(M > 1) {
+         const float2 b = tw.w[Twiddles<PL>::slots_before(P) + g];
+         const float2 w1 = SIGN < 0 ? make_float2(b.x, -b.y) : b;
+         if constexpr(DIT) twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
+         dftR<R, SIGN, g, G>(r);
+         if constexpr(!DIT) twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
+      } else {
+         dftR<R, SIGN, g, G>(r);
+      }
+   });
+}
+
+// Forward DIF of the lane's registers: r holds positions L + q*T on entry and
+// the digit-order spectrum positions L*V + k on exit (last pass at M = 1).
+template<class PL, class LD, int LANES>
+__device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
+{
+   static_for<PL::NP>([&](auto pi) {
+      constexpr int p = decltype(pi)::value;
+      if constexpr(p > 0) { pass_barrier<LANES>(); lds_gather<PL, p, LD>(r, A, L); }
+      compute_pass<PL, p, -1, false>(r, tw);
+      if constexpr(p < PL::NP - 1) lds_scatter<PL, p, LD>(r, A, L);
+   });
+}
+
+// Inverse DIT: r holds spectrum positions L*V + k on entry and natural-order
+// positions L + q*T on exit.
+template<class PL, class LD, int LANES>
+__device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
+{
+   static_for<PL::NP>([&](auto qi) {
+      constexpr int p = PL::NP - 1 - decltype(qi)::value;
+      if constexpr(p < PL::NP - 1) lds_gather<PL, p, LD>(r, A, L);
+      compute_pass<PL, p, +1, true>(r, tw);
+      if constexpr(p > 0) { lds_scatter<PL, p, LD>(r, A, L); pass_barrier<LANES>(); }
+   });
+}
+
+// ---- the mid operation at the M = 1 boundary -----------------------------------------
+enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
+// filter layouts: DR = digit order, slot i holds bin mixedrev(i) (what the
+// reference's MidMultiply reads, fufft.cuh:635); LANE = the same values laid
+// out lane-major, lane L's k-th value at L + k*T (the reference's bperm,
+// fufft.cuh:1444-1446), which keeps the read coalesced
+enum { FLT_DR = 0, FLT_LANE = 1 };
+
+// mid and fl are kernel arguments, uniform across the grid, so the branches
+// below are scalar and cost nothing per point; MID_NONE reads no filter.
+template<class PL>
+__device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const float2* __restrict__ f, int L,
+                                       int mid, int fl)
+{
+   if(mid == MID_NONE) return;
+   const int fb = (fl == FLT_DR) ? L * PL::V : L;
+   const int fs = (fl == FLT_DR) ? 1 : PL::T;
+   float2 b[PL::V];
+#pragma unroll
+   for(int k = 0; k < PL::V; k++) b[k] = f[fb + k * fs];
+   if(mid == MID_MUL) {
+#pragma unroll
+      for(int k = 0; k < PL::V; k++) r[k] = cmul(r[k], b[k]);
+   } else {
+#pragma unroll
+      for(int k = 0; k < PL::V; k++) r[k] = cmul_conj(r[k], b[k]);
+   }
+}
+
+}  // namespace fufft

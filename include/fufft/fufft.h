@@ -1,0 +1,178 @@
+/*
+ * fuFFT for MI355X (gfx950) -- C ABI of the fused cyclic-convolution path.
+ *
+ * The reference (weiwang217/FuFFT) has no library: its interface is a set of
+ * CUDA kernel templates launched by its benchmark driver, plus the host-side
+ * planning that driver does.  Each entry point below replaces one of those
+ * launches (or one piece of that planning) and cites it.  Conventions:
+ *
+ *   - Device pointers are caller-owned; nothing here allocates device memory
+ *     on the hot path.  The first call on a device uploads the twiddle table
+ *     (a one-time synchronous copy into static device memory); call
+ *     fufft_init() up front to keep that out of timed or captured regions.
+ *   - Complex data is interleaved fp32 (re, im), 8 bytes per point, 16-byte
+ *     aligned base pointers.
+ *   - stream is a hipStream_t (NULL = the default stream).  Calls are
+ *     asynchronous, stateless and thread-safe across streams.
+ *   - Every function returns FUFFT_OK (0) or a negative status; none exits.
+ *     HIP launch errors are reported as FUFFT_ERR_HIP.
+ *   - Filters are spectra with 1/N already folded in, in the digit order the
+ *     forward DIF leaves behind (see fufft_plan_filter_f32).  filt_stride is 0
+ *     (one filter shared by the batch) or n (one filter per signal).
+ *
+ * Supported sizes (fufft_supported): single-launch N = 2^k with
+ * 256 <= N <= 16384 for FUFFT_V16 and 512 <= N <= 4096 for FUFFT_R8; the
+ * four-step path takes N = 16^L * MID up to 2^20.
+ */
+#ifndef FUFFT_FUFFT_H
+#define FUFFT_FUFFT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status -------------------------------------------------------------- */
+#define FUFFT_OK                0
+#define FUFFT_ERR_INVALID      -1   /* null pointer, bad count, stride or enum */
+#define FUFFT_ERR_UNSUPPORTED  -2   /* size / variant combination not built    */
+#define FUFFT_ERR_HIP          -3   /* HIP runtime error (init, launch)        */
+#define FUFFT_ERR_ALIGN        -4   /* pointer not 16-byte aligned             */
+
+/* ---- enums ----------------------------------------------------------------- */
+/* mid operation between forward and inverse (Mid policies, fufft.cuh:616-650) */
+#define FUFFT_MID_MUL   0   /* A * B        convolution  (MidMultiply)      */
+#define FUFFT_MID_CONJ  1   /* A * conj(B)  correlation  (MidConjMultiply)  */
+#define FUFFT_MID_NONE  2   /* round trip, N * input      (MidNothing)       */
+
+/* lane layout / radix family */
+#define FUFFT_V16  0   /* 16 values per lane, radix 16 (fufft_pipeline_v16)  */
+#define FUFFT_R8   1   /* 8 values per lane, radix 8 (fufft_pipeline_ip)     */
+
+/* filter layouts */
+#define FUFFT_LAYOUT_DR    0  /* slot i holds bin mixedrev(i) (MidMultiply, fufft.cuh:635) */
+#define FUFFT_LAYOUT_LANE  1  /* lane-major: value of slot V*L+k at L+k*(N/V)
+                                 (bperm of fufft_pipeline_v16f, fufft.cuh:1444-1446) */
+
+/* filter_kind for fufft_plan_filter_f32 */
+#define FUFFT_FILTER_SPECTRUM  0  /* input is a natural-order spectrum             */
+#define FUFFT_FILTER_TAPS      1  /* input is time-domain taps; DFT taken in fp64  */
+
+/* ---- library ---------------------------------------------------------------- */
+/* Upload the twiddle table to `device` (idempotent, thread-safe). */
+int fufft_init(int device);
+const char* fufft_status_string(int status);
+/* 1 if a single-launch kernel exists for (n, variant), else 0 */
+int fufft_supported(int64_t n, int variant);
+
+/* ---- host planning (no GPU needed) ------------------------------------------
+ * Pass plan in DIF order: lead radix first, then radix 16 (or 8); returns the
+ * pass count or a negative status.  (cpu_mixed.cpp:36-49, bench_fufft.cu:129-134) */
+int fufft_plan_radices(int64_t n, int variant, int* radices /* >= 32 */);
+/* perm[i] = spectrum bin held by slot i after the forward DIF: bit-group
+ * reversal over the radix widths in pass order.
+ * (mixedrev_host, bench_fufft.cu:63-82; chain_rev, verify_kernel.cpp:460-477) */
+int fufft_digit_order(int64_t n, int variant, int32_t* perm);
+/* Turn a natural-order spectrum or time-domain taps (n complex) into the
+ * filter a conv call reads: fp64 DFT for taps, optional 1/n fold, digit-order
+ * permutation, optional lane-major layout.  Host memory in and out.
+ * (bench_fufft.cu:156-170, verify_kernel.cpp:1381-1387) */
+int fufft_plan_filter_f32(int64_t n, int variant, int layout, int filter_kind,
+                          int fold_inv_n, const float* in, float* out);
+/* The device twiddle table, recomputed on the host: for every P = 2^p,
+ * 1 <= p <= log_max, entries [P, 2P) hold (cos, sin)(2*pi*t/P) rounded to
+ * fp32.  out must hold 2 * 2^(log_max+1) floats. */
+int fufft_twiddle_table_host(int log_max, float* out);
+
+/* ---- fp32 fused convolution ------------------------------------------------
+ * out = IDFT(DFT(in) mid filt) for batch signals of n points, one launch,
+ * three HBM passes.  in == out is allowed.
+ * Replaces fufft_pipeline_v16<N,LEAD,NRV,CPB> (fufft.cuh:1518-1534),
+ * fufft_pipeline_v16f (fufft.cuh:1499-1516) and
+ * fufft_pipeline_ip<N,LEAD,NR8,CPB,Mid> (fufft.cuh:1757-1772), launched by
+ * run_conv (bench_fufft.cu:215-221). */
+int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
+                   void* out, int64_t n, int64_t batch, int mid, int variant,
+                   int layout, void* stream);
+
+/* ---- split path: one signal against many filters ----------------------------
+ * fwd: natural-order signal -> digit-order spectrum (fufft_pipeline_fwd,
+ * fufft.cuh:1343-1370).  apply: spectrum (spec_stride 0 = one spectrum for
+ * the whole batch, n = one per item) mid filt -> inverse -> natural order
+ * (fufft_pipeline_apply, fufft.cuh:1372-1407).  fwd followed by apply is
+ * bit-identical to fufft_conv_f32. */
+int fufft_fwd_f32(const void* in, void* spec, int64_t n, int64_t batch,
+                  int variant, void* stream);
+int fufft_apply_f32(const void* spec, int64_t spec_stride, const void* filt,
+                    int64_t filt_stride, void* out, int64_t n, int64_t batch,
+                    int mid, int variant, int layout, void* stream);
+
+/* ---- two-for-one real convolution --------------------------------------------
+ * u = x (*) h, v = y (*) h for real x, y (fp32, n per signal) and a REAL
+ * time-domain filter h whose spectrum is filt: both ride one complex
+ * transform (fufft_conv_r2, fufft.cuh:1260-1330). */
+int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
+                      int64_t filt_stride, float* u, float* v, int64_t n,
+                      int64_t batch, int variant, int layout, void* stream);
+
+/* ---- int16 block floating point ----------------------------------------------
+ * A point is two int16 (re in the low halfword, im in the high halfword);
+ * every block of FUFFT_BFP_BLOCK consecutive points of a signal shares one
+ * int8 exponent e, value = q * 2^e.  Exponent rule: e = -128 for an all-zero
+ * (or subnormal) block, else the smallest e with absmax <= 32767 * 2^e,
+ * clamped at -128; q = rint(x * 2^-e), so |q| <= 32767.
+ * Replaces fufft_pipeline_v16_bfp (fufft.cuh:1614-1701), whose format is one
+ * fp32 scale per transform and an int16 filter; here the filter is fp32. */
+#define FUFFT_BFP_BLOCK 64
+int fufft_bfp_exponent(float absmax);
+/* host reference codec (bfp_quant_host, bench_fufft.cu:105-117) */
+int fufft_bfp_quantize(const float* x, int64_t npts, int16_t* q, int8_t* e);
+int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float* x);
+int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
+                     int64_t filt_stride, void* qout, int8_t* eout, int64_t n,
+                     int64_t batch, int mid, int layout, void* stream);
+
+/* ---- four-step large N -------------------------------------------------------------
+ * N = 16^lout * mid with mid a single-launch size: lout radix-16 DIF levels
+ * over HBM, the fused conv on contiguous mid-point chunks in place, lout DIT
+ * levels (run_large / MidLaunch, bench_fufft.cu:357-492;
+ * fufft_outer_pass_r, fufft.cuh:1113-1140).  buf is transformed in place.
+ * filt is in the chained digit order (fufft_large_digit_order).
+ * 4*lout + 3 HBM passes. */
+int fufft_large_plan(int64_t n, int* lout, int* mid);
+int fufft_large_digit_order(int64_t n, int32_t* perm);
+int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n,
+                                const float* in, float* out);
+int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
+                         int64_t n, int64_t batch, int mid, void* stream);
+
+/* ---- 2D ---------------------------------------------------------------------------
+ * h x w images, row-major, h and w single-launch sizes.  Rows DIF, columns
+ * DIF, mid, columns DIT, rows DIT (fufft_conv2d, fufft.cuh:1209-1258); the
+ * filter slot (r, c) holds spectrum bin (mixedrev_h(r), mixedrev_w(c)).
+ * Runs as three launches in place on out: row forward, fused column conv,
+ * row inverse (7 HBM passes for an image too large for one workgroup). */
+int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind,
+                            int fold_inv_n, const float* in, float* out);
+int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride,
+                     void* out, int64_t h, int64_t w, int64_t batch, int mid,
+                     void* stream);
+/* Two real images per complex transform with a REAL filter; work is a
+ * caller-owned complex scratch of h*w*batch points (the packed images). */
+int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt,
+                        int64_t filt_stride, float* u, float* v, void* work,
+                        int64_t h, int64_t w, int64_t batch, void* stream);
+/* split 2D path: fwd = rows DIF then columns DIF into spec (2D digit order);
+ * apply = spec mid filt, columns DIT, rows DIT into out.  spec_stride 0 shares
+ * one spectrum across the batch. */
+int fufft_fwd2d_f32(const void* in, void* spec, int64_t h, int64_t w,
+                    int64_t batch, void* stream);
+int fufft_apply2d_f32(const void* spec, int64_t spec_stride, const void* filt,
+                      int64_t filt_stride, void* out, int64_t h, int64_t w,
+                      int64_t batch, int mid, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FUFFT_FUFFT_H */

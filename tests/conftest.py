@@ -1,0 +1,52 @@
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP library)")
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(12345)
+
+
+def gpu_available() -> bool:
+    try:
+        import torch
+        return torch.cuda.is_available()
+    except Exception:
+        return False
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """cuda:0 with the library initialised; skips when no GPU is visible."""
+    if not gpu_available():
+        pytest.skip("no GPU visible")
+    import torch
+    import fufft_amd as ff
+    ff.init(0)
+    return torch.device("cuda:0")
+
+
+def crandn(rng, shape, scale=1.0):
+    return ((rng.standard_normal(shape) + 1j * rng.standard_normal(shape)) * scale).astype(np.complex64)
+
+
+def cuniform(rng, shape, lo=-1.0, hi=1.0):
+    return (rng.uniform(lo, hi, shape) + 1j * rng.uniform(lo, hi, shape)).astype(np.complex64)
+
+
+def bits_equal(a, b) -> bool:
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))

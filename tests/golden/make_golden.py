@@ -1,0 +1,88 @@
+"""Write the golden fixtures from the reference's compiled CPU transcription.
+
+Run in the build container, where /root/reference exists and `make -C oracle
+ref` has built oracle/_ref/libfufft_ref.so:
+
+    python -m tests.golden.make_golden
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import oracle as O
+from tests.golden.golden import HERE
+
+
+def _cu(rng, shape):
+    return (rng.uniform(-1, 1, shape) + 1j * rng.uniform(-1, 1, shape)).astype(np.complex64)
+
+
+def _lead_count(n, v):
+    rads = O.factor(n, v)
+    return (rads[0] if rads[0] != v else 1), rads.count(v)
+
+
+def main() -> None:
+    R = O.load_ref()
+    if R is None:
+        raise SystemExit("oracle/_ref/libfufft_ref.so is not built (needs /root/reference)")
+    rng = np.random.default_rng(20261201)
+
+    def save(name, **kw):
+        np.savez_compressed(HERE / f"{name}.npz", **kw)
+
+    for n in (64, 512, 1024):
+        batch = 2
+        a, b = _cu(rng, (batch, n)), _cu(rng, (batch, n)) / n
+        bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 16))])
+        lead, nrv = _lead_count(n, 16)
+        out = np.empty_like(a)
+        R.ref_vk_pipeline_v16(n, lead, nrv, 1, a.ctypes.data, bdr.ctypes.data, out.ctypes.data, batch)
+        save(f"v16_n{n}", kind="v16", n=n, a=a, bdr=bdr, out=out.reshape(-1))
+
+    for n in (512, 4096):
+        batch = 1
+        a, b = _cu(rng, (batch, n)), _cu(rng, (batch, n)) / n
+        bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 8))])
+        lead, nr8 = _lead_count(n, 8)
+        out = np.empty_like(a)
+        R.ref_vk_pipeline_ip(n, lead, nr8, 1, a.ctypes.data, bdr.ctypes.data, out.ctypes.data, batch)
+        save(f"r8_n{n}", kind="r8", n=n, a=a, bdr=bdr, out=out.reshape(-1))
+
+    n, batch = 512, 2
+    a, b = _cu(rng, (batch, n)), _cu(rng, (batch, n)) / n
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 8))])
+    lead, nr8 = _lead_count(n, 8)
+    spec, out = np.empty_like(a), np.empty_like(a)
+    R.ref_vk_pipeline_fwd(n, lead, nr8, 1, a.ctypes.data, spec.ctypes.data, batch)
+    R.ref_vk_pipeline_apply(n, lead, nr8, 1, spec.ctypes.data, bdr.ctypes.data, out.ctypes.data, batch)
+    save("split_n512", kind="split", n=n, a=a, bdr=bdr, spec=spec.reshape(-1), out=out.reshape(-1))
+
+    h, w = 64, 64
+    a, b = _cu(rng, (1, h, w)), _cu(rng, (1, h, w)) / (h * w)
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(h, 8))][:, :, O.mixedrev(O.kernel_plan(w, 8))])
+    out = np.empty_like(a)
+    R.ref_vk_conv2d(h, w, a.ctypes.data, bdr.ctypes.data, out.ctypes.data, 1)
+    save("conv2d_64x64", kind="conv2d", h=h, w=w, a=a, bdr=bdr, out=out.reshape(-1))
+
+    n, batch = 256, 2
+    x = rng.uniform(-1, 1, (batch, n)).astype(np.float32)
+    y = rng.uniform(-1, 1, (batch, n)).astype(np.float32)
+    b = _cu(rng, (batch, n)) / n
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 8))])
+    lead, nr8 = _lead_count(n, 8)
+    u, v = np.empty_like(x), np.empty_like(y)
+    R.ref_vk_conv_r2(n, lead, nr8, 1, x.ctypes.data, y.ctypes.data, bdr.ctypes.data,
+                     u.ctypes.data, v.ctypes.data, batch)
+    save("r2_n256", kind="r2", n=n, x=x, y=y, bdr=bdr, u=u.reshape(-1), v=v.reshape(-1))
+
+    n, mid = 4096, 256
+    a, b = _cu(rng, (1, n)), _cu(rng, (1, n)) / n
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.large_plan(1, mid))])
+    A = a.copy()
+    R.ref_vk_conv_foursteps_cfg(A.ctypes.data, bdr.ctypes.data, n, 1, 16, mid, 1)
+    save("fourstep_n4096_mid256", kind="fourstep", n=n, lout=1, mid=mid, a=a, bdr=bdr, out=A.reshape(-1))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,185 @@
+"""GPU parity of the 1D fused path (fufft_conv_f32 / fwd / apply / conv_r2).
+
+Bar: bit-identical to the oracle in table-twiddle mode (same operation order,
+same twiddle table, -ffp-contract=off on both sides), and rel L2 <= 2e-6
+against fp64 (the north_star bound for fp32).
+"""
+import numpy as np
+import pytest
+
+from conftest import bits_equal, crandn, cuniform
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 2e-6
+V = {"v16": 16, "r8": 8}
+SIZES = [("v16", n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + \
+        [("r8", n) for n in (512, 1024, 2048, 4096)]
+
+
+def to_dev(x, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def from_dev(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def run_conv(dev, a, filt, n, filt_stride, mid, variant, layout, inplace=False):
+    import torch
+    import fufft_amd as ff
+    da = to_dev(a, dev)
+    df = to_dev(filt, dev)
+    dout = da if inplace else torch.empty_like(da)
+    ff.conv(da, df, dout, n=n, batch=a.size // n, filt_stride=filt_stride, mid=mid,
+            variant=variant, layout=layout)
+    return from_dev(dout).reshape(-1)
+
+
+def lane_major(fdr, n, v):
+    """filter slot v*L + k moved to L + k*T (the reference's bperm)"""
+    t = n // v
+    return np.ascontiguousarray(fdr.reshape(-1, t, v).transpose(0, 2, 1)).reshape(-1)
+
+
+@pytest.mark.parametrize("variant,n", SIZES)
+@pytest.mark.parametrize("mid", ["mul", "conj", "none"])
+def test_conv_matches_oracle_bitwise(dev, variant, n, mid, rng):
+    batch = max(4, 65536 // n)
+    a = crandn(rng, (batch, n))
+    spec = crandn(rng, n) / n
+    plan = O.kernel_plan(n, V[variant])
+    fdr = spec[O.mixedrev(plan)]
+    print(f"case conv variant={variant} n={n} mid={mid} batch={batch}", flush=True)
+    got = run_conv(dev, a, fdr, n, 0, mid, variant, "dr")
+    want = O.conv(a, fdr, n, plan, filt_stride=0, mid=mid)
+    assert bits_equal(got, want)
+    truth = O.conv_spec_f64(a[:8], spec, n, mid=mid)
+    assert O.rel_l2(got[:8 * n], truth) <= TOL_F32
+
+
+@pytest.mark.parametrize("variant,n", [("v16", 512), ("v16", 4096), ("r8", 1024)])
+def test_per_signal_filter_and_lane_layout(dev, variant, n, rng):
+    batch = 64
+    v = V[variant]
+    a = cuniform(rng, (batch, n))
+    spec = cuniform(rng, (batch, n)) / n
+    plan = O.kernel_plan(n, v)
+    fdr = np.ascontiguousarray(spec[:, O.mixedrev(plan)]).reshape(-1)
+    want = O.conv(a, fdr, n, plan, filt_stride=n)
+    print(f"case per-signal variant={variant} n={n}", flush=True)
+    assert bits_equal(run_conv(dev, a, fdr, n, n, "mul", variant, "dr"), want)
+    assert bits_equal(run_conv(dev, a, lane_major(fdr, n, v), n, n, "mul", variant, "lane"), want)
+
+
+@pytest.mark.parametrize("n", [1024, 4096])
+def test_in_place(dev, n, rng):
+    a = crandn(rng, (32, n))
+    spec = crandn(rng, n) / n
+    plan = O.kernel_plan(n, 16)
+    fdr = spec[O.mixedrev(plan)]
+    print(f"case in-place n={n}", flush=True)
+    assert bits_equal(run_conv(dev, a, fdr, n, 0, "mul", "v16", "dr", inplace=True),
+                      O.conv(a, fdr, n, plan))
+
+
+@pytest.mark.parametrize("variant,n", [("v16", 512), ("v16", 2048), ("r8", 512), ("r8", 4096)])
+def test_split_fwd_apply_bit_identical_to_fused(dev, variant, n, rng):
+    import torch
+    import fufft_amd as ff
+    batch = 16
+    a = crandn(rng, (batch, n))
+    spec = crandn(rng, (batch, n)) / n
+    plan = O.kernel_plan(n, V[variant])
+    fdr = np.ascontiguousarray(spec[:, O.mixedrev(plan)]).reshape(-1)
+    print(f"case split variant={variant} n={n}", flush=True)
+    da, df = to_dev(a, dev), to_dev(fdr, dev)
+    dspec, dout = torch.empty_like(da), torch.empty_like(da)
+    ff.fwd(da, dspec, n=n, batch=batch, variant=variant)
+    ff.apply(dspec, df, dout, n=n, batch=batch, spec_stride=n, filt_stride=n, variant=variant)
+    assert bits_equal(from_dev(dspec).reshape(-1), O.fwd(a, n, plan))
+    fused = run_conv(dev, a, fdr, n, n, "mul", variant, "dr")
+    assert bits_equal(from_dev(dout).reshape(-1), fused)
+
+
+def test_split_broadcast_one_spectrum_many_filters(dev, rng):
+    """one signal forward once, then applied against 256 filters"""
+    import torch
+    import fufft_amd as ff
+    n, nf = 4096, 256
+    a = crandn(rng, (1, n))
+    filters = crandn(rng, (nf, n)) / n
+    plan = O.kernel_plan(n, 16)
+    fdr = np.ascontiguousarray(filters[:, O.mixedrev(plan)]).reshape(-1)
+    print("case split broadcast", flush=True)
+    da, df = to_dev(a, dev), to_dev(fdr, dev)
+    dspec = torch.empty_like(da)
+    dout = torch.empty((nf * n,), dtype=torch.complex64, device=dev)
+    ff.fwd(da, dspec, n=n, batch=1)
+    ff.apply(dspec, df, dout, n=n, batch=nf, spec_stride=0, filt_stride=n)
+    got = from_dev(dout)
+    spec1 = O.fwd(a, n, plan)
+    assert bits_equal(got, O.apply(spec1, fdr, n, nf, plan, spec_stride=0, filt_stride=n))
+    truth = O.conv_spec_f64(np.repeat(a, 4, axis=0), filters[:4], n, spec_stride=n)
+    assert O.rel_l2(got[:4 * n], truth) <= TOL_F32
+
+
+@pytest.mark.parametrize("variant,n", [("v16", 512), ("r8", 512), ("v16", 4096)])
+def test_conv_r2_two_real_signals(dev, variant, n, rng):
+    import torch
+    import fufft_amd as ff
+    batch = 32
+    x = rng.uniform(0, 1, (batch, n)).astype(np.float32)
+    y = rng.uniform(0, 1, (batch, n)).astype(np.float32)
+    h = rng.uniform(0, 1, n)
+    spec = (np.fft.fft(h) / n).astype(np.complex64)           # spectrum of a REAL filter
+    plan = O.kernel_plan(n, V[variant])
+    fdr = spec[O.mixedrev(plan)]
+    print(f"case r2 variant={variant} n={n}", flush=True)
+    dx, dy, df = to_dev(x, dev), to_dev(y, dev), to_dev(fdr, dev)
+    du, dv = torch.empty_like(dx), torch.empty_like(dy)
+    ff.conv_r2(dx, dy, df, du, dv, n=n, batch=batch, variant=variant)
+    u, v = from_dev(du).reshape(-1), from_dev(dv).reshape(-1)
+    ou, ov = O.conv_r2(x, y, fdr, n, plan)
+    assert bits_equal(u, ou) and bits_equal(v, ov)
+    # packed-real equals the complex kernel on x + iy
+    z = run_conv(dev, (x + 1j * y).astype(np.complex64), fdr, n, 0, "mul", variant, "dr")
+    assert bits_equal(u, z.real.copy()) and bits_equal(v, z.imag.copy())
+    truth = np.real(np.fft.ifft(np.fft.fft(x[:2].astype(np.float64), axis=1) * np.fft.fft(h)[None], axis=1))
+    assert O.rel_l2(u[:2 * n], truth.reshape(-1)) <= TOL_F32
+
+
+def test_full_size_properties(dev, rng):
+    """The bench workload size (2^27 points): every signal is checked through
+    linearity against an oracle sample and a checksum of the round trip."""
+    import torch
+    import fufft_amd as ff
+    n, batch = 4096, (1 << 27) // 4096
+    torch.manual_seed(7)
+    da = torch.randn(batch * n, dtype=torch.complex64, device=dev)
+    spec = crandn(rng, n) / n
+    plan = O.kernel_plan(n, 16)
+    df = to_dev(spec[O.mixedrev(plan)], dev)
+    dout = torch.empty_like(da)
+    print("case full-size n=4096 batch=32768", flush=True)
+    ff.conv(da, df, dout, n=n, batch=batch)
+    # sample 64 signals spread over the batch: bit-identical to the oracle
+    idx = np.linspace(0, batch - 1, 64).astype(np.int64)
+    a_s = da.view(batch, n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
+    got_s = dout.view(batch, n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
+    assert bits_equal(got_s.reshape(-1), O.conv(a_s, spec[O.mixedrev(plan)], n, plan))
+    # round trip with no mid operation returns N * input for every signal
+    ff.conv(da, df, dout, n=n, batch=batch, mid="none")
+    err = torch.linalg.vector_norm(dout / n - da) / torch.linalg.vector_norm(da)
+    assert float(err) < 1e-6
+
+
+def test_empty_batch_is_noop(dev):
+    import torch
+    import fufft_amd as ff
+    d = torch.zeros(4096, dtype=torch.complex64, device=dev)
+    ff.conv(d, d, d, n=4096, batch=0)
