@@ -23,7 +23,7 @@ namespace fufft {
 
 constexpr int cpb_for(int T) { return T >= 128 ? 1 : 256 / T; }
 
-template<int N, int V, int LAYOUT, int KIND>
+template<int N, int V, int LAYOUT, int KIND, int MID>
 __global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
 conv1d_kernel(const Conv1dParams p)
 {
@@ -33,6 +33,8 @@ conv1d_kernel(const Conv1dParams p)
    constexpr int CPB   = cpb_for(T);
    constexpr int SLOT  = LD::size(N);
    constexpr int LANES = T < 64 ? 64 : T;
+   constexpr int TPW   = T < 64 ? 64 / T : 1;     // transforms per wavefront
+   constexpr int EL    = (KIND == K_CONV_R2) ? 4 : 8;   // bytes per point in HBM
 
    extern __shared__ float2 lds[];
    const int slot = threadIdx.x / T;
@@ -40,65 +42,76 @@ conv1d_kernel(const Conv1dParams p)
    const uint32_t t = blockIdx.x * CPB + slot;
    if(t >= p.ntrans) return;                 // T > 64 => CPB == 1: whole group leaves
 
+   // the wavefront's first transform (uniform) and this lane's offset from it
+   const uint32_t t0 = (T >= 64) ? (uint32_t)uniform((int)t)
+                                 : blockIdx.x * CPB + (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
+   const uint32_t lane_off = ((t - t0) * N + L) * EL;
+   const size_t   wbase    = (size_t)t0 * N * EL;
+   constexpr uint32_t WBYTES = TPW * N * EL;
+
    float2* A = lds + slot * SLOT;
-   const size_t base = (size_t)t * N;
    Twiddles<PL> tw;
    tw.load(p.tw, L);
    float2 r[V];
 
    if constexpr(KIND == K_APPLY) {
       // spectrum positions L*V .. L*V+V-1, two complex per 16-byte load
-      const float4* s = reinterpret_cast<const float4*>(
-         static_cast<const float2*>(p.spec) + (size_t)(t % p.scount) * N + L * V);
+      const Buf sb(p.spec, p.scount * (uint32_t)N * 8u);
+      const uint32_t so = ((t % p.scount) * N + L * V) * 8u;
 #pragma unroll
       for(int m = 0; m < V / 2; m++) {
-         const float4 q = s[m];
+         const float4 q = sb.ld4(so, m * 16);
          r[2 * m] = make_float2(q.x, q.y);
          r[2 * m + 1] = make_float2(q.z, q.w);
       }
    } else {
       if constexpr(KIND == K_CONV_R2) {
-         const float* x = static_cast<const float*>(p.in0) + base;
-         const float* y = static_cast<const float*>(p.in1) + base;
+         const Buf xb(static_cast<const char*>(p.in0) + wbase, WBYTES);
+         const Buf yb(static_cast<const char*>(p.in1) + wbase, WBYTES);
 #pragma unroll
-         for(int q = 0; q < V; q++) r[q] = make_float2(x[L + q * T], y[L + q * T]);
+         for(int q = 0; q < V; q++) r[q] = make_float2(xb.ld1(lane_off, q * T * 4), yb.ld1(lane_off, q * T * 4));
       } else {
-         const float2* x = static_cast<const float2*>(p.in0) + base;
+         const Buf xb(static_cast<const char*>(p.in0) + wbase, WBYTES);
 #pragma unroll
-         for(int q = 0; q < V; q++) r[q] = x[L + q * T];
+         for(int q = 0; q < V; q++) r[q] = xb.ld2(lane_off, q * T * 8);
       }
       forward_dif<PL, LD, LANES>(r, A, L, tw);
    }
 
    if constexpr(KIND == K_FWD) {
-      float4* s = reinterpret_cast<float4*>(static_cast<float2*>(p.out0) + base + L * V);
+      const Buf ob(static_cast<char*>(p.out0) + wbase, WBYTES);
+      const uint32_t so = ((t - t0) * N + L * V) * 8u;
 #pragma unroll
       for(int m = 0; m < V / 2; m++)
-         s[m] = make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y);
+         ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * 16);
       return;
    } else {
-      mid_op<PL>(r, static_cast<const float2*>(p.filt) + (size_t)(t % p.fcount) * N, L, p.mid, p.fl);
+      {
+         const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
+         const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
+         mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
+      }
       inverse_dit<PL, LD, LANES>(r, A, L, tw);
 
       if constexpr(KIND == K_CONV_R2) {
-         float* u = static_cast<float*>(p.out0) + base;
-         float* v = static_cast<float*>(p.out1) + base;
+         const Buf ub(static_cast<char*>(p.out0) + wbase, WBYTES);
+         const Buf vb(static_cast<char*>(p.out1) + wbase, WBYTES);
 #pragma unroll
-         for(int q = 0; q < V; q++) { u[L + q * T] = r[q].x; v[L + q * T] = r[q].y; }
+         for(int q = 0; q < V; q++) { ub.st1(r[q].x, lane_off, q * T * 4); vb.st1(r[q].y, lane_off, q * T * 4); }
       } else {
-         float2* o = static_cast<float2*>(p.out0) + base;
+         const Buf ob(static_cast<char*>(p.out0) + wbase, WBYTES);
 #pragma unroll
-         for(int q = 0; q < V; q++) o[L + q * T] = r[q];
+         for(int q = 0; q < V; q++) ob.st2(r[q], lane_off, q * T * 8);
       }
    }
 }
 
-template<int N, int V, int LAYOUT, int KIND>
+template<int N, int V, int LAYOUT, int KIND, int MID>
 static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
 {
    constexpr int T = N / V, CPB = cpb_for(T);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
-   const void* k = reinterpret_cast<const void*>(&conv1d_kernel<N, V, LAYOUT, KIND>);
+   const void* k = reinterpret_cast<const void*>(&conv1d_kernel<N, V, LAYOUT, KIND, MID>);
    if(shm > 65536) {
       const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
       if(e != hipSuccess) return e;
@@ -109,14 +122,25 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
    return hipLaunchKernel(k, grid, block, argv, shm, s);
 }
 
+template<int N, int V, int LAYOUT, int KIND>
+static hipError_t launch_mid(const Conv1dParams& p, hipStream_t s)
+{
+   switch(p.mid) {
+      case MID_MUL:  return launch_one<N, V, LAYOUT, KIND, MID_MUL>(p, s);
+      case MID_CONJ: return launch_one<N, V, LAYOUT, KIND, MID_CONJ>(p, s);
+      case MID_NONE: return launch_one<N, V, LAYOUT, KIND, MID_NONE>(p, s);
+      default:       return hipErrorInvalidValue;
+   }
+}
+
 template<int N, int V, int LAYOUT>
 static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
 {
    switch(kind) {
-      case K_CONV:    return launch_one<N, V, LAYOUT, K_CONV>(p, s);
-      case K_CONV_R2: return launch_one<N, V, LAYOUT, K_CONV_R2>(p, s);
-      case K_FWD:     return launch_one<N, V, LAYOUT, K_FWD>(p, s);
-      case K_APPLY:   return launch_one<N, V, LAYOUT, K_APPLY>(p, s);
+      case K_CONV:    return launch_mid<N, V, LAYOUT, K_CONV>(p, s);
+      case K_CONV_R2: return launch_one<N, V, LAYOUT, K_CONV_R2, MID_MUL>(p, s);
+      case K_FWD:     return launch_one<N, V, LAYOUT, K_FWD, MID_NONE>(p, s);
+      case K_APPLY:   return launch_mid<N, V, LAYOUT, K_APPLY>(p, s);
       default:        return hipErrorInvalidValue;
    }
 }

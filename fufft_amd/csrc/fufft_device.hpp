@@ -176,6 +176,7 @@ __device__ __forceinline__ void dftR(float2 (&r)[NR])
 #define FUFFT_TW_LOG_MAX 20
 #define FUFFT_TW_ENTRIES (2u << FUFFT_TW_LOG_MAX)
 
+
 template<int SIGN>
 __device__ __forceinline__ float2 tw_load(const float2* __restrict__ tw, int idx)
 {
@@ -220,6 +221,58 @@ __device__ __forceinline__ void twiddle_group(float2 (&r)[NR], float2 w1)
    if constexpr(R == 16 && CHAIN == CHAIN_EVENODD) tw_evenodd<OFF, STRIDE>(r, w1);
    else                                             tw_single<R, OFF, STRIDE>(r, w1);
 }
+
+// ---- buffer-resource memory access ---------------------------------------------------
+// Global traffic goes through raw buffer instructions: the base address lives in
+// a wave-uniform 128-bit resource (SGPRs), each lane supplies one 32-bit byte
+// offset, and per-tap offsets ride in the scalar offset field, so a lane keeps
+// one VGPR of addressing instead of a 64-bit pointer per tap.  Accesses beyond
+// num_records bytes read zero and drop writes.
+struct Buf {
+   __amdgpu_buffer_rsrc_t r;
+   // dword 3 of the resource: 32-bit data format, as gfx9 untyped access expects
+   static constexpr int kFlags = 0x00020000;
+
+   __device__ __forceinline__ Buf(const void* base, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kFlags)) {}
+
+   __device__ __forceinline__ float ld1(uint32_t voff, uint32_t soff) const
+   {
+      return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+   }
+   __device__ __forceinline__ float2 ld2(uint32_t voff, uint32_t soff) const
+   {
+      return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+   }
+   __device__ __forceinline__ float4 ld4(uint32_t voff, uint32_t soff) const
+   {
+      return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+   }
+   __device__ __forceinline__ uint32_t ldu(uint32_t voff, uint32_t soff) const
+   {
+      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+   }
+   __device__ __forceinline__ void st1(float v, uint32_t voff, uint32_t soff) const
+   {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
+   }
+   __device__ __forceinline__ void st2(float2 v, uint32_t voff, uint32_t soff) const
+   {
+      typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), r, voff, soff, 0);
+   }
+   __device__ __forceinline__ void st4(float4 v, uint32_t voff, uint32_t soff) const
+   {
+      typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, voff, soff, 0);
+   }
+   __device__ __forceinline__ void stu(uint32_t v, uint32_t voff, uint32_t soff) const
+   {
+      __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, 0);
+   }
+};
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // ---- synchronisation between passes -------------------------------------------
 // A transform held by one wavefront needs no s_barrier: LDS operations of a

@@ -123,10 +123,15 @@ __device__ __forceinline__ void lds_scatter(const float2 (&r)[PL::V], float2* A,
 }
 
 // ---- stage twiddles --------------------------------------------------------------
-// The base twiddle W^j of every group depends only on the lane, so all of them
-// are read once at kernel start and kept in registers: (cos, sin)(2*pi*j/P)
-// serves the forward pass as (c, -s) and the inverse pass as (c, s).  Slot
-// numbering: passes with M > 1 in order, G_p slots each.
+// Every group keeps one base twiddle W^j and generates the rest by the
+// reference's recurrences: the even/odd chains for radix 16, the single chain
+// for radix 2/4/8 (fufft.cuh:436-450, 701-720, 743-746).  (Reading all stage
+// twiddles from a table instead costs more: each lane's row lands in its own
+// cache line, and the vector-memory path, not the VALU, becomes the limit.)
+// Base twiddles depend only on the lane, so all of them are read once at
+// kernel start: (cos, sin)(2*pi*j/P) serves the forward pass as (c, -s) and
+// the inverse pass as (c, s).  Slot numbering: passes with M > 1 in order,
+// G_p slots each.
 template<class PL>
 struct Twiddles {
    static constexpr int slots_before(int p)
@@ -139,23 +144,22 @@ struct Twiddles {
    static constexpr int COUNT = slots_before(PL::NP) > 0 ? slots_before(PL::NP) : 1;
    float2 w[COUNT];
 
-   __device__ __forceinline__ void load(const float2* __restrict__ tw, int L)
+   __device__ __forceinline__ void load(const float2* table, int L)
    {
+      const Buf tb(table, FUFFT_TW_ENTRIES * 8u);
       static_for<PL::NP>([&](auto pi) {
          constexpr int p = decltype(pi)::value;
          constexpr int R = PL::radix(p), M = PL::stride(p), G = PL::V / R;
          if constexpr(M > 1) {
 #pragma unroll
             for(int g = 0; g < G; g++)
-               w[slots_before(p) + g] = tw[R * M + ((L + g * PL::T) & (M - 1))];
+               w[slots_before(p) + g] = tb.ld2((uint32_t)(((L + g * PL::T) & (M - 1)) * 8), R * M * 8);
          }
       });
    }
 };
 
-// Butterflies + stage twiddles of pass P for all groups of lane L.  Lead
-// passes use the single twiddle chain, radix-16 passes the even/odd chains
-// (fufft.cuh:743-746).
+// Butterflies + stage twiddles of pass P for all groups of the lane.
 template<class PL, int P, int SIGN, bool DIT>
 __device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<PL>& tw)
 {
@@ -208,24 +212,18 @@ enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
 // fufft.cuh:1444-1446), which keeps the read coalesced
 enum { FLT_DR = 0, FLT_LANE = 1 };
 
-// mid and fl are kernel arguments, uniform across the grid, so the branches
-// below are scalar and cost nothing per point; MID_NONE reads no filter.
-template<class PL>
-__device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const float2* __restrict__ f, int L,
-                                       int mid, int fl)
+// The lane's V filter values sit at byte offsets voff + k*kstep of the filter
+// buffer.  MID is a template parameter: a runtime branch between the two
+// products makes the compiler keep both results live across the join.
+template<class PL, int MID>
+__device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t kstep)
 {
-   if(mid == MID_NONE) return;
-   const int fb = (fl == FLT_DR) ? L * PL::V : L;
-   const int fs = (fl == FLT_DR) ? 1 : PL::T;
-   float2 b[PL::V];
+   if constexpr(MID != MID_NONE) {
 #pragma unroll
-   for(int k = 0; k < PL::V; k++) b[k] = f[fb + k * fs];
-   if(mid == MID_MUL) {
-#pragma unroll
-      for(int k = 0; k < PL::V; k++) r[k] = cmul(r[k], b[k]);
-   } else {
-#pragma unroll
-      for(int k = 0; k < PL::V; k++) r[k] = cmul_conj(r[k], b[k]);
+      for(int k = 0; k < PL::V; k++) {
+         const float2 b = f.ld2(voff, k * kstep);
+         r[k] = (MID == MID_MUL) ? cmul(r[k], b) : cmul_conj(r[k], b);
+      }
    }
 }
 

@@ -113,16 +113,24 @@ def factor(n: int, v: int) -> list[int]:
     return list(buf[:k])
 
 
-def kernel_plan(n: int, v: int) -> Plan:
-    """The plan of a single-launch kernel: lead radix (single chain), then radix
-    v passes -- radix 16 with the even/odd chains, radix 8 single chain."""
+def ref_plan(n: int, v: int) -> Plan:
+    """The reference kernels' plan: lead radix with the single twiddle chain,
+    then radix-v passes -- radix 16 with the even/odd chains (fufft.cuh:743-746),
+    radix 8 with the single chain."""
     rads = factor(n, v)
     return Plan(rads, [CHAIN_EVENODD if r == 16 else CHAIN_SINGLE for r in rads])
 
 
-def large_plan(lout: int, mid_n: int, mid_v: int = 16) -> Plan:
+def kernel_plan(n: int, v: int) -> Plan:
+    """This build's single-launch kernel plan: the reference's chains (even/odd
+    for radix 16, single otherwise); only the base twiddle source differs, and
+    that is selected by the `tw` argument of the transforms."""
+    return ref_plan(n, v)
+
+
+def large_plan(lout: int, mid_n: int, mid_v: int = 16, ref: bool = False) -> Plan:
     """Four-step chain: lout radix-16 outer levels (single chain) + the middle."""
-    m = kernel_plan(mid_n, mid_v)
+    m = ref_plan(mid_n, mid_v) if ref else kernel_plan(mid_n, mid_v)
     return Plan([16] * lout + m.radices, [CHAIN_SINGLE] * lout + m.chains)
 
 

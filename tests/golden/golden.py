@@ -27,25 +27,25 @@ def replay(case: dict) -> dict:
     kind = str(case["kind"])
     if kind == "v16":
         n = int(case["n"])
-        return {"out": O.conv(case["a"], case["bdr"], n, O.kernel_plan(n, 16), filt_stride=n, tw=O.TW_LIBM)}
+        return {"out": O.conv(case["a"], case["bdr"], n, O.ref_plan(n, 16), filt_stride=n, tw=O.TW_LIBM)}
     if kind == "r8":
         n = int(case["n"])
-        return {"out": O.conv(case["a"], case["bdr"], n, O.kernel_plan(n, 8), filt_stride=n, tw=O.TW_LIBM)}
+        return {"out": O.conv(case["a"], case["bdr"], n, O.ref_plan(n, 8), filt_stride=n, tw=O.TW_LIBM)}
     if kind == "split":
         n = int(case["n"])
-        plan = O.kernel_plan(n, 8)
+        plan = O.ref_plan(n, 8)
         spec = O.fwd(case["a"], n, plan, tw=O.TW_LIBM)
         out = O.apply(spec, case["bdr"], n, spec.size // n, plan, spec_stride=n, filt_stride=n, tw=O.TW_LIBM)
         return {"spec": spec, "out": out}
     if kind == "conv2d":
         h, w = int(case["h"]), int(case["w"])
-        return {"out": O.conv2d(case["a"], case["bdr"], h, w, O.kernel_plan(h, 8), O.kernel_plan(w, 8),
+        return {"out": O.conv2d(case["a"], case["bdr"], h, w, O.ref_plan(h, 8), O.ref_plan(w, 8),
                                 filt_stride=h * w, tw=O.TW_LIBM)}
     if kind == "r2":
         n = int(case["n"])
-        u, v = O.conv_r2(case["x"], case["y"], case["bdr"], n, O.kernel_plan(n, 8), filt_stride=n, tw=O.TW_LIBM)
+        u, v = O.conv_r2(case["x"], case["y"], case["bdr"], n, O.ref_plan(n, 8), filt_stride=n, tw=O.TW_LIBM)
         return {"u": u, "v": v}
     if kind == "fourstep":
         n, lout, mid = int(case["n"]), int(case["lout"]), int(case["mid"])
-        return {"out": O.conv(case["a"], case["bdr"], n, O.large_plan(lout, mid), filt_stride=n, tw=O.TW_LIBM)}
+        return {"out": O.conv(case["a"], case["bdr"], n, O.large_plan(lout, mid, ref=True), filt_stride=n, tw=O.TW_LIBM)}
     raise ValueError(kind)

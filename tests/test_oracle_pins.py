@@ -35,7 +35,7 @@ def test_v16_libm_matches_reference_bitwise(n, cpb, rng):
     batch = 4
     a = cuniform(rng, (batch, n))
     b = cuniform(rng, (batch, n)) / n
-    plan = O.kernel_plan(n, 16)
+    plan = O.ref_plan(n, 16)
     bdr = np.ascontiguousarray(b[:, O.mixedrev(plan)])
     lead, nrv = lead_and_count(n, 16)
     ref = np.empty_like(a)
@@ -50,7 +50,7 @@ def test_r8_libm_matches_reference_bitwise(n, rng):
     batch = 3
     a = cuniform(rng, (batch, n))
     b = cuniform(rng, (batch, n)) / n
-    plan = O.kernel_plan(n, 8)
+    plan = O.ref_plan(n, 8)
     bdr = np.ascontiguousarray(b[:, O.mixedrev(plan)])
     lead, nr8 = lead_and_count(n, 8)
     ref = np.empty_like(a)
@@ -65,7 +65,7 @@ def test_split_libm_matches_reference_bitwise(n, rng):
     batch = 3
     a = cuniform(rng, (batch, n))
     b = cuniform(rng, (batch, n)) / n
-    plan = O.kernel_plan(n, 8)
+    plan = O.ref_plan(n, 8)
     bdr = np.ascontiguousarray(b[:, O.mixedrev(plan)])
     lead, nr8 = lead_and_count(n, 8)
     spec = np.empty_like(a)
@@ -90,7 +90,7 @@ def test_fourstep_libm_matches_reference_bitwise(n, mid, rng):
         m //= 16
         lout += 1
     assert m == mid
-    plan = O.large_plan(lout, mid)
+    plan = O.large_plan(lout, mid, ref=True)
     bdr = np.ascontiguousarray(b[:, O.mixedrev(plan)])
     # the reference derives the chained order with its own chain_rev
     rads = (O.C.c_int * len(plan.radices))(*plan.radices)
@@ -108,7 +108,7 @@ def test_conv2d_libm_matches_reference_bitwise(h, w, rng):
     batch = 2
     a = cuniform(rng, (batch, h, w))
     b = cuniform(rng, (batch, h, w)) / (h * w)
-    ph, pw = O.kernel_plan(h, 8), O.kernel_plan(w, 8)
+    ph, pw = O.ref_plan(h, 8), O.ref_plan(w, 8)
     bdr = np.ascontiguousarray(b[:, O.mixedrev(ph)][:, :, O.mixedrev(pw)])
     ref = np.empty_like(a)
     REF.ref_vk_conv2d(h, w, a.ctypes.data, bdr.ctypes.data, ref.ctypes.data, batch)
@@ -123,7 +123,7 @@ def test_conv_r2_libm_matches_reference_bitwise(n, rng):
     x = rng.uniform(-1, 1, (batch, n)).astype(np.float32)
     y = rng.uniform(-1, 1, (batch, n)).astype(np.float32)
     b = cuniform(rng, (batch, n)) / n
-    plan = O.kernel_plan(n, 8)
+    plan = O.ref_plan(n, 8)
     bdr = np.ascontiguousarray(b[:, O.mixedrev(plan)])
     lead, nr8 = lead_and_count(n, 8)
     u = np.empty_like(x)
