@@ -3,8 +3,10 @@
 
 A "step" is one launch of the fused convolution over one batch of 2^27
 points held in HBM: N = 4096, batch 32768, one shared filter (BASELINE.json
-metric and configs[1]; the other configs are parity-test cases).  Prints ONE
-JSON line.
+metric, configs[1]).  The metric names fp32 AND int16-BFP, so the same JSON
+line carries the fp32 figure as `value` and the int16-BFP figure for the same
+N and batch under "bfp", plus a short fp32 sweep over the other
+configs[1] sizes under "sweep".  Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 
@@ -15,10 +17,11 @@ kernels are launched on.  Inputs are resident in HBM before the timed region.
 roofline.achieved uses the reference's bandwidth model, 3 passes x 8 B = 24
 bytes per point for fp32 (bench_fufft.cu:314-317), over the average launch
 duration; with a shared filter one of those passes is served from cache, so
-the physical minimum is 16 B/pt and `physical` reports that figure too.
-roofline.traffic is the HBM bytes per launch measured by rocprofv3 PMC
-(FETCH_SIZE + WRITE_SIZE) for this same command, read from the committed
-summary profiles/conv_f32_n4096.md when present.
+the physical minimum is 16 B/pt and `physical` reports that figure too.  For
+int16-BFP the model is 3 x 4 = 12 B/pt (physical 8 B/pt + 2 B per 64-point
+block of exponents).  roofline.traffic is the HBM bytes per launch measured by
+rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE) for this same command, read from the
+committed summary profiles/conv_f32_n4096.md when present.
 
 The cpu_baseline leg times the reference's own fp64 CPU conv path
 (cpu_mixed.cpp, built into oracle/_ref) -- or, where that was not built, this
@@ -51,15 +54,15 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--n", type=int, default=4096)
     p.add_argument("--points-log2", type=int, default=27)
-    p.add_argument("--variant", default="v16")
+    p.add_argument("--variant", default="auto")
+    p.add_argument("--sweep", default="512,1024,2048",
+                   help="extra fp32 sizes timed with --sweep-steps launches each ('' for none)")
+    p.add_argument("--sweep-steps", type=int, default=50)
+    p.add_argument("--no-bfp", action="store_true")
+    p.add_argument("--bfp-sizes", default="4096,512")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     return p.parse_args()
-
-
-def spectrum_from_taps(rng, n):
-    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
-    return taps
 
 
 def time_launches(torch, fn, steps, warmup, stream):
@@ -85,6 +88,75 @@ def measured_traffic(n, pts):
     if not m or int(m.group(2)) != pts:
         return None
     return float(m.group(1))
+
+
+def rel_l2(got, want):
+    return float(np.linalg.norm(got - want) / np.linalg.norm(want))
+
+
+def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed):
+    """fp32 fused conv at size n over pts points: (seconds per launch, rel L2 of a sample)."""
+    batch = pts // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
+    out = torch.empty_like(x)
+    rng = np.random.default_rng(seed)
+    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS)).to(dev)
+
+    def step():
+        ff.conv(x, filt, out, n=n, batch=batch, variant=variant, stream=stream)
+
+    # correctness before timing: fp64 numpy on a sample of signals
+    step()
+    torch.cuda.synchronize()
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
+    xs = x.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
+    ys = out.view(batch, n)[idx].cpu().numpy()
+    want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    rel = rel_l2(ys, want)
+    secs = time_launches(torch, step, steps, warmup, stream)
+    del x, out
+    return secs / steps, rel
+
+
+def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed):
+    """int16-BFP fused conv: Gaussian x 10^u per signal (u ~ U[-3, 3]), quantised on
+    the host by the library codec, one shared fp32 filter spectrum."""
+    batch = pts // n
+    rng = np.random.default_rng(seed)
+    x = np.empty((batch, n), dtype=np.complex64)
+    chunk = max(1, (1 << 22) // n)
+    for b0 in range(0, batch, chunk):
+        b1 = min(batch, b0 + chunk)
+        re = rng.standard_normal((b1 - b0, n), dtype=np.float32)
+        im = rng.standard_normal((b1 - b0, n), dtype=np.float32)
+        s = (10.0 ** rng.uniform(-3, 3, (b1 - b0, 1))).astype(np.float32)
+        x[b0:b1].real = re * s
+        x[b0:b1].imag = im * s
+    q, e = ff.bfp_quantize(x)
+    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+    filt = torch.from_numpy(ff.plan_filter(taps, n, variant="auto", kind=ff.FILTER_TAPS)).to(dev)
+    dq, de = torch.from_numpy(q).to(dev), torch.from_numpy(e).to(dev)
+    qo, eo = torch.empty_like(dq), torch.empty_like(de)
+
+    def step():
+        ff.conv_bfp16(dq, de, filt, qo, eo, n=n, batch=batch, stream=stream)
+
+    step()
+    torch.cuda.synchronize()
+    idx = np.linspace(0, batch - 1, 16).astype(np.int64)
+    qs = qo.view(batch, 2 * n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
+    es = eo.view(batch, n // ff.BFP_BLOCK)[torch.from_numpy(idx).to(dev)].cpu().numpy()
+    got = ff.bfp_dequantize(qs, es).reshape(16, n)
+    want = np.fft.ifft(np.fft.fft(x[idx].astype(np.complex128), axis=1)
+                       * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    per_sig = np.linalg.norm(got - want, axis=1) / np.linalg.norm(want, axis=1)
+    del x
+    secs = time_launches(torch, step, steps, warmup, stream)
+    del dq, de, qo, eo
+    return secs / steps, rel_l2(got, want), float(per_sig.max())
 
 
 def cpu_baseline(n, seconds, threads):
@@ -134,7 +206,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the path shards along the batch with no exchange, see DESIGN.md)", file=sys.stderr)
+              "(the path shards along the batch with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -146,36 +218,12 @@ def main():
     n = args.n
     pts = 1 << args.points_log2
     batch = pts // n
-    rng = np.random.default_rng(1)
-
-    # synthetic workload: signal and taps i.i.d. N(0,1) from a seed
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(1234)
-    x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
-    out = torch.empty_like(x)
-    taps = spectrum_from_taps(rng, n)
-    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=args.variant, kind=ff.FILTER_TAPS)).to(dev)
     stream = torch.cuda.current_stream()
 
-    # correctness before timing: fp64 numpy on a sample of signals
-    ff.conv(x, filt, out, n=n, batch=batch, variant=args.variant, stream=stream)
-    torch.cuda.synchronize()
-    idx = np.linspace(0, batch - 1, 16).astype(np.int64)
-    xs = x.view(batch, n)[torch.from_numpy(idx).to(dev)].cpu().numpy().astype(np.complex128)
-    ys = out.view(batch, n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
-    want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
-    rel = float(np.linalg.norm(ys - want) / np.linalg.norm(want))
+    avg, rel = bench_fp32(torch, ff, dev, n, pts, args.variant, args.steps, args.warmup, stream, 1234)
     if not rel <= 2e-6:
-        print(json.dumps({"error": f"accuracy check failed: rel L2 {rel:.3e}"}))
+        print(json.dumps({"error": f"fp32 accuracy check failed at N={n}: rel L2 {rel:.3e}"}))
         sys.exit(1)
-
-    def step():
-        ff.conv(x, filt, out, n=n, batch=batch, variant=args.variant, stream=stream)
-
-    torch.cuda.synchronize()
-    secs = time_launches(torch, step, args.steps, args.warmup, stream)
-    torch.cuda.synchronize()
-    avg = secs / args.steps
     gpts = pts / avg / 1e9
     achieved = 24.0 * pts / avg / 1e9
     physical = 16.0 * pts / avg / 1e9
@@ -195,7 +243,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"fused fp32 cyclic conv, N={n}, batch {batch} (2^{args.points_log2} points), "
-                               f"one shared filter, mid=multiply, variant={args.variant}",
+                               f"one shared filter, mid=multiply, variant={ff.resolve_variant(n, args.variant)}",
                    "n": n, "batch": batch, "points": pts},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
@@ -204,6 +252,39 @@ def main():
                                   "frac": round(physical / HBM_PEAK_GBS, 4)}},
         "accuracy": {"rel_l2_vs_fp64_sample": rel},
     }
+
+    sweep = {}
+    for s in [int(v) for v in args.sweep.split(",") if v.strip()]:
+        if s == n:
+            continue
+        a, r = bench_fp32(torch, ff, dev, s, pts, args.variant, args.sweep_steps, 3, stream, 77 + s)
+        sweep[str(s)] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                         "frac_24B": round(24.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                         "variant": ff.resolve_variant(s, args.variant), "rel_l2": r}
+        if not r <= 2e-6:
+            print(json.dumps({"error": f"fp32 accuracy check failed at N={s}: rel L2 {r:.3e}"}))
+            sys.exit(1)
+    if sweep:
+        line["sweep"] = sweep
+
+    if not args.no_bfp:
+        bfp = {}
+        for s in [int(v) for v in args.bfp_sizes.split(",") if v.strip()]:
+            a, r, worst = bench_bfp(torch, ff, dev, s, pts, args.steps if s == n else args.sweep_steps,
+                                    args.warmup if s == n else 3, stream, 99 + s)
+            if not r <= 1e-4:
+                print(json.dumps({"error": f"BFP accuracy check failed at N={s}: rel L2 {r:.3e}"}))
+                sys.exit(1)
+            g = pts / a / 1e9
+            bfp[str(s)] = {"gpoints_s": round(g, 3), "ms": round(a * 1e3, 5),
+                           "achieved_12B_gbs": round(12.0 * pts / a / 1e9, 1),
+                           "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                           "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst,
+                           "variant": ff.resolve_variant(s, "auto")}
+            if s == n:
+                bfp[str(s)]["speedup_vs_fp32"] = round(g / gpts, 3)
+        line["bfp"] = bfp
+
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(n, args.cpu_seconds, threads)

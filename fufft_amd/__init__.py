@@ -25,11 +25,18 @@ _LIB_PATH = Path(__file__).resolve().parent / "libfufft_amd.so"
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN = 0, -1, -2, -3, -4
 MID = {"mul": 0, "conj": 1, "none": 2}
-VARIANT = {"v16": 0, "r8": 1}
+VARIANT = {"v16": 0, "r8": 1, "auto": 2}
 LAYOUT = {"dr": 0, "lane": 1}
 FILTER_SPECTRUM, FILTER_TAPS = 0, 1
 BFP_BLOCK = 64
 VALUES_PER_LANE = {"v16": 16, "r8": 8}
+
+
+def resolve_variant(n: int, variant: str) -> str:
+    """The lane layout FUFFT_AUTO picks for n (mirrors the library's rule)."""
+    if variant != "auto":
+        return variant
+    return "r8" if 512 <= n <= 8192 else "v16"
 
 
 class FufftError(RuntimeError):
@@ -60,7 +67,7 @@ def _load() -> C.CDLL:
         "fufft_bfp_exponent": ([C.c_float], i32),
         "fufft_bfp_quantize": ([vp, i64, vp, vp], i32),
         "fufft_bfp_dequantize": ([vp, vp, i64, vp], i32),
-        "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, i32, vp], i32),
         "fufft_large_plan": ([i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
         "fufft_large_digit_order": ([i64, C.POINTER(C.c_int32)], i32),
         "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
@@ -173,6 +180,13 @@ def conv_r2(x, y, filt, u, v, n: int, batch: int, filt_stride: int = 0, variant:
     check(lib.fufft_conv_r2_f32(_ptr(x), _ptr(y), _ptr(filt), filt_stride, _ptr(u), _ptr(v), n,
                                 batch, VARIANT[variant], LAYOUT[layout], _stream(stream)),
           "fufft_conv_r2_f32")
+
+
+def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int = 0,
+               mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None) -> None:
+    check(lib.fufft_conv_bfp16(_ptr(qin), _ptr(ein), _ptr(filt), filt_stride, _ptr(qout),
+                               _ptr(eout), n, batch, MID[mid], VARIANT[variant], LAYOUT[layout],
+                               _stream(stream)), "fufft_conv_bfp16")
 
 
 def bfp_exponent(absmax: float) -> int:

@@ -1,0 +1,186 @@
+// int16 block-floating-point fused convolution for gfx950.
+//
+// Replaces fufft_pipeline_v16_bfp (fufft.cuh:1614-1701).  HBM carries 4 bytes
+// per point (int16 re in the low halfword, int16 im in the high halfword) plus
+// one int8 exponent per block of 64 consecutive points; all arithmetic in
+// between is the fp32 pipeline of conv1d.hip, bit for bit.  The reference
+// keeps one fp32 scale per transform and an int16 filter; here the filter is
+// fp32 and the exponent rule is
+//    e = -128 for an all-zero (or subnormal) block, else the smallest integer
+//        with absmax <= 32767 * 2^e, clamped at -128;   q = rint(x * 2^-e).
+//
+// Mapping: a transform has T = N/V >= 64 lanes, and register q of a wavefront
+// holds the 64 consecutive points 64*w + q*T .. (w = wavefront index within
+// the transform), i.e. exactly one block.  So input exponents are uniform per
+// (wavefront, register) and each output block's abs-max is one reduction across
+// the wavefront -- no LDS pass and no workgroup barrier for the scale, unlike
+// the reference's shared-memory atomicMax rendezvous (fufft.cuh:1674-1692).
+#include "fufft_device.hpp"
+#include "fufft_plan.hpp"
+#include "fufft_internal.hpp"
+
+namespace fufft {
+
+constexpr int bfp_cpb(int T) { return T >= 128 ? 1 : 256 / T; }
+
+// exponent of a block from its abs-max bits (see the rule above); every
+// operation is exact, so it agrees with the host codec and the CPU oracle
+__device__ __forceinline__ int bfp_exponent_bits(uint32_t bits)
+{
+   bits &= 0x7fffffffu;
+   const int xb = (int)(bits >> 23);
+   int e = xb - 141 + ((bits & 0x7fffffu) > 0x7ffe00u ? 1 : 0);
+   e = e < -128 ? -128 : e;
+   return xb == 0 ? -128 : e;
+}
+
+template<int CTRL>
+__device__ __forceinline__ float dpp_mov(float v)
+{
+   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// max over the 64 lanes of a wavefront, result uniform
+__device__ __forceinline__ float wave_max(float x)
+{
+   // DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
+   x = __builtin_fmaxf(x, dpp_mov<0xB1>(x));
+   x = __builtin_fmaxf(x, dpp_mov<0x4E>(x));
+   x = __builtin_fmaxf(x, dpp_mov<0x141>(x));
+   x = __builtin_fmaxf(x, dpp_mov<0x140>(x));
+   const int xi = __builtin_bit_cast(int, x);
+   const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 0));
+   const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
+   const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
+   const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
+   return __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
+}
+
+template<int N, int V, int LAYOUT, int MID>
+__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V))
+bfp_kernel(const BfpParams p)
+{
+   using PL = Plan<N, V>;
+   using LD = Lds<V, LAYOUT>;
+   constexpr int T     = PL::T;
+   constexpr int CPB   = bfp_cpb(T);
+   constexpr int SLOT  = LD::size(N);
+   constexpr int NB    = N / 64;                  // exponent blocks per transform
+   static_assert(T >= 64, "a wavefront register must cover one 64-point block");
+
+   extern __shared__ float2 lds[];
+   const int slot = threadIdx.x / T;
+   const int L    = threadIdx.x % T;
+   const int lane = threadIdx.x & 63;
+   const uint32_t t = blockIdx.x * CPB + slot;    // uniform per wavefront (T >= 64)
+   if(t >= p.ntrans) return;
+   const uint32_t tu = (uint32_t)uniform((int)t);
+   const int w = uniform(L >> 6);                 // wavefront within the transform
+
+   float2* A = lds + slot * SLOT;
+   Twiddles<PL> tw;
+   tw.load(p.tw, L);
+
+   // this wavefront's V input exponents: block w + q*T/64 of transform t
+   const Buf eb(p.ein + (size_t)tu * NB, NB);
+   const int my_e = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(
+      eb.r, (uint32_t)(w + (lane < V ? lane : 0) * (T / 64)), 0, 0);
+
+   const Buf qb(static_cast<const char*>(p.qin) + (size_t)tu * N * 4, N * 4);
+   float2 r[V];
+#pragma unroll
+   for(int q = 0; q < V; q++) {
+      const uint32_t word = qb.ldu((uint32_t)L * 4u, q * T * 4);
+      const int e = __builtin_amdgcn_readlane(my_e, q);
+      r[q] = make_float2(__builtin_amdgcn_ldexpf((float)(int)(int16_t)(word & 0xffffu), e),
+                         __builtin_amdgcn_ldexpf((float)((int)word >> 16), e));
+   }
+
+   forward_dif<PL, LD, (T < 64 ? 64 : T)>(r, A, L, tw);
+   {
+      const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
+      const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
+      mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
+   }
+   inverse_dit<PL, LD, (T < 64 ? 64 : T)>(r, A, L, tw);
+
+   // quantise: register q of this wavefront is block w + q*T/64
+   const Buf ob(static_cast<char*>(p.qout) + (size_t)tu * N * 4, N * 4);
+   const Buf xb(p.eout + (size_t)tu * NB, NB);
+#pragma unroll
+   for(int q = 0; q < V; q++) {
+      const float m = wave_max(__builtin_fmaxf(__builtin_fabsf(r[q].x), __builtin_fabsf(r[q].y)));
+      const int e = uniform(bfp_exponent_bits(__builtin_bit_cast(uint32_t, m)));
+      const int qr = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(r[q].x, -e));
+      const int qi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(r[q].y, -e));
+      ob.stu(((uint32_t)qr & 0xffffu) | ((uint32_t)qi << 16), (uint32_t)L * 4u, q * T * 4);
+      if(lane == 0)
+         __builtin_amdgcn_raw_buffer_store_b8((unsigned char)e, xb.r, (uint32_t)(w + q * (T / 64)), 0, 0);
+   }
+}
+
+template<int N, int V, int LAYOUT, int MID>
+static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
+{
+   constexpr int T = N / V, CPB = bfp_cpb(T);
+   const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
+   const void* k = reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID>);
+   if(shm > 65536) {
+      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+      if(e != hipSuccess) return e;
+   }
+   const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
+   BfpParams arg = p;
+   void* argv[] = { &arg };
+   return hipLaunchKernel(k, grid, block, argv, shm, s);
+}
+
+template<int N, int V>
+static hipError_t launch_bfp_nv(int layout, const BfpParams& p, hipStream_t s)
+{
+   if(layout == LAYOUT_XOR) {
+      switch(p.mid) {
+         case MID_MUL:  return launch_bfp_one<N, V, LAYOUT_XOR, MID_MUL>(p, s);
+         case MID_CONJ: return launch_bfp_one<N, V, LAYOUT_XOR, MID_CONJ>(p, s);
+         default:       return launch_bfp_one<N, V, LAYOUT_XOR, MID_NONE>(p, s);
+      }
+   }
+   switch(p.mid) {
+      case MID_MUL:  return launch_bfp_one<N, V, LAYOUT_PAD, MID_MUL>(p, s);
+      case MID_CONJ: return launch_bfp_one<N, V, LAYOUT_PAD, MID_CONJ>(p, s);
+      default:       return launch_bfp_one<N, V, LAYOUT_PAD, MID_NONE>(p, s);
+   }
+}
+
+bool bfp_supported(int n, int v)
+{
+   if(v == 8)  return n >= 512 && n <= 8192 && (n & (n - 1)) == 0;
+   if(v == 16) return n >= 1024 && n <= 16384 && (n & (n - 1)) == 0;
+   return false;
+}
+
+hipError_t launch_bfp(int n, int v, int layout, const BfpParams& p, hipStream_t s)
+{
+   if(v == 8) {
+      switch(n) {
+         case 512:  return launch_bfp_nv<512, 8>(layout, p, s);
+         case 1024: return launch_bfp_nv<1024, 8>(layout, p, s);
+         case 2048: return launch_bfp_nv<2048, 8>(layout, p, s);
+         case 4096: return launch_bfp_nv<4096, 8>(layout, p, s);
+         case 8192: return launch_bfp_nv<8192, 8>(layout, p, s);
+         default:   break;
+      }
+   } else if(v == 16) {
+      switch(n) {
+         case 1024:  return launch_bfp_nv<1024, 16>(layout, p, s);
+         case 2048:  return launch_bfp_nv<2048, 16>(layout, p, s);
+         case 4096:  return launch_bfp_nv<4096, 16>(layout, p, s);
+         case 8192:  return launch_bfp_nv<8192, 16>(layout, p, s);
+         case 16384: return launch_bfp_nv<16384, 16>(layout, p, s);
+         default:    break;
+      }
+   }
+   return hipErrorInvalidValue;
+}
+
+}  // namespace fufft

@@ -49,11 +49,13 @@ void fill_table(int log_max, float* out)
    }
 }
 
+// LDS layout: padded by default (additive addresses); FUFFT_LDS_LAYOUT=xor
+// selects the zero-padding XOR swizzle (a tuning knob, both are bit-identical)
 int lds_layout()
 {
    static const int layout = [] {
       const char* e = std::getenv("FUFFT_LDS_LAYOUT");
-      return (e && std::strcmp(e, "pad") == 0) ? LAYOUT_PAD : LAYOUT_XOR;
+      return (e && std::strcmp(e, "xor") == 0) ? LAYOUT_XOR : LAYOUT_PAD;
    }();
    return layout;
 }
@@ -100,6 +102,15 @@ int status_of(hipError_t e) { return e == hipSuccess ? FUFFT_OK : FUFFT_ERR_HIP;
 bool pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+// FUFFT_AUTO resolves to the faster lane layout measured on MI355X: radix 8
+// (eight values per lane: twice the wavefronts per CU for the same LDS) from
+// N = 512 to 8192, radix 16 elsewhere.
+int resolve_variant(int64_t n, int variant)
+{
+   if(variant != FUFFT_AUTO) return variant;
+   return (n >= 512 && n <= 8192) ? FUFFT_R8 : FUFFT_V16;
+}
 
 int values_per_lane(int variant)
 {
@@ -198,13 +209,13 @@ const char* fufft_status_string(int status)
 
 int fufft_supported(int64_t n, int variant)
 {
-   const int v = values_per_lane(variant);
+   const int v = values_per_lane(resolve_variant(n, variant));
    return (v && pow2(n) && n <= 16384 && conv1d_supported((int)n, v)) ? 1 : 0;
 }
 
 int fufft_plan_radices(int64_t n, int variant, int* radices)
 {
-   const int v = values_per_lane(variant);
+   const int v = values_per_lane(resolve_variant(n, variant));
    if(!v || !radices || !pow2(n) || n < 2) return FUFFT_ERR_INVALID;
    return factor(n, v, radices);
 }
@@ -222,7 +233,7 @@ int fufft_digit_order(int64_t n, int variant, int32_t* perm)
 int fufft_plan_filter_f32(int64_t n, int variant, int layout, int filter_kind,
                           int fold_inv_n, const float* in, float* out)
 {
-   const int v = values_per_lane(variant);
+   const int v = values_per_lane(resolve_variant(n, variant));
    if(!v || !in || !out || !pow2(n) || n < v) return FUFFT_ERR_INVALID;
    if(layout != FUFFT_LAYOUT_DR && layout != FUFFT_LAYOUT_LANE) return FUFFT_ERR_INVALID;
    if(filter_kind != FUFFT_FILTER_SPECTRUM && filter_kind != FUFFT_FILTER_TAPS) return FUFFT_ERR_INVALID;
@@ -251,7 +262,7 @@ int fufft_twiddle_table_host(int log_max, float* out)
 
 static int check_1d(int64_t n, int64_t batch, int variant, int mid, int layout, int* v)
 {
-   *v = values_per_lane(variant);
+   *v = values_per_lane(resolve_variant(n, variant));
    if(!*v) return FUFFT_ERR_INVALID;
    if(mid < FUFFT_MID_MUL || mid > FUFFT_MID_NONE) return FUFFT_ERR_INVALID;
    if(layout != FUFFT_LAYOUT_DR && layout != FUFFT_LAYOUT_LANE) return FUFFT_ERR_INVALID;
@@ -339,6 +350,30 @@ int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
    p.in0 = x; p.in1 = y; p.filt = filt; p.out0 = u; p.out1 = v;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = FUFFT_MID_MUL; p.fl = layout;
    return run_conv1d(K_CONV_R2, (int)n, vl, p, stream);
+}
+
+// ---- BFP fused conv ------------------------------------------------------------------
+
+int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
+                     int64_t filt_stride, void* qout, int8_t* eout, int64_t n,
+                     int64_t batch, int mid, int variant, int layout, void* stream)
+{
+   const int vv = resolve_variant(n, variant);
+   const int v = values_per_lane(vv);
+   if(!v || mid < FUFFT_MID_MUL || mid > FUFFT_MID_NONE) return FUFFT_ERR_INVALID;
+   if(layout != FUFFT_LAYOUT_DR && layout != FUFFT_LAYOUT_LANE) return FUFFT_ERR_INVALID;
+   if(batch < 0 || batch > 0xffffffffll) return FUFFT_ERR_INVALID;
+   if(!pow2(n) || n > 16384 || !bfp_supported((int)n, v)) return FUFFT_ERR_UNSUPPORTED;
+   if(!qin || !ein || !qout || !eout || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(!aligned4(qin) || !aligned4(qout) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   BfpParams p{};
+   int st;
+   if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   if(batch == 0) return FUFFT_OK;
+   p.qin = qin; p.ein = ein; p.filt = filt; p.qout = qout; p.eout = eout;
+   p.ntrans = (uint32_t)batch; p.mid = mid; p.fl = layout;
+   return status_of(launch_bfp((int)n, v, lds_layout(), p, static_cast<hipStream_t>(stream)));
 }
 
 // ---- BFP host codec -----------------------------------------------------------------

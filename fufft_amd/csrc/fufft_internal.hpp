@@ -42,8 +42,8 @@ struct BfpParams {
    int32_t       fl;
 };
 
-bool       bfp_supported(int n);
-hipError_t launch_bfp(int n, int layout, const BfpParams& p, hipStream_t s);
+bool       bfp_supported(int n, int v);
+hipError_t launch_bfp(int n, int v, int layout, const BfpParams& p, hipStream_t s);
 
 // ---- four-step outer levels (large.hip) -------------------------------------------
 hipError_t launch_outer_pass(float2* buf, int64_t total, int R, int M, int sign, int dit,

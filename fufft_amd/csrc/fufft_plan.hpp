@@ -58,18 +58,20 @@ __device__ __forceinline__ void static_for(F&& f)
 }
 
 // ---- LDS layouts ------------------------------------------------------------------
-// phys(i) maps logical position i of a transform to its float2 slot.  Every
-// pass touches positions base(L) + k*M; with 8-byte accesses a bank conflict
-// arises when lanes serviced in the same cycle hit equal slot numbers modulo
-// 16 (32 banks x 4 B, 16 lanes per cycle) or modulo 32 (64 banks, 32 lanes per
-// cycle).  Both layouts below are bijections; tests/test_lds_audit.py checks
-// every access pattern of every plan against both models.
+// phys(i) maps logical position i of a transform to its float2 slot.  gfx950
+// LDS has 64 banks of 4 bytes; a ds_read_b64 / ds_write_b64 is serviced 32
+// lanes at a time, so lanes of an aligned half-wave conflict when their slots
+// are equal modulo 32 (measured with SQ_LDS_BANK_CONFLICT; each extra way costs
+// one cycle per instruction).  tests/test_lds_audit.py checks every access
+// pattern of every plan against this model.
 //
 // Xor: bits [0, v) ^= bits [v, 2v), bits [v, 5) ^= bits [2v, v+5).  Conflict
-// free under both models; costs about one v_xor per access in the M = 1 and
-// M = V passes.
-// Pad: one spare slot after every 16 (phys = i + i/16).  Every access of a pass
-// becomes base(L) + compile-time offset; 6.25% more LDS.
+// free for every pass pattern, but the XOR keeps one address register per tap.
+// Pad: one spare slot after every V (phys = i + i/V, i.e. 1/16 or 1/8 more
+// LDS).  For every pass the padded address is additive,
+//    phys(base + k*M) = phys(base) + phys(k*M),
+// so a lane computes one address per group and the taps use immediate
+// offsets.  At most 2-way conflicts remain in the consecutive-lane passes.
 enum { LAYOUT_XOR = 0, LAYOUT_PAD = 1 };
 
 template<int V, int LAYOUT>
@@ -79,17 +81,21 @@ template<int V>
 struct Lds<V, LAYOUT_XOR> {
    static constexpr int LOGV = ilog2c(V);
    static constexpr int HI   = 5 - LOGV;      // bits folded into [v, 5)
+   static constexpr bool additive = false;
    static constexpr int size(int n) { return n; }
    __device__ __forceinline__ static int phys(int i)
    {
       return i ^ ((i >> LOGV) & (V - 1)) ^ (((i >> (2 * LOGV)) & ((1 << HI) - 1)) << LOGV);
    }
+   static constexpr int cphys(int i) { return i; }
 };
 
 template<int V>
 struct Lds<V, LAYOUT_PAD> {
-   static constexpr int size(int n) { return n + n / 16; }
-   __device__ __forceinline__ static int phys(int i) { return i + (i >> 4); }
+   static constexpr bool additive = true;
+   static constexpr int size(int n) { return n + n / V; }
+   __device__ __forceinline__ static int phys(int i) { return i + i / V; }
+   static constexpr int cphys(int i) { return i + i / V; }
 };
 
 // ---- pass machinery ---------------------------------------------------------------
@@ -102,14 +108,25 @@ __device__ __forceinline__ int tap_pos(int L, int g, int k)
    return b * R * M + j + k * M;
 }
 
+// LDS slot of tap k of group g: one address per group plus a compile-time
+// offset for additive layouts, the full map per tap otherwise
 template<class PL, int P, class LD>
-__device__ __forceinline__ void lds_gather(float2 (&r)[PL::V], const float2* A, int L)
+__device__ __forceinline__ float2* tap_ptr(float2* A, int base_phys, int L, int g, int k)
+{
+   if constexpr(LD::additive) return A + base_phys + LD::cphys(k * PL::stride(P));
+   else                       return A + LD::phys(tap_pos<PL, P>(L, g, k));
+}
+
+template<class PL, int P, class LD>
+__device__ __forceinline__ void lds_gather(float2 (&r)[PL::V], float2* A, int L)
 {
    constexpr int R = PL::radix(P), G = PL::V / R;
 #pragma unroll
-   for(int g = 0; g < G; g++)
+   for(int g = 0; g < G; g++) {
+      const int bp = LD::additive ? LD::phys(tap_pos<PL, P>(L, g, 0)) : 0;
 #pragma unroll
-      for(int k = 0; k < R; k++) r[g + k * G] = A[LD::phys(tap_pos<PL, P>(L, g, k))];
+      for(int k = 0; k < R; k++) r[g + k * G] = *tap_ptr<PL, P, LD>(A, bp, L, g, k);
+   }
 }
 
 template<class PL, int P, class LD>
@@ -117,9 +134,11 @@ __device__ __forceinline__ void lds_scatter(const float2 (&r)[PL::V], float2* A,
 {
    constexpr int R = PL::radix(P), G = PL::V / R;
 #pragma unroll
-   for(int g = 0; g < G; g++)
+   for(int g = 0; g < G; g++) {
+      const int bp = LD::additive ? LD::phys(tap_pos<PL, P>(L, g, 0)) : 0;
 #pragma unroll
-      for(int k = 0; k < R; k++) A[LD::phys(tap_pos<PL, P>(L, g, k))] = r[g + k * G];
+      for(int k = 0; k < R; k++) *tap_ptr<PL, P, LD>(A, bp, L, g, k) = r[g + k * G];
+   }
 }
 
 // ---- stage twiddles --------------------------------------------------------------

@@ -21,7 +21,7 @@
  *     (one filter shared by the batch) or n (one filter per signal).
  *
  * Supported sizes (fufft_supported): single-launch N = 2^k with
- * 256 <= N <= 16384 for FUFFT_V16 and 512 <= N <= 4096 for FUFFT_R8; the
+ * 256 <= N <= 16384 for FUFFT_V16 and 512 <= N <= 8192 for FUFFT_R8; the
  * four-step path takes N = 16^L * MID up to 2^20.
  */
 #ifndef FUFFT_FUFFT_H
@@ -49,6 +49,9 @@ extern "C" {
 /* lane layout / radix family */
 #define FUFFT_V16  0   /* 16 values per lane, radix 16 (fufft_pipeline_v16)  */
 #define FUFFT_R8   1   /* 8 values per lane, radix 8 (fufft_pipeline_ip)     */
+#define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X:
+                          FUFFT_R8 for 512 <= N <= 8192, else FUFFT_V16.
+                          The filter must be planned with the same variant. */
 
 /* filter layouts */
 #define FUFFT_LAYOUT_DR    0  /* slot i holds bin mixedrev(i) (MidMultiply, fufft.cuh:635) */
@@ -129,9 +132,15 @@ int fufft_bfp_exponent(float absmax);
 /* host reference codec (bfp_quant_host, bench_fufft.cu:105-117) */
 int fufft_bfp_quantize(const float* x, int64_t npts, int16_t* q, int8_t* e);
 int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float* x);
+/* Fused conv on BFP data: dequantise on load, the fp32 pipeline of
+ * fufft_conv_f32 (bit for bit), quantise on store with the rule above.
+ * qin / qout: n*batch points (4 bytes each); ein / eout: n*batch/64 exponents;
+ * filt: fp32 filter planned for the same variant.  Needs n/V >= 64 lanes:
+ * FUFFT_R8 512..8192, FUFFT_V16 1024..16384.  qin == qout and ein == eout are
+ * allowed. */
 int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
                      int64_t filt_stride, void* qout, int8_t* eout, int64_t n,
-                     int64_t batch, int mid, int layout, void* stream);
+                     int64_t batch, int mid, int variant, int layout, void* stream);
 
 /* ---- four-step large N -------------------------------------------------------------
  * N = 16^lout * mid with mid a single-launch size: lout radix-16 DIF levels

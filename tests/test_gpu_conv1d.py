@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 TOL_F32 = 2e-6
 V = {"v16": 16, "r8": 8}
 SIZES = [("v16", n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + \
-        [("r8", n) for n in (512, 1024, 2048, 4096)]
+        [("r8", n) for n in (512, 1024, 2048, 4096, 8192)]
 
 
 def to_dev(x, dev):

@@ -1,0 +1,111 @@
+"""CPU audit of the LDS layouts used by the fused kernels (fufft_plan.hpp).
+
+For every plan (V, N) and every pass, it enumerates the slot each lane touches
+for each tap and checks, under the gfx950 bank model measured with
+SQ_LDS_BANK_CONFLICT (64 banks x 4 B; an 8-byte access is serviced 32 lanes
+at a time, so lanes of an aligned half-wave conflict when their slots agree
+modulo 32):
+
+  - the layout is a bijection onto [0, size(N));
+  - the padded layout is additive for every pass, phys(base + k*M) =
+    phys(base) + phys(k*M), which the kernels rely on when they address taps
+    with one register plus immediate offsets;
+  - the conflict degree stays within the bound documented for the layout
+    (XOR: conflict free everywhere; PAD: at most 2-way);
+  - the reference's own swizzle, derived for 32 banks / 16-lane phases, is not
+    conflict free under this model (why the layout was re-derived).
+"""
+import itertools
+
+import pytest
+
+
+def ilog2(x):
+    return x.bit_length() - 1
+
+
+def phys_xor(i, v):
+    lv = ilog2(v)
+    hi = 5 - lv
+    return i ^ ((i >> lv) & (v - 1)) ^ (((i >> (2 * lv)) & ((1 << hi) - 1)) << lv)
+
+
+def phys_pad(i, v):
+    return i + i // v
+
+
+def plan(n, v):
+    m, lv = ilog2(n), ilog2(v)
+    lead = 1 << (m % lv)
+    rads = ([lead] if lead > 1 else []) + [v] * (m // lv)
+    out, M = [], n
+    for r in rads:
+        M //= r
+        out.append((r, M))
+    return out
+
+
+def tap_pos(L, g, k, R, M, T):
+    gidx = L + g * T
+    j, b = gidx % M, gidx // M
+    return b * R * M + j + k * M
+
+
+def lane_sets(n, v):
+    """(pass, group, k) -> list of logical positions, one per lane"""
+    T = n // v
+    for (R, M) in plan(n, v):
+        G = v // R
+        for g, k in itertools.product(range(G), range(R)):
+            yield (R, M, g, k), [tap_pos(L, g, k, R, M, T) for L in range(T)]
+
+
+def degree(slots, lanes=32):
+    worst = 1
+    for h in range(0, len(slots), lanes):
+        banks = {}
+        for s in slots[h:h + lanes]:
+            banks.setdefault(s % 32, set()).add(s)
+        worst = max(worst, max(len(x) for x in banks.values()))
+    return worst
+
+
+PLANS = [(16, n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + [(8, n) for n in (512, 1024, 2048, 4096)]
+
+
+@pytest.mark.parametrize("v,n", PLANS)
+def test_layouts_are_bijections(v, n):
+    assert sorted(phys_xor(i, v) for i in range(n)) == list(range(n))
+    pad = [phys_pad(i, v) for i in range(n)]
+    assert len(set(pad)) == n and max(pad) < n + n // v
+
+
+@pytest.mark.parametrize("v,n", PLANS)
+def test_pad_layout_is_additive(v, n):
+    T = n // v
+    for (R, M), g in ((rm, g) for rm in plan(n, v) for g in range(v // rm[0])):
+        for L in range(T):
+            base = tap_pos(L, g, 0, R, M, T)
+            for k in range(R):
+                assert phys_pad(base + k * M, v) == phys_pad(base, v) + phys_pad(k * M, v), (R, M, L, g, k)
+
+
+@pytest.mark.parametrize("v,n", PLANS)
+def test_conflict_degree(v, n):
+    for key, pos in lane_sets(n, v):
+        if len(pos) < 32:          # transforms narrower than a half-wave sit side by side
+            stride = n
+            reps = 32 // len(pos)
+            pos = [p + r * stride for r in range(reps) for p in pos]
+        assert degree([phys_xor(p, v) for p in pos]) == 1, ("xor", key)
+        assert degree([phys_pad(p, v) for p in pos]) <= 2, ("pad", key)
+
+
+def test_reference_swizzle_conflicts_on_gfx950():
+    """SWZ16 (fufft.cuh:668) targets 32 banks x 16-lane phases; under the
+    64-bank, 32-lane model its M = 1 pattern is not conflict free."""
+    def swz16(i):
+        return i ^ ((i >> 3) & 15) ^ ((i >> 7) & 15)
+    n, v = 4096, 16
+    worst = max(degree([swz16(p) for p in pos]) for _, pos in lane_sets(n, v))
+    assert worst > 1
