@@ -62,7 +62,19 @@ def parse():
     p.add_argument("--bfp-sizes", default="4096,512")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--copy-only", action="store_true",
+                   help="time only a device copy of the workload's bytes (HBM ceiling and the "
+                        "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
+
+
+def copy_ceiling(torch, dev, pts, steps, warmup, stream):
+    """GB/s (read + write) of torch's device copy over pts complex64 points."""
+    x = torch.empty(pts, dtype=torch.complex64, device=dev).fill_(1.0)
+    y = torch.empty_like(x)
+    secs = time_launches(torch, lambda: y.copy_(x), steps, warmup, stream)
+    del x, y
+    return 2.0 * pts * 8 * steps / secs / 1e9, secs / steps
 
 
 def time_launches(torch, fn, steps, warmup, stream):
@@ -220,6 +232,12 @@ def main():
     batch = pts // n
     stream = torch.cuda.current_stream()
 
+    if args.copy_only:
+        gbs, t = copy_ceiling(torch, dev, pts, args.steps, args.warmup, stream)
+        print(json.dumps({"copy_bytes": 2 * pts * 8, "ms": round(t * 1e3, 5), "gb_s": round(gbs, 1)}))
+        return
+    copy_gbs, _ = copy_ceiling(torch, dev, pts, 20, 3, stream)
+
     avg, rel = bench_fp32(torch, ff, dev, n, pts, args.variant, args.steps, args.warmup, stream, 1234)
     if not rel <= 2e-6:
         print(json.dumps({"error": f"fp32 accuracy check failed at N={n}: rel L2 {rel:.3e}"}))
@@ -249,7 +267,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "model_bytes_per_point": 24,
                      "physical": {"bytes_per_point": 16, "achieved": round(physical, 1),
-                                  "frac": round(physical / HBM_PEAK_GBS, 4)}},
+                                  "frac": round(physical / HBM_PEAK_GBS, 4)},
+                     "copy_ceiling_gbs": round(copy_gbs, 1)},
         "accuracy": {"rel_l2_vs_fp64_sample": rel},
     }
 
