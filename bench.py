@@ -60,6 +60,8 @@ def parse():
     p.add_argument("--sweep-steps", type=int, default=50)
     p.add_argument("--no-bfp", action="store_true")
     p.add_argument("--bfp-sizes", default="4096,512")
+    p.add_argument("--large-sizes", default="32768,65536",
+                   help="four-step sizes timed with --sweep-steps calls each ('' for none)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--copy-only", action="store_true",
@@ -130,6 +132,34 @@ def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed):
     rel = rel_l2(ys, want)
     secs = time_launches(torch, step, steps, warmup, stream)
     del x, out
+    return secs / steps, rel
+
+
+def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed):
+    """Four-step conv: batch pts/n of U[-1,1) signals, one
+    shared filter, in place.  Returns (seconds per call, rel L2 of a sample)."""
+    batch = pts // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = (torch.rand(2 * pts, device=dev, generator=gen) * 2 - 1).view(torch.complex64)
+    rng = np.random.default_rng(seed)
+    taps = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)).astype(np.complex64)
+    filt = torch.from_numpy(ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS)).to(dev)
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 8).astype(np.int64)).to(dev)
+    xs = x.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
+    ff.conv_large(x, filt, n=n, batch=batch, stream=stream)
+    torch.cuda.synchronize()
+    ys = x.view(batch, n)[idx].cpu().numpy()
+    want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    rel = rel_l2(ys, want)
+    # the call is in place, so the timed launches re-convolve their own output;
+    # they use an all-pass filter (unit-modulus spectrum, random phase) of the
+    # same cost, which keeps the data's norm fixed over any number of launches
+    phase = np.exp(2j * np.pi * rng.uniform(0, 1, n)).astype(np.complex64)
+    filt = torch.from_numpy(ff.plan_filter_large(phase, n, kind=ff.FILTER_SPECTRUM)).to(dev)
+    secs = time_launches(torch, lambda: ff.conv_large(x, filt, n=n, batch=batch, stream=stream),
+                         steps, warmup, stream)
+    del x
     return secs / steps, rel
 
 
@@ -303,6 +333,23 @@ def main():
             if s == n:
                 bfp[str(s)]["speedup_vs_fp32"] = round(g / gpts, 3)
         line["bfp"] = bfp
+
+    large = {}
+    for s in [int(v) for v in args.large_sizes.split(",") if v.strip()]:
+        lout, mid = ff.large_plan(s)
+        a, r = bench_large(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 5 + s)
+        if not r <= 2e-6:
+            print(json.dumps({"error": f"four-step accuracy check failed at N={s}: rel L2 {r:.3e}"}))
+            sys.exit(1)
+        model = (4 * lout + 3) * 8
+        large[str(s)] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                         "plan": f"{lout} outer radix-16 level(s) + fused middle N={mid}",
+                         "model_bytes_per_point": model,
+                         "frac_model": round(model * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                         "physical_bytes_per_point": model - 8,
+                         "rel_l2": r}
+    if large:
+        line["large"] = large
 
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)

@@ -189,6 +189,39 @@ def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int 
                                _stream(stream)), "fufft_conv_bfp16")
 
 
+# ---- four-step large N -------------------------------------------------------------------
+
+def large_plan(n: int) -> tuple[int, int]:
+    """(lout, mid): n = 16^lout * mid, the middle a single-launch size."""
+    lout, mid = C.c_int(), C.c_int()
+    check(lib.fufft_large_plan(n, C.byref(lout), C.byref(mid)), "fufft_large_plan")
+    return lout.value, mid.value
+
+
+def large_digit_order(n: int) -> np.ndarray:
+    perm = np.empty(n, dtype=np.int32)
+    check(lib.fufft_large_digit_order(n, perm.ctypes.data_as(C.POINTER(C.c_int32))),
+          "fufft_large_digit_order")
+    return perm
+
+
+def plan_filter_large(x: np.ndarray, n: int, kind: int = FILTER_SPECTRUM,
+                      fold_inv_n: bool = True) -> np.ndarray:
+    src = np.ascontiguousarray(x, dtype=np.complex64)
+    assert src.size == n
+    out = np.empty(n, dtype=np.complex64)
+    check(lib.fufft_plan_filter_large_f32(n, kind, int(fold_inv_n), src.ctypes.data, out.ctypes.data),
+          "fufft_plan_filter_large_f32")
+    return out
+
+
+def conv_large(buf, filt, n: int, batch: int, filt_stride: int = 0, mid: str = "mul",
+               stream=None) -> None:
+    """Four-step conv of a batch of n-point signals, in place on buf."""
+    check(lib.fufft_conv_large_f32(_ptr(buf), _ptr(filt), filt_stride, n, batch, MID[mid],
+                                   _stream(stream)), "fufft_conv_large_f32")
+
+
 def bfp_exponent(absmax: float) -> int:
     return lib.fufft_bfp_exponent(absmax)
 

@@ -415,4 +415,95 @@ int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float*
    return FUFFT_OK;
 }
 
+// ---- four-step large N -----------------------------------------------------------------
+
+int fufft_large_plan(int64_t n, int* lout, int* mid)
+{
+   if(!lout || !mid) return FUFFT_ERR_INVALID;
+   if(!pow2(n) || n < 8192 || n > ((int64_t)1 << FUFFT_TW_LOG_MAX)) return FUFFT_ERR_UNSUPPORTED;
+   // fewest outer levels that bring the middle to a single-workgroup size
+   // <= 4096; the middle then lies in [512, 4096], where the radix-8 kernel
+   // is the fastest
+   int lo = 1;
+   while((n >> (4 * lo)) > 4096) lo++;
+   *lout = lo;
+   *mid = (int)(n >> (4 * lo));
+   return FUFFT_OK;
+}
+
+// chain radices: lout radix-16 outer levels, then the middle's own plan
+static int large_radices(int64_t n, int* lout, int* mid, int* r)
+{
+   const int st = fufft_large_plan(n, lout, mid);
+   if(st != FUFFT_OK) return st;
+   int np = 0;
+   for(int i = 0; i < *lout; i++) r[np++] = 16;
+   np += factor(*mid, values_per_lane(resolve_variant(*mid, FUFFT_AUTO)), r + np);
+   return np;
+}
+
+int fufft_large_digit_order(int64_t n, int32_t* perm)
+{
+   int r[64], lout = 0, mid = 0;
+   const int np = large_radices(n, &lout, &mid, r);
+   if(np < 0) return np;
+   if(!perm) return FUFFT_ERR_INVALID;
+   for(int64_t i = 0; i < n; i++) perm[i] = group_reverse((int32_t)i, r, np);
+   return FUFFT_OK;
+}
+
+int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n, const float* in,
+                                float* out)
+{
+   int r[64], lout = 0, mid = 0;
+   const int np = large_radices(n, &lout, &mid, r);
+   if(np < 0) return np;
+   if(!in || !out) return FUFFT_ERR_INVALID;
+   if(filter_kind != FUFFT_FILTER_SPECTRUM && filter_kind != FUFFT_FILTER_TAPS) return FUFFT_ERR_INVALID;
+   const std::vector<double> s = spectrum_of(n, filter_kind, fold_inv_n, in);
+   for(int64_t i = 0; i < n; i++) {
+      const int32_t bin = group_reverse((int32_t)i, r, np);
+      out[2 * i]     = (float)s[2 * bin];
+      out[2 * i + 1] = (float)s[2 * bin + 1];
+   }
+   return FUFFT_OK;
+}
+
+int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64_t n,
+                         int64_t batch, int mid, void* stream)
+{
+   int lout = 0, mn = 0;
+   int st = fufft_large_plan(n, &lout, &mn);
+   if(st != FUFFT_OK) return st;
+   if(mid < FUFFT_MID_MUL || mid > FUFFT_MID_NONE) return FUFFT_ERR_INVALID;
+   if(batch < 0 || batch * (n / 16) > 0xffffffffll) return FUFFT_ERR_INVALID;
+   if(!buf || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(!aligned16(buf) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   if(filt_stride != 0 && filt_stride != n) return FUFFT_ERR_INVALID;
+   const int v = values_per_lane(resolve_variant(mn, FUFFT_AUTO));
+   if(!conv1d_supported(mn, v)) return FUFFT_ERR_UNSUPPORTED;
+   Conv1dParams p{};
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   if(batch == 0) return FUFFT_OK;
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   float2* a = static_cast<float2*>(buf);
+   hipError_t e = hipSuccess;
+   // forward outer levels, largest stride first
+   for(int l = 0; l < lout && e == hipSuccess; l++)
+      e = launch_outer_pass(a, n, batch, n >> (4 * (l + 1)), false, p.tw, s);
+   if(e != hipSuccess) return status_of(e);
+   // the middle: every mn-point chunk is one fused conv, in place; chunk c of
+   // a transform uses filter slots [c*mn, (c+1)*mn) of the chained order
+   const int64_t chunks = batch * (n / mn);
+   p.in0 = buf; p.out0 = buf; p.filt = filt;
+   p.ntrans = (uint32_t)chunks;
+   p.fcount = (uint32_t)(filt_stride == 0 ? n / mn : chunks);
+   p.scount = 1; p.mid = mid; p.fl = FUFFT_LAYOUT_DR;
+   if((e = launch_conv1d(K_CONV, mn, v, lds_layout(), p, s)) != hipSuccess) return status_of(e);
+   // inverse outer levels, smallest stride first
+   for(int l = lout - 1; l >= 0 && e == hipSuccess; l--)
+      e = launch_outer_pass(a, n, batch, n >> (4 * (l + 1)), true, p.tw, s);
+   return status_of(e);
+}
+
 }  // extern "C"

@@ -46,7 +46,9 @@ bool       bfp_supported(int n, int v);
 hipError_t launch_bfp(int n, int v, int layout, const BfpParams& p, hipStream_t s);
 
 // ---- four-step outer levels (large.hip) -------------------------------------------
-hipError_t launch_outer_pass(float2* buf, int64_t total, int R, int M, int sign, int dit,
+// one radix-16 level (stride M) over a batch of n-point transforms, in place;
+// dit = false: forward DIF level, dit = true: inverse DIT level
+hipError_t launch_outer_pass(float2* buf, int64_t n, int64_t batch, int64_t M, bool dit,
                              const float2* tw, hipStream_t s);
 
 // ---- 2D column kernels (conv2d.hip) -------------------------------------------------
