@@ -62,6 +62,7 @@ def parse():
     p.add_argument("--bfp-sizes", default="4096,512")
     p.add_argument("--large-sizes", default="32768,65536",
                    help="four-step sizes timed with --sweep-steps calls each ('' for none)")
+    p.add_argument("--no-2d", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--copy-only", action="store_true",
@@ -161,6 +162,64 @@ def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed):
                          steps, warmup, stream)
     del x
     return secs / steps, rel
+
+
+def bench_2d(torch, ff, dev, pts, steps, warmup, stream, seed):
+    """BASELINE configs[4] at 512 x 512: (a) two real images per complex
+    transform, 2^27 real pixels U[0,1), one real filter U[0,1); (b) the split
+    path: one image transformed once, applied against 256 filters with
+    Gaussian spectra.  Returns a dict for the JSON line."""
+    h = w = 512
+    np_img = h * w
+    nimg = pts // np_img // 2                    # packed complex transforms
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.rand(nimg * np_img, device=dev, generator=gen)
+    y = torch.rand(nimg * np_img, device=dev, generator=gen)
+    u, v = torch.empty_like(x), torch.empty_like(y)
+    work = torch.empty(nimg * np_img, dtype=torch.complex64, device=dev)
+    taps = rng.uniform(0, 1, np_img).astype(np.complex64)
+    filt = torch.from_numpy(ff.plan_filter2d(taps, h, w, kind=ff.FILTER_TAPS)).to(dev)
+
+    def r2():
+        ff.conv2d_r2(x, y, filt, u, v, work, h, w, nimg, stream=stream)
+
+    r2()
+    torch.cuda.synchronize()
+    xs = x.view(nimg, h, w)[0].cpu().numpy().astype(np.float64)
+    want = np.real(np.fft.ifft2(np.fft.fft2(xs) * np.fft.fft2(taps.real.reshape(h, w).astype(np.float64))))
+    rel_r2 = rel_l2(u.view(nimg, h, w)[0].cpu().numpy(), want)
+    t_r2 = time_launches(torch, r2, steps, warmup, stream) / steps
+    del x, y, u, v, work
+
+    nf = 256
+    a = torch.rand(2 * np_img, device=dev, generator=gen).view(torch.complex64)
+    spec = torch.empty_like(a)
+    spec_nat = (rng.standard_normal((nf, np_img)) + 1j * rng.standard_normal((nf, np_img))).astype(np.complex64)
+    filters = torch.from_numpy(np.concatenate([ff.plan_filter2d(spec_nat[i], h, w) for i in range(nf)])).to(dev)
+    out = torch.empty(nf * np_img, dtype=torch.complex64, device=dev)
+    ff.fwd2d(a, spec, h, w, 1, stream=stream)
+
+    def apply():
+        ff.apply2d(spec, filters, out, h, w, nf, spec_stride=0, filt_stride=np_img, stream=stream)
+
+    apply()
+    torch.cuda.synchronize()
+    fa = np.fft.fft2(a.cpu().numpy().reshape(h, w).astype(np.complex128))
+    rel_ap = rel_l2(out.view(nf, np_img)[5].cpu().numpy(),
+                    np.fft.ifft2(fa * spec_nat[5].reshape(h, w)).reshape(-1))
+    t_ap = time_launches(torch, apply, steps, warmup, stream) / steps
+    del a, spec, filters, out
+    return {
+        "real_two_for_one_512x512": {
+            "gpixels_s": round(2 * nimg * np_img / t_r2 / 1e9, 3), "ms": round(t_r2 * 1e3, 5),
+            "images": 2 * nimg, "rel_l2": rel_r2,
+            "bytes_per_pixel": 24, "frac_24B": round(24.0 * 2 * nimg * np_img / t_r2 / 1e9 / HBM_PEAK_GBS, 4)},
+        "split_apply_512x512_x256": {
+            "gpoints_s": round(nf * np_img / t_ap / 1e9, 3), "ms": round(t_ap * 1e3, 5), "rel_l2": rel_ap,
+            "bytes_per_point": 32, "frac_32B": round(32.0 * nf * np_img / t_ap / 1e9 / HBM_PEAK_GBS, 4)},
+    }
 
 
 def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed):
@@ -350,6 +409,14 @@ def main():
                          "rel_l2": r}
     if large:
         line["large"] = large
+
+    if not args.no_2d:
+        d2 = bench_2d(torch, ff, dev, pts, args.sweep_steps, 3, stream, 11)
+        for k, v in d2.items():
+            if not v["rel_l2"] <= 2e-6:
+                print(json.dumps({"error": f"2D accuracy check failed ({k}): rel L2 {v['rel_l2']:.3e}"}))
+                sys.exit(1)
+        line["conv2d"] = d2
 
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)

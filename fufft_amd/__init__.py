@@ -72,6 +72,7 @@ def _load() -> C.CDLL:
         "fufft_large_digit_order": ([i64, C.POINTER(C.c_int32)], i32),
         "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
         "fufft_conv_large_f32": ([vp, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_plan2d": ([i64, i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
         "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, vp, vp], i32),
         "fufft_conv2d_f32": ([vp, vp, i64, vp, i64, i64, i64, i32, vp], i32),
         "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp], i32),
@@ -220,6 +221,48 @@ def conv_large(buf, filt, n: int, batch: int, filt_stride: int = 0, mid: str = "
     """Four-step conv of a batch of n-point signals, in place on buf."""
     check(lib.fufft_conv_large_f32(_ptr(buf), _ptr(filt), filt_stride, n, batch, MID[mid],
                                    _stream(stream)), "fufft_conv_large_f32")
+
+
+# ---- 2D ------------------------------------------------------------------------------------
+
+def plan2d(h: int, w: int) -> tuple[int, int]:
+    """(values per lane of the row plan, of the column plan)."""
+    vr, vc = C.c_int(), C.c_int()
+    check(lib.fufft_plan2d(h, w, C.byref(vr), C.byref(vc)), "fufft_plan2d")
+    return vr.value, vc.value
+
+
+def plan_filter2d(x: np.ndarray, h: int, w: int, kind: int = FILTER_SPECTRUM,
+                  fold_inv_n: bool = True) -> np.ndarray:
+    """2D filter as the column kernels read it: slot (r, c) = bin (rev_h(r), rev_w(c))."""
+    src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
+    assert src.size == h * w
+    out = np.empty(h * w, dtype=np.complex64)
+    check(lib.fufft_plan_filter2d_f32(h, w, kind, int(fold_inv_n), src.ctypes.data, out.ctypes.data),
+          "fufft_plan_filter2d_f32")
+    return out
+
+
+def conv2d(inp, filt, out, h: int, w: int, batch: int, filt_stride: int = 0, mid: str = "mul",
+           stream=None) -> None:
+    check(lib.fufft_conv2d_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), h, w, batch, MID[mid],
+                               _stream(stream)), "fufft_conv2d_f32")
+
+
+def conv2d_r2(x, y, filt, u, v, work, h: int, w: int, batch: int, filt_stride: int = 0,
+              stream=None) -> None:
+    check(lib.fufft_conv2d_r2_f32(_ptr(x), _ptr(y), _ptr(filt), filt_stride, _ptr(u), _ptr(v),
+                                  _ptr(work), h, w, batch, _stream(stream)), "fufft_conv2d_r2_f32")
+
+
+def fwd2d(inp, spec, h: int, w: int, batch: int, stream=None) -> None:
+    check(lib.fufft_fwd2d_f32(_ptr(inp), _ptr(spec), h, w, batch, _stream(stream)), "fufft_fwd2d_f32")
+
+
+def apply2d(spec, filt, out, h: int, w: int, batch: int, spec_stride: int = 0, filt_stride: int = 0,
+            mid: str = "mul", stream=None) -> None:
+    check(lib.fufft_apply2d_f32(_ptr(spec), spec_stride, _ptr(filt), filt_stride, _ptr(out), h, w,
+                                batch, MID[mid], _stream(stream)), "fufft_apply2d_f32")
 
 
 def bfp_exponent(absmax: float) -> int:

@@ -278,10 +278,36 @@ static int filter_count(int64_t filt_stride, int64_t n, int64_t batch, uint32_t*
    return FUFFT_ERR_INVALID;
 }
 
+// The kernels address a per-transform filter or spectrum array with 32-bit
+// byte offsets; a launch whose such array exceeds 4 GiB is split into chunks
+// of transforms (the per-transform arrays then advance with the chunk).
 static int run_conv1d(int kind, int n, int v, const Conv1dParams& p, void* stream)
 {
    if(p.ntrans == 0) return FUFFT_OK;
-   return status_of(launch_conv1d(kind, n, v, lds_layout(), p, static_cast<hipStream_t>(stream)));
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   const uint64_t bytes = (uint64_t)n * 8;
+   const bool big_f = (uint64_t)p.fcount * bytes > 0xffffffffull;
+   const bool big_s = (uint64_t)p.scount * bytes > 0xffffffffull;
+   if(!big_f && !big_s) return status_of(launch_conv1d(kind, n, v, lds_layout(), p, s));
+   if((big_f && p.fcount != p.ntrans) || (big_s && p.scount != p.ntrans)) return FUFFT_ERR_INVALID;
+   const bool real_in  = kind == K_CONV_R2 || kind == K_FWD_R2;
+   const bool real_out = kind == K_CONV_R2 || kind == K_APPLY_R2;
+   const uint32_t step = (uint32_t)(0xffffffffull / bytes) & ~255u;
+   for(uint32_t t0 = 0; t0 < p.ntrans; t0 += step) {
+      const uint32_t cnt = p.ntrans - t0 < step ? p.ntrans - t0 : step;
+      const size_t pts = (size_t)t0 * n;
+      Conv1dParams q = p;
+      q.ntrans = cnt;
+      if(p.in0)  q.in0  = static_cast<const char*>(p.in0) + pts * (real_in ? 4 : 8);
+      if(p.in1)  q.in1  = static_cast<const char*>(p.in1) + pts * 4;
+      if(p.out0) q.out0 = static_cast<char*>(p.out0) + pts * (real_out ? 4 : 8);
+      if(p.out1) q.out1 = static_cast<char*>(p.out1) + pts * 4;
+      if(p.fcount == p.ntrans && p.filt) { q.filt = static_cast<const char*>(p.filt) + pts * 8; q.fcount = cnt; }
+      if(p.scount == p.ntrans && p.spec) { q.spec = static_cast<const char*>(p.spec) + pts * 8; q.scount = cnt; }
+      const hipError_t e = launch_conv1d(kind, n, v, lds_layout(), q, s);
+      if(e != hipSuccess) return status_of(e);
+   }
+   return FUFFT_OK;
 }
 
 int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
@@ -373,7 +399,24 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
    if(batch == 0) return FUFFT_OK;
    p.qin = qin; p.ein = ein; p.filt = filt; p.qout = qout; p.eout = eout;
    p.ntrans = (uint32_t)batch; p.mid = mid; p.fl = layout;
-   return status_of(launch_bfp((int)n, v, lds_layout(), p, static_cast<hipStream_t>(stream)));
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   // per-signal filters beyond 4 GiB: chunks keep the 32-bit filter offsets in range
+   const uint64_t fbytes = (uint64_t)n * 8;
+   if((uint64_t)p.fcount * fbytes <= 0xffffffffull) return status_of(launch_bfp((int)n, v, lds_layout(), p, s));
+   const uint32_t step = (uint32_t)(0xffffffffull / fbytes) & ~255u;
+   for(uint32_t t0 = 0; t0 < p.ntrans; t0 += step) {
+      BfpParams q = p;
+      q.ntrans = p.ntrans - t0 < step ? p.ntrans - t0 : step;
+      q.fcount = q.ntrans;
+      q.qin  = static_cast<const char*>(p.qin) + (size_t)t0 * n * 4;
+      q.qout = static_cast<char*>(p.qout) + (size_t)t0 * n * 4;
+      q.ein  = p.ein + (size_t)t0 * (n / FUFFT_BFP_BLOCK);
+      q.eout = p.eout + (size_t)t0 * (n / FUFFT_BFP_BLOCK);
+      q.filt = static_cast<const char*>(p.filt) + (size_t)t0 * fbytes;
+      const hipError_t e = launch_bfp((int)n, v, lds_layout(), q, s);
+      if(e != hipSuccess) return status_of(e);
+   }
+   return FUFFT_OK;
 }
 
 // ---- BFP host codec -----------------------------------------------------------------
@@ -499,11 +542,218 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
    p.ntrans = (uint32_t)chunks;
    p.fcount = (uint32_t)(filt_stride == 0 ? n / mn : chunks);
    p.scount = 1; p.mid = mid; p.fl = FUFFT_LAYOUT_DR;
-   if((e = launch_conv1d(K_CONV, mn, v, lds_layout(), p, s)) != hipSuccess) return status_of(e);
+   if((st = run_conv1d(K_CONV, mn, v, p, stream)) != FUFFT_OK) return st;
    // inverse outer levels, smallest stride first
    for(int l = lout - 1; l >= 0 && e == hipSuccess; l--)
       e = launch_outer_pass(a, n, batch, n >> (4 * (l + 1)), true, p.tw, s);
    return status_of(e);
+}
+
+}  // extern "C"
+
+// ---- 2D ------------------------------------------------------------------------------
+// Rows use the 1D kernels at FUFFT_AUTO; columns the column kernels (conv2d.hip).
+
+extern "C" int fufft_plan2d(int64_t h, int64_t w, int* v_rows, int* v_cols)
+{
+   if(!v_rows || !v_cols) return FUFFT_ERR_INVALID;
+   if(!pow2(h) || !pow2(w) || h > 2048 || w > 16384) return FUFFT_ERR_UNSUPPORTED;
+   const int vr = values_per_lane(resolve_variant(w, FUFFT_AUTO));
+   const int vc = col_values_per_lane((int)h);
+   if(!vc || !vr || !conv1d_supported((int)w, vr)) return FUFFT_ERR_UNSUPPORTED;
+   *v_rows = vr;
+   *v_cols = vc;
+   return FUFFT_OK;
+}
+
+namespace {
+
+struct Plan2d {
+   int vr = 0, vc = 0, nr = 0, nc = 0;
+   int rr[64], rc[64];
+};
+
+int plan2d(int64_t h, int64_t w, Plan2d* p)
+{
+   const int st = fufft_plan2d(h, w, &p->vr, &p->vc);
+   if(st != FUFFT_OK) return st;
+   p->nr = factor(w, p->vr, p->rr);
+   p->nc = factor(h, p->vc, p->rc);
+   return FUFFT_OK;
+}
+
+int check_2d(int64_t h, int64_t w, int64_t batch, Plan2d* p)
+{
+   const int st = plan2d(h, w, p);
+   if(st != FUFFT_OK) return st;
+   if(batch < 0 || batch * h > 0xffffffffll) return FUFFT_ERR_INVALID;
+   return FUFFT_OK;
+}
+
+// the three launches of a 2D pass share this row-launch helper: n = w points
+// per row, h * batch rows
+Conv1dParams rows_params(const float2* tw, int64_t h, int64_t batch)
+{
+   Conv1dParams p{};
+   p.tw = tw;
+   p.ntrans = (uint32_t)(h * batch);
+   p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR;
+   return p;
+}
+
+ColParams col_params(const float2* tw, int64_t w, int64_t batch)
+{
+   ColParams c{};
+   c.tw = tw; c.nimg = (uint32_t)batch; c.fcount = 1; c.scount = 1; c.mid = FUFFT_MID_NONE;
+   c.w = (uint32_t)w;
+   return c;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind, int fold_inv_n,
+                            const float* in, float* out)
+{
+   Plan2d pl;
+   int st = plan2d(h, w, &pl);
+   if(st != FUFFT_OK) return st;
+   if(!in || !out) return FUFFT_ERR_INVALID;
+   if(filter_kind != FUFFT_FILTER_SPECTRUM && filter_kind != FUFFT_FILTER_TAPS) return FUFFT_ERR_INVALID;
+   const int64_t np = h * w;
+   std::vector<double> s(2 * (size_t)np);
+   for(int64_t i = 0; i < 2 * np; i++) s[i] = in[i];
+   if(filter_kind == FUFFT_FILTER_TAPS) {
+      std::vector<double> line(2 * (size_t)(h > w ? h : w));
+      for(int64_t r = 0; r < h; r++) {
+         line.assign(s.begin() + 2 * r * w, s.begin() + 2 * (r + 1) * w);
+         dft_f64(line, w, -1);
+         std::copy(line.begin(), line.begin() + 2 * w, s.begin() + 2 * r * w);
+      }
+      line.resize(2 * (size_t)h);
+      for(int64_t c = 0; c < w; c++) {
+         for(int64_t r = 0; r < h; r++) { line[2 * r] = s[2 * (r * w + c)]; line[2 * r + 1] = s[2 * (r * w + c) + 1]; }
+         dft_f64(line, h, -1);
+         for(int64_t r = 0; r < h; r++) { s[2 * (r * w + c)] = line[2 * r]; s[2 * (r * w + c) + 1] = line[2 * r + 1]; }
+      }
+   }
+   const double scale = fold_inv_n ? 1.0 / (double)np : 1.0;
+   for(int64_t r = 0; r < h; r++) {
+      const int64_t br = group_reverse((int32_t)r, pl.rc, pl.nc);
+      for(int64_t c = 0; c < w; c++) {
+         const int64_t bc = group_reverse((int32_t)c, pl.rr, pl.nr);
+         out[2 * (r * w + c)]     = (float)(s[2 * (br * w + bc)] * scale);
+         out[2 * (r * w + c) + 1] = (float)(s[2 * (br * w + bc) + 1] * scale);
+      }
+   }
+   return FUFFT_OK;
+}
+
+int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride, void* out,
+                     int64_t h, int64_t w, int64_t batch, int mid, void* stream)
+{
+   Plan2d pl;
+   int st = check_2d(h, w, batch, &pl);
+   if(st != FUFFT_OK) return st;
+   if(mid < FUFFT_MID_MUL || mid > FUFFT_MID_NONE) return FUFFT_ERR_INVALID;
+   if(!in || !out || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   if(filt_stride != 0 && filt_stride != h * w) return FUFFT_ERR_INVALID;
+   const float2* tw = nullptr;
+   if((st = current_table(&tw)) != FUFFT_OK) return st;
+   if(batch == 0) return FUFFT_OK;
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   // rows DIF into digit order (out), columns DIF -> mid -> DIT in place,
+   // rows DIT in place
+   Conv1dParams r = rows_params(tw, h, batch);
+   r.in0 = in; r.out0 = out;
+   if((st = run_conv1d(K_FWD, (int)w, pl.vr, r, stream)) != FUFFT_OK) return st;
+   ColParams c = col_params(tw, w, batch);
+   c.in = out; c.out = out; c.filt = filt; c.mid = mid;
+   c.fcount = (uint32_t)(filt_stride == 0 ? 1 : batch);
+   hipError_t e = launch_col(COL_CONV, (int)h, c, s);
+   if(e != hipSuccess) return status_of(e);
+   r = rows_params(tw, h, batch);
+   r.spec = out; r.scount = r.ntrans; r.out0 = out;
+   return run_conv1d(K_APPLY, (int)w, pl.vr, r, stream);
+}
+
+int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt, int64_t filt_stride,
+                        float* u, float* v, void* work, int64_t h, int64_t w, int64_t batch,
+                        void* stream)
+{
+   Plan2d pl;
+   int st = check_2d(h, w, batch, &pl);
+   if(st != FUFFT_OK) return st;
+   if(!x || !y || !filt || !u || !v || !work) return FUFFT_ERR_INVALID;
+   if(!aligned4(x) || !aligned4(y) || !aligned4(u) || !aligned4(v) || !aligned16(filt) ||
+      !aligned16(work))
+      return FUFFT_ERR_ALIGN;
+   if(filt_stride != 0 && filt_stride != h * w) return FUFFT_ERR_INVALID;
+   const float2* tw = nullptr;
+   if((st = current_table(&tw)) != FUFFT_OK) return st;
+   if(batch == 0) return FUFFT_OK;
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   // z = x + i y: rows DIF straight from the two real arrays into work
+   Conv1dParams r = rows_params(tw, h, batch);
+   r.in0 = x; r.in1 = y; r.out0 = work;
+   if((st = run_conv1d(K_FWD_R2, (int)w, pl.vr, r, stream)) != FUFFT_OK) return st;
+   ColParams c = col_params(tw, w, batch);
+   c.in = work; c.out = work; c.filt = filt; c.mid = FUFFT_MID_MUL;
+   c.fcount = (uint32_t)(filt_stride == 0 ? 1 : batch);
+   hipError_t e = launch_col(COL_CONV, (int)h, c, s);
+   if(e != hipSuccess) return status_of(e);
+   // rows DIT from work; Re -> u, Im -> v (a real filter keeps the two apart)
+   r = rows_params(tw, h, batch);
+   r.spec = work; r.scount = r.ntrans; r.out0 = u; r.out1 = v;
+   return run_conv1d(K_APPLY_R2, (int)w, pl.vr, r, stream);
+}
+
+int fufft_fwd2d_f32(const void* in, void* spec, int64_t h, int64_t w, int64_t batch, void* stream)
+{
+   Plan2d pl;
+   int st = check_2d(h, w, batch, &pl);
+   if(st != FUFFT_OK) return st;
+   if(!in || !spec) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(spec)) return FUFFT_ERR_ALIGN;
+   const float2* tw = nullptr;
+   if((st = current_table(&tw)) != FUFFT_OK) return st;
+   if(batch == 0) return FUFFT_OK;
+   Conv1dParams r = rows_params(tw, h, batch);
+   r.in0 = in; r.out0 = spec;
+   if((st = run_conv1d(K_FWD, (int)w, pl.vr, r, stream)) != FUFFT_OK) return st;
+   ColParams c = col_params(tw, w, batch);
+   c.in = spec; c.out = spec;
+   return status_of(launch_col(COL_FWD, (int)h, c, static_cast<hipStream_t>(stream)));
+}
+
+int fufft_apply2d_f32(const void* spec, int64_t spec_stride, const void* filt, int64_t filt_stride,
+                      void* out, int64_t h, int64_t w, int64_t batch, int mid, void* stream)
+{
+   Plan2d pl;
+   int st = check_2d(h, w, batch, &pl);
+   if(st != FUFFT_OK) return st;
+   if(mid < FUFFT_MID_MUL || mid > FUFFT_MID_NONE) return FUFFT_ERR_INVALID;
+   if(!spec || !out || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(!aligned16(spec) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   const int64_t np = h * w;
+   if((filt_stride != 0 && filt_stride != np) || (spec_stride != 0 && spec_stride != np))
+      return FUFFT_ERR_INVALID;
+   // a spectrum shared by the batch must not be overwritten by the first image
+   if(spec_stride == 0 && batch > 1 && spec == out) return FUFFT_ERR_INVALID;
+   const float2* tw = nullptr;
+   if((st = current_table(&tw)) != FUFFT_OK) return st;
+   if(batch == 0) return FUFFT_OK;
+   ColParams c = col_params(tw, w, batch);
+   c.spec = spec; c.out = out; c.filt = filt; c.mid = mid;
+   c.fcount = (uint32_t)(filt_stride == 0 ? 1 : batch);
+   c.scount = (uint32_t)(spec_stride == 0 ? 1 : batch);
+   hipError_t e = launch_col(COL_APPLY, (int)h, c, static_cast<hipStream_t>(stream));
+   if(e != hipSuccess) return status_of(e);
+   Conv1dParams r = rows_params(tw, h, batch);
+   r.spec = out; r.scount = r.ntrans; r.out0 = out;
+   return run_conv1d(K_APPLY, (int)w, pl.vr, r, stream);
 }
 
 }  // extern "C"

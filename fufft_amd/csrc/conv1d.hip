@@ -36,7 +36,14 @@ conv1d_kernel(const Conv1dParams p)
    constexpr int SLOT  = LD::size(N);
    constexpr int LANES = T < 64 ? 64 : T;
    constexpr int TPW   = T < 64 ? 64 / T : 1;     // transforms per wavefront
-   constexpr int EL    = (KIND == K_CONV_R2) ? 4 : 8;   // bytes per point in HBM
+   // bytes per point of the natural-order side in HBM: real pairs x / y (or
+   // u / v) travel as two separate float arrays
+   constexpr bool REAL_IN   = KIND == K_CONV_R2 || KIND == K_FWD_R2;
+   constexpr bool REAL_OUT  = KIND == K_CONV_R2 || KIND == K_APPLY_R2;
+   constexpr bool FROM_SPEC = KIND == K_APPLY || KIND == K_APPLY_R2;
+   constexpr bool TO_SPEC   = KIND == K_FWD || KIND == K_FWD_R2;
+   constexpr int  EL_IN     = REAL_IN ? 4 : 8;
+   constexpr int  EL_OUT    = REAL_OUT ? 4 : 8;
 
    extern __shared__ float2 lds[];
    const int slot = threadIdx.x / T;
@@ -47,16 +54,14 @@ conv1d_kernel(const Conv1dParams p)
    // the wavefront's first transform (uniform) and this lane's offset from it
    const uint32_t t0 = (T >= 64) ? (uint32_t)uniform((int)t)
                                  : blockIdx.x * CPB + (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
-   const uint32_t lane_off = ((t - t0) * N + L) * EL;
-   const size_t   wbase    = (size_t)t0 * N * EL;
-   constexpr uint32_t WBYTES = TPW * N * EL;
+   const uint32_t lane_pos = (t - t0) * N + L;
 
    float2* A = lds + slot * SLOT;
    Twiddles<PL> tw;
    tw.load(p.tw, L);
    float2 r[V];
 
-   if constexpr(KIND == K_APPLY) {
+   if constexpr(FROM_SPEC) {
       // spectrum positions L*V .. L*V+V-1, two complex per 16-byte load
       const Buf sb(p.spec, p.scount * (uint32_t)N * 8u);
       const uint32_t so = ((t % p.scount) * N + L * V) * 8u;
@@ -67,21 +72,24 @@ conv1d_kernel(const Conv1dParams p)
          r[2 * m + 1] = make_float2(q.z, q.w);
       }
    } else {
-      if constexpr(KIND == K_CONV_R2) {
-         const Buf xb(static_cast<const char*>(p.in0) + wbase, WBYTES);
-         const Buf yb(static_cast<const char*>(p.in1) + wbase, WBYTES);
+      const size_t wb = (size_t)t0 * N * EL_IN;
+      constexpr uint32_t WB = TPW * N * EL_IN;
+      if constexpr(REAL_IN) {
+         const Buf xb(static_cast<const char*>(p.in0) + wb, WB);
+         const Buf yb(static_cast<const char*>(p.in1) + wb, WB);
 #pragma unroll
-         for(int q = 0; q < V; q++) r[q] = make_float2(xb.ld1(lane_off, q * T * 4), yb.ld1(lane_off, q * T * 4));
+         for(int q = 0; q < V; q++)
+            r[q] = make_float2(xb.ld1(lane_pos * 4u, q * T * 4), yb.ld1(lane_pos * 4u, q * T * 4));
       } else {
-         const Buf xb(static_cast<const char*>(p.in0) + wbase, WBYTES);
+         const Buf xb(static_cast<const char*>(p.in0) + wb, WB);
 #pragma unroll
-         for(int q = 0; q < V; q++) r[q] = xb.ld2(lane_off, q * T * 8);
+         for(int q = 0; q < V; q++) r[q] = xb.ld2(lane_pos * 8u, q * T * 8);
       }
       forward_dif<PL, LD, LANES>(r, A, L, tw);
    }
 
-   if constexpr(KIND == K_FWD) {
-      const Buf ob(static_cast<char*>(p.out0) + wbase, WBYTES);
+   if constexpr(TO_SPEC) {
+      const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
       const uint32_t so = ((t - t0) * N + L * V) * 8u;
 #pragma unroll
       for(int m = 0; m < V / 2; m++)
@@ -95,15 +103,20 @@ conv1d_kernel(const Conv1dParams p)
       }
       inverse_dit<PL, LD, LANES>(r, A, L, tw);
 
-      if constexpr(KIND == K_CONV_R2) {
-         const Buf ub(static_cast<char*>(p.out0) + wbase, WBYTES);
-         const Buf vb(static_cast<char*>(p.out1) + wbase, WBYTES);
+      const size_t wb = (size_t)t0 * N * EL_OUT;
+      constexpr uint32_t WB = TPW * N * EL_OUT;
+      if constexpr(REAL_OUT) {
+         const Buf ub(static_cast<char*>(p.out0) + wb, WB);
+         const Buf vb(static_cast<char*>(p.out1) + wb, WB);
 #pragma unroll
-         for(int q = 0; q < V; q++) { ub.st1(r[q].x, lane_off, q * T * 4); vb.st1(r[q].y, lane_off, q * T * 4); }
+         for(int q = 0; q < V; q++) {
+            ub.st1(r[q].x, lane_pos * 4u, q * T * 4);
+            vb.st1(r[q].y, lane_pos * 4u, q * T * 4);
+         }
       } else {
-         const Buf ob(static_cast<char*>(p.out0) + wbase, WBYTES);
+         const Buf ob(static_cast<char*>(p.out0) + wb, WB);
 #pragma unroll
-         for(int q = 0; q < V; q++) ob.st2(r[q], lane_off, q * T * 8);
+         for(int q = 0; q < V; q++) ob.st2(r[q], lane_pos * 8u, q * T * 8);
       }
    }
 }
@@ -266,6 +279,11 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
       case K_CONV_R2: return launch_one<N, V, LAYOUT, K_CONV_R2, MID_MUL>(p, s);
       case K_FWD:     return launch_one<N, V, LAYOUT, K_FWD, MID_NONE>(p, s);
       case K_APPLY:   return launch_mid<N, V, LAYOUT, K_APPLY>(p, s);
+      case K_FWD_R2:  return launch_one<N, V, LAYOUT, K_FWD_R2, MID_NONE>(p, s);
+      case K_APPLY_R2:
+         // only the 2D two-for-one path uses it, as the row inverse
+         return p.mid == MID_NONE ? launch_one<N, V, LAYOUT, K_APPLY_R2, MID_NONE>(p, s)
+                                  : hipErrorInvalidValue;
       default:        return hipErrorInvalidValue;
    }
 }

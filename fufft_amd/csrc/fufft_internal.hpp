@@ -8,7 +8,9 @@
 namespace fufft {
 
 // ---- 1D fused pipeline (conv1d.hip) ------------------------------------------------
-enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3 };
+// K_FWD_R2 / K_APPLY_R2: the forward half reading two real arrays, the
+// inverse half writing two real arrays (2D two-for-one rows)
+enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5 };
 
 struct Conv1dParams {
    const void*   in0;      // complex input, or real x (K_CONV_R2)
@@ -53,17 +55,19 @@ hipError_t launch_outer_pass(float2* buf, int64_t n, int64_t batch, int64_t M, b
 
 // ---- 2D column kernels (conv2d.hip) -------------------------------------------------
 struct ColParams {
-   const void*   in;       // h x w complex images (rows contiguous)
+   const void*   in;       // h x w complex images, rows contiguous (COL_CONV, COL_FWD)
+   const void*   spec;     // 2D digit-order spectra (COL_APPLY)
    void*         out;
-   const void*   filt;     // 2D filter, digit order per dimension
+   const void*   filt;     // 2D filter, slot (r, c) = bin (rev_h(r), rev_w(c))
    const float2* tw;
-   uint32_t      nimg;
-   uint32_t      fcount;
+   uint32_t      nimg;     // images in the launch
+   uint32_t      fcount;   // image i uses filter (i % fcount)
+   uint32_t      scount;   // image i uses spectrum (i % scount)
    int32_t       mid;
-   int32_t       w;        // row length
+   uint32_t      w;        // row length
 };
 enum { COL_CONV = 0, COL_FWD = 1, COL_APPLY = 2 };
-bool       col_supported(int h, int w);
+int        col_values_per_lane(int h);      // 0 if h is not a supported column length
 hipError_t launch_col(int kind, int h, const ColParams& p, hipStream_t s);
 
 }  // namespace fufft

@@ -162,6 +162,12 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
  * filter slot (r, c) holds spectrum bin (mixedrev_h(r), mixedrev_w(c)).
  * Runs as three launches in place on out: row forward, fused column conv,
  * row inverse (7 HBM passes for an image too large for one workgroup). */
+/* Values per lane of the row plan (the 1D kernel at FUFFT_AUTO for length w)
+ * and of the column plan (8 up to h = 512, 16 for h = 1024, 2048); the
+ * per-dimension digit orders are those of fufft_digit_order with that many
+ * values per lane.  No reference counterpart (the reference fixes both
+ * dimensions at compile time, fufft.cuh:1209-1214). */
+int fufft_plan2d(int64_t h, int64_t w, int* v_rows, int* v_cols);
 int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind,
                             int fold_inv_n, const float* in, float* out);
 int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride,

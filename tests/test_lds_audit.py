@@ -109,3 +109,24 @@ def test_reference_swizzle_conflicts_on_gfx950():
     n, v = 4096, 16
     worst = max(degree([swz16(p) for p in pos]) for _, pos in lane_sets(n, v))
     assert worst > 1
+
+
+# column kernels (conv2d.hip): C columns side by side, thread = (L, col) with
+# the column fastest, per-column slot skewed by 32 / C float2
+COLS = [(256, 8, 16), (512, 8, 16), (1024, 16, 16), (2048, 16, 8)]
+
+
+@pytest.mark.parametrize("h,v,c", COLS)
+def test_column_tiles_conflict_free(h, v, c):
+    T = h // v
+    slotc = h + h // v + 32 // c
+    for (R, M) in plan(h, v):
+        for g, k in itertools.product(range(v // R), range(R)):
+            addrs = [(tid % c) * slotc + phys_pad(tap_pos(tid // c, g, k, R, M, T), v)
+                     for tid in range(c * T)]
+            for w0 in range(0, len(addrs), 64):
+                assert degree(addrs[w0:w0 + 64]) == 1, (h, v, c, R, M, g, k)
+    # without the skew the C columns of a half-wavefront share banks
+    addrs = [(tid % c) * (h + h // v) + phys_pad(tap_pos(tid // c, 0, 0, *plan(h, v)[0], T), v)
+             for tid in range(64)]
+    assert degree(addrs) > 1
