@@ -1,0 +1,145 @@
+"""CPU tests of the HIP library's host side (no GPU calls).
+
+- every function include/fufft/fufft.h declares is exported by libfufft_amd.so;
+- host planning (radices, digit orders, filter planning in 1D, four-step and
+  2D) agrees with the oracle's plans;
+- the twiddle table the library uploads equals the oracle's table entry for
+  entry, bit for bit;
+- the BFP host codec equals the oracle's;
+- argument errors come back as status codes before any HIP call.
+"""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from conftest import crandn
+from oracle import oracle as O
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def header_functions():
+    text = (ROOT / "include" / "fufft" / "fufft.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fufft_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    import fufft_amd as ff
+    names = header_functions()
+    assert len(names) >= 25
+    missing = [n for n in names if not hasattr(ff.lib, n)]
+    assert not missing, missing
+
+
+@pytest.mark.parametrize("variant,v", [("v16", 16), ("r8", 8)])
+@pytest.mark.parametrize("n", [256, 512, 1024, 2048, 4096, 8192, 16384])
+def test_plan_and_digit_order_match_oracle(variant, v, n):
+    import fufft_amd as ff
+    plan = O.kernel_plan(n, v)
+    assert ff.plan_radices(n, variant) == plan.radices
+    assert np.array_equal(ff.digit_order(n, variant), O.mixedrev(plan))
+
+
+def test_auto_variant_rule():
+    import fufft_amd as ff
+    for n in [256, 512, 4096, 8192, 16384]:
+        want = "r8" if 512 <= n <= 8192 else "v16"
+        assert ff.resolve_variant(n, "auto") == want
+        assert ff.plan_radices(n, "auto") == ff.plan_radices(n, want)
+
+
+@pytest.mark.parametrize("n", [8192, 32768, 65536, 131072])
+def test_large_plan_matches_oracle(n):
+    import fufft_amd as ff
+    lout, mid = ff.large_plan(n)
+    assert 16 ** lout * mid == n and 512 <= mid <= 4096
+    assert np.array_equal(ff.large_digit_order(n), O.mixedrev(O.large_plan(lout, mid, 8)))
+
+
+def test_filter_planning_1d_layouts(rng):
+    import fufft_amd as ff
+    n, v = 2048, 8
+    taps = crandn(rng, n)
+    want = np.fft.fft(taps.astype(np.complex128)) / n
+    dr = ff.plan_filter(taps, n, variant="r8", kind=ff.FILTER_TAPS)
+    perm = O.mixedrev(O.kernel_plan(n, v))
+    assert np.max(np.abs(dr - want[perm])) <= 2e-7 * np.max(np.abs(want))
+    # the spectrum form skips the host DFT: slot i is the fp32 bin perm[i] / n
+    spec = (want * n).astype(np.complex64)
+    dr2 = ff.plan_filter(spec, n, variant="r8", kind=ff.FILTER_SPECTRUM)
+    assert np.array_equal(dr2, (spec.astype(np.complex128) / n).astype(np.complex64)[perm])
+    lane = ff.plan_filter(spec, n, variant="r8", layout="lane", kind=ff.FILTER_SPECTRUM)
+    t = n // v
+    assert np.array_equal(lane, dr2.reshape(t, v).T.reshape(-1))
+
+
+def test_filter_planning_large_and_2d(rng):
+    import fufft_amd as ff
+    n = 32768
+    taps = crandn(rng, n)
+    want = np.fft.fft(taps.astype(np.complex128)) / n
+    got = ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS)
+    assert np.max(np.abs(got - want[ff.large_digit_order(n)])) <= 2e-7 * np.max(np.abs(want))
+    h, w = 256, 1024
+    taps2 = crandn(rng, h * w)
+    vr, vc = ff.plan2d(h, w)
+    S = np.fft.fft2(taps2.reshape(h, w).astype(np.complex128)) / (h * w)
+    rh, rw = O.mixedrev(O.kernel_plan(h, vc)), O.mixedrev(O.kernel_plan(w, vr))
+    got2 = ff.plan_filter2d(taps2, h, w, kind=ff.FILTER_TAPS)
+    want2 = S[np.ix_(rh, rw)].reshape(-1)
+    assert np.max(np.abs(got2 - want2)) <= 2e-7 * np.max(np.abs(want2))
+
+
+def test_twiddle_table_matches_oracle_bitwise():
+    import fufft_amd as ff
+    log_max = 13
+    tab = ff.twiddle_table_host(log_max).view(np.float32).reshape(-1, 2)
+    c, s = C.c_float(), C.c_float()
+    for p in range(1, log_max + 1):
+        P = 1 << p
+        js = range(P) if P <= 1024 else list(range(0, P, 7)) + [P - 1]
+        for j in js:
+            O.lib.or_twiddle(O.TW_TABLE, +1, P, j, C.byref(c), C.byref(s))
+            assert tab[P + j, 0] == np.float32(c.value) and tab[P + j, 1] == np.float32(s.value), (P, j)
+
+
+def test_bfp_codec_matches_oracle(rng):
+    import fufft_amd as ff
+    vals = [0.0, 1e-45, 1.17e-38, 1.0, 32767.0, 32767.5, 32768.0, 65534.0, 65535.0, 3.4e38]
+    for m in vals + list(np.abs(rng.standard_normal(200) * 10.0 ** rng.uniform(-30, 30, 200))):
+        x = float(np.float32(m))
+        assert ff.bfp_exponent(x) == O.bfp_exponent(x), x
+    x = (crandn(rng, 64 * 40) * 10.0 ** rng.uniform(-3, 3)).astype(np.complex64)
+    x[:64] = 0
+    q, e = ff.bfp_quantize(x)
+    oq, oe = O.bfp_quantize(x)
+    assert np.array_equal(q, oq) and np.array_equal(e, oe)
+    assert np.array_equal(ff.bfp_dequantize(q, e), O.bfp_dequantize(oq, oe))
+
+
+def test_status_codes_without_gpu_calls():
+    """Size, pointer and alignment checks precede every HIP call."""
+    import fufft_amd as ff
+    L = ff.lib
+    fake = 1 << 20                              # never dereferenced: the checks fail first
+    assert L.fufft_conv_f32(fake, fake, 0, fake, 1000, 1, 0, 2, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, 1, 7, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_f32(None, fake, 0, fake, 4096, 1, 0, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_f32(fake + 8, fake, 0, fake, 4096, 1, 0, 2, 0, None) == ff.ERR_ALIGN
+    assert L.fufft_conv_f32(fake, fake, 17, fake, 4096, 1, 0, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, -1, 0, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, 1, 0, 9, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 256, 1, 0, 1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_large_f32(fake, fake, 0, 4096, 1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_large_f32(fake, fake, 3, 32768, 1, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 128, 512, 1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 100, 1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv2d_f32(fake, fake, 5, fake, 512, 512, 1, 0, None) == ff.ERR_INVALID
+    assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake, 512, 512, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_bfp_quantize(None, 64, None, None) == ff.ERR_INVALID
+    assert L.fufft_bfp_quantize(fake, 65, fake, fake) == ff.ERR_INVALID
+    assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("pointer")
