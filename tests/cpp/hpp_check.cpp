@@ -1,0 +1,26 @@
+// Host-only check of the C++ mirror header: planning calls and status codes
+// (no device work).  Built and run by tests/test_library_cpu.py.
+#include "fufft/fufft.hpp"
+
+#include <cstdio>
+
+int main()
+{
+   const int64_t n = 4096;
+   std::vector<float> taps(2 * n, 0.0f), filt(2 * n);
+   taps[0] = 1.0f;                                  // delta taps: flat spectrum 1/n
+   if(fufft::plan_filter(taps.data(), filt.data(), n) != FUFFT_OK) return 1;
+   for(int64_t i = 0; i < n; i++)
+      if(filt[2 * i] != 1.0f / n || filt[2 * i + 1] != 0.0f) return 2;
+   const std::vector<int32_t> perm = fufft::digit_order(n);
+   std::vector<int> seen(n, 0);
+   for(int32_t p : perm) seen[p]++;
+   for(int s : seen) if(s != 1) return 3;          // a permutation
+   // argument errors come back before any device call
+   if(fufft::pipeline<fufft::MidConjMultiply>(nullptr, nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID) return 4;
+   if(fufft::pipeline<fufft::MidMultiply>(nullptr, nullptr, nullptr, 1000, 1) != FUFFT_ERR_UNSUPPORTED) return 5;
+   if(fufft::conv_large<fufft::MidNothing>(nullptr, nullptr, 1024, 1) != FUFFT_ERR_UNSUPPORTED) return 6;
+   if(!fufft::supported(n) || fufft::supported(100)) return 7;
+   std::printf("ok %s\n", fufft::status_string(FUFFT_OK));
+   return 0;
+}

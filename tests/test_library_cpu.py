@@ -143,3 +143,19 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_bfp_quantize(None, 64, None, None) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(fake, 65, fake, fake) == ff.ERR_INVALID
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("pointer")
+
+
+def test_cpp_mirror_header_builds_and_runs(tmp_path):
+    """include/fufft/fufft.hpp compiles with g++ and links against the library."""
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    lib_dir = ROOT / "fufft_amd"
+    exe = tmp_path / "hpp_check"
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", f"-I{ROOT / 'include'}",
+                    str(ROOT / "tests" / "cpp" / "hpp_check.cpp"), f"-L{lib_dir}", "-lfufft_amd",
+                    f"-Wl,-rpath,{lib_dir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, (out.returncode, out.stderr)
+    assert out.stdout.startswith("ok")
