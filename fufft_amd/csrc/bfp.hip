@@ -12,9 +12,10 @@
 // Mapping: a transform has T = N/V >= 64 lanes, and register q of a wavefront
 // holds the 64 consecutive points 64*w + q*T .. (w = wavefront index within
 // the transform), i.e. exactly one block.  So input exponents are uniform per
-// (wavefront, register) and each output block's abs-max is one reduction across
-// the wavefront -- no LDS pass and no workgroup barrier for the scale, unlike
-// the reference's shared-memory atomicMax rendezvous (fufft.cuh:1674-1692).
+// (wavefront, register), and the V output blocks' abs-maxima come from one
+// transposed cross-lane reduction of the wavefront's V registers -- no LDS pass
+// and no workgroup barrier for the scale, unlike the reference's shared-memory
+// atomicMax rendezvous (fufft.cuh:1674-1692).
 #include "fufft_device.hpp"
 #include "fufft_plan.hpp"
 #include "fufft_internal.hpp"
@@ -34,26 +35,69 @@ __device__ __forceinline__ int bfp_exponent_bits(uint32_t bits)
    return xb == 0 ? -128 : e;
 }
 
+// ---- block maxima across a wavefront ------------------------------------------------
+// The V registers of a wavefront are V blocks; their maxima are found with one
+// transposed reduction instead of V full-wave reductions.  Values are the bits
+// of non-negative floats, so unsigned compares order them exactly and the DPP
+// lane moves fold into v_max_u32_dpp.
+
 template<int CTRL>
-__device__ __forceinline__ float dpp_mov(float v)
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v)
 {
-   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
 }
 
-// max over the 64 lanes of a wavefront, result uniform
-__device__ __forceinline__ float wave_max(float x)
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// partner lane for level S: xor 1, xor 2 (quad_perm), then rotations by 4 and
+// 8 within a row of 16.  A rotation by 4 is not an involution, but the partner
+// always has the opposite bit 2 and the same bits 0-1, and the rotation by 8
+// that follows joins the remaining quads, so every lane still sees all 16.
+template<int S>
+__device__ __forceinline__ uint32_t level_partner(uint32_t v)
 {
-   // DPP controls: quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror
-   x = __builtin_fmaxf(x, dpp_mov<0xB1>(x));
-   x = __builtin_fmaxf(x, dpp_mov<0x4E>(x));
-   x = __builtin_fmaxf(x, dpp_mov<0x141>(x));
-   x = __builtin_fmaxf(x, dpp_mov<0x140>(x));
-   const int xi = __builtin_bit_cast(int, x);
-   const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 0));
-   const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 16));
-   const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 32));
-   const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(xi, 48));
-   return __builtin_fmaxf(__builtin_fmaxf(a, b), __builtin_fmaxf(c, d));
+   if constexpr(S == 0)      return dpp_u<0xB1>(v);    // quad_perm [1,0,3,2]
+   else if constexpr(S == 1) return dpp_u<0x4E>(v);    // quad_perm [2,3,0,1]
+   else if constexpr(S == 2) return dpp_u<0x124>(v);   // row_ror:4
+   else                      return dpp_u<0x128>(v);   // row_ror:8 (= xor 8)
+}
+
+__device__ __forceinline__ uint32_t swap_max16(uint32_t v)
+{
+   const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);   // rows 0<->1, 2<->3
+   return umax(r[0], r[1]);
+}
+
+__device__ __forceinline__ uint32_t swap_max32(uint32_t v)
+{
+   const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);   // halves swapped
+   return umax(r[0], r[1]);
+}
+
+// On return lane l holds the wavefront maximum of m[l % V].  Level s halves
+// the register count: lanes with bit s clear keep the even register of each
+// pair and receive their partner's even register; lanes with bit s set keep
+// and receive the odd one.  The lane bits left over after log2(V) levels
+// reduce plainly.
+template<int V>
+__device__ __forceinline__ uint32_t block_maxima(uint32_t (&m)[V], uint32_t lane)
+{
+   constexpr int LOGV = V == 16 ? 4 : 3;
+   static_assert(V == 8 || V == 16, "one register per block level");
+   static_for<LOGV>([&](auto si) {
+      constexpr int S = decltype(si)::value;
+      constexpr int K = V >> S;
+      const bool hi = (lane >> S) & 1u;
+#pragma unroll
+      for(int i = 0; i < K / 2; i++) {
+         const uint32_t keep = hi ? m[2 * i + 1] : m[2 * i];
+         const uint32_t send = hi ? m[2 * i] : m[2 * i + 1];
+         m[i] = umax(keep, level_partner<S>(send));
+      }
+   });
+   uint32_t x = m[0];
+   if constexpr(LOGV == 3) x = umax(x, dpp_u<0x128>(x));
+   return swap_max32(swap_max16(x));
 }
 
 template<int N, int V, int LAYOUT, int MID>
@@ -105,17 +149,27 @@ bfp_kernel(const BfpParams p)
    inverse_dit<PL, LD, (T < 64 ? 64 : T)>(r, A, L, tw);
 
    // quantise: register q of this wavefront is block w + q*T/64
+   uint32_t m[V];
+#pragma unroll
+   for(int q = 0; q < V; q++)
+      m[q] = __builtin_bit_cast(uint32_t, __builtin_fmaxf(__builtin_fabsf(r[q].x), __builtin_fabsf(r[q].y)));
+   const int e_lane = bfp_exponent_bits(block_maxima<V>(m, (uint32_t)lane));   // block lane % V
    const Buf ob(static_cast<char*>(p.qout) + (size_t)tu * N * 4, N * 4);
-   const Buf xb(p.eout + (size_t)tu * NB, NB);
 #pragma unroll
    for(int q = 0; q < V; q++) {
-      const float m = wave_max(__builtin_fmaxf(__builtin_fabsf(r[q].x), __builtin_fabsf(r[q].y)));
-      const int e = uniform(bfp_exponent_bits(__builtin_bit_cast(uint32_t, m)));
-      const int qr = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(r[q].x, -e));
-      const int qi = (int)__builtin_rintf(__builtin_amdgcn_ldexpf(r[q].y, -e));
-      ob.stu(((uint32_t)qr & 0xffffu) | ((uint32_t)qi << 16), (uint32_t)L * 4u, q * T * 4);
-      if(lane == 0)
-         __builtin_amdgcn_raw_buffer_store_b8((unsigned char)e, xb.r, (uint32_t)(w + q * (T / 64)), 0, 0);
+      const int e = __builtin_amdgcn_readlane(e_lane, q);
+      // adding 1.5 * 2^23 rounds |v| < 2^22 to the nearest integer, ties to
+      // even (= rint), and leaves it in the low mantissa bits
+      const float yr = __builtin_amdgcn_ldexpf(r[q].x, -e) + 12582912.0f;
+      const float yi = __builtin_amdgcn_ldexpf(r[q].y, -e) + 12582912.0f;
+      // low halfwords of yr (bytes 0-1) and yi (bytes 4-5 of {yi, yr}) -> {im, re}
+      const uint32_t word = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, yi),
+                                                  __builtin_bit_cast(uint32_t, yr), 0x05040100u);
+      ob.stu(word, (uint32_t)L * 4u, q * T * 4);
+   }
+   if(lane < V) {
+      const Buf xb(p.eout + (size_t)tu * NB, NB);
+      __builtin_amdgcn_raw_buffer_store_b8((unsigned char)e_lane, xb.r, (uint32_t)(w + lane * (T / 64)), 0, 0);
    }
 }
 
