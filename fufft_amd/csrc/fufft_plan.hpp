@@ -197,14 +197,39 @@ __device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<
    });
 }
 
+// Synchronisation of the exchange between pass P and pass P + 1.  WL is the
+// number of consecutive lanes of one transform inside a wavefront (64, or T
+// when a wavefront holds whole transforms, or 64/C for the column kernels).
+// With one group per lane, pass P's lane L owns the positions
+// (L / M) * R * M + (L % M) + k * M; when M <= WL the lane bits that pick the
+// wavefront only reach the (L / M) part, so every wavefront owns one
+// contiguous region of R * WL positions in pass P and in pass P + 1 alike and
+// the exchange never leaves the wavefront: a wavefront fence suffices, and
+// only exchanges across wavefronts need the workgroup barrier.  (Within a
+// pass a lane writes back exactly the positions it read, so gather -> scatter
+// of one pass needs no synchronisation at all.)
+template<class PL, int P, int WL>
+constexpr bool exchange_in_wave()
+{
+   if constexpr(PL::T <= WL) return true;
+   else return PL::stride(P) <= WL && PL::V / PL::radix(P) == 1 && PL::V / PL::radix(P + 1) == 1;
+}
+
+template<class PL, int P, int LANES, int WL>
+__device__ __forceinline__ void exchange_sync()
+{
+   if constexpr(exchange_in_wave<PL, P, WL>()) pass_barrier<64>();
+   else                                        pass_barrier<LANES>();
+}
+
 // Forward DIF of the lane's registers: r holds positions L + q*T on entry and
 // the digit-order spectrum positions L*V + k on exit (last pass at M = 1).
-template<class PL, class LD, int LANES>
+template<class PL, class LD, int LANES, int WL = 64>
 __device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
 {
    static_for<PL::NP>([&](auto pi) {
       constexpr int p = decltype(pi)::value;
-      if constexpr(p > 0) { pass_barrier<LANES>(); lds_gather<PL, p, LD>(r, A, L); }
+      if constexpr(p > 0) { exchange_sync<PL, p - 1, LANES, WL>(); lds_gather<PL, p, LD>(r, A, L); }
       compute_pass<PL, p, -1, false>(r, tw);
       if constexpr(p < PL::NP - 1) lds_scatter<PL, p, LD>(r, A, L);
    });
@@ -212,14 +237,14 @@ __device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L
 
 // Inverse DIT: r holds spectrum positions L*V + k on entry and natural-order
 // positions L + q*T on exit.
-template<class PL, class LD, int LANES>
+template<class PL, class LD, int LANES, int WL = 64>
 __device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
 {
    static_for<PL::NP>([&](auto qi) {
       constexpr int p = PL::NP - 1 - decltype(qi)::value;
       if constexpr(p < PL::NP - 1) lds_gather<PL, p, LD>(r, A, L);
       compute_pass<PL, p, +1, true>(r, tw);
-      if constexpr(p > 0) { lds_scatter<PL, p, LD>(r, A, L); pass_barrier<LANES>(); }
+      if constexpr(p > 0) { lds_scatter<PL, p, LD>(r, A, L); exchange_sync<PL, p - 1, LANES, WL>(); }
    });
 }
 

@@ -130,3 +130,49 @@ def test_column_tiles_conflict_free(h, v, c):
     addrs = [(tid % c) * (h + h // v) + phys_pad(tap_pos(tid // c, 0, 0, *plan(h, v)[0], T), v)
              for tid in range(64)]
     assert degree(addrs) > 1
+
+
+# exchange_in_wave (fufft_plan.hpp): the exchange between pass p and p + 1 may
+# use a wavefront fence instead of the workgroup barrier.  Brute force: every
+# position a lane writes in pass p is read in pass p + 1 by a lane of the same
+# wavefront (and, for WAR, every position a wavefront reads in pass p + 1 was
+# written by that wavefront), whenever the predicate says so.
+def exchange_in_wave(n, v, p, wl):
+    T = n // v
+    rads = plan(n, v)
+    if T <= wl:
+        return True
+    (R, M), (R2, _) = rads[p], rads[p + 1]
+    return M <= wl and v // R == 1 and v // R2 == 1
+
+
+def owners(n, v, p):
+    T = n // v
+    R, M = plan(n, v)[p]
+    own = {}
+    for L in range(T):
+        for g in range(v // R):
+            for k in range(R):
+                own[tap_pos(L, g, k, R, M, T)] = L
+    return own
+
+
+WAVE_CASES = [(16, n, 64) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + \
+             [(8, n, 64) for n in (512, 1024, 2048, 4096, 8192)] + \
+             [(8, 256, 4), (8, 512, 4), (16, 1024, 4), (16, 2048, 8)]
+
+
+@pytest.mark.parametrize("v,n,wl", WAVE_CASES)
+def test_wave_local_exchanges(v, n, wl):
+    rads = plan(n, v)
+    local = 0
+    for p in range(len(rads) - 1):
+        if not exchange_in_wave(n, v, p, wl):
+            continue
+        local += 1
+        a, b = owners(n, v, p), owners(n, v, p + 1)
+        for pos, L in a.items():
+            assert b[pos] // wl == L // wl, (n, v, wl, p, pos)
+    # the plans that matter do drop barriers: R8 4096 keeps 1 of 3 per direction
+    if (v, n, wl) == (8, 4096, 64):
+        assert local == 2
