@@ -58,6 +58,7 @@ def _load() -> C.CDLL:
         "fufft_supported": ([i64, i32], i32),
         "fufft_plan_radices": ([i64, i32, C.POINTER(C.c_int)], i32),
         "fufft_digit_order": ([i64, i32, C.POINTER(C.c_int32)], i32),
+        "fufft_plan_chains": ([i64, i32, C.POINTER(C.c_int)], i32),
         "fufft_plan_filter_f32": ([i64, i32, i32, i32, i32, vp, vp], i32),
         "fufft_twiddle_table_host": ([i32, vp], i32),
         "fufft_conv_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp], i32),
@@ -129,6 +130,15 @@ def plan_radices(n: int, variant: str = "v16") -> list[int]:
     np_ = lib.fufft_plan_radices(n, VARIANT[variant], buf)
     if np_ < 0:
         raise FufftError(np_, "fufft_plan_radices")
+    return list(buf[:np_])
+
+
+def plan_chains(n: int, variant: str = "v16") -> list[int]:
+    """Per pass: 0 single twiddle chain, 1 radix-16 even/odd chains."""
+    buf = (C.c_int * 64)()
+    np_ = lib.fufft_plan_chains(n, VARIANT[variant], buf)
+    if np_ < 0:
+        raise FufftError(np_, "fufft_plan_chains")
     return list(buf[:np_])
 
 

@@ -259,15 +259,26 @@ enum { FLT_DR = 0, FLT_LANE = 1 };
 // The lane's V filter values sit at byte offsets voff + k*kstep of the filter
 // buffer.  MID is a template parameter: a runtime branch between the two
 // products makes the compiler keep both results live across the join.
+// With kstep == 8 (the digit-order layout) the V values are contiguous and
+// are read two per 16-byte load, halving the vector-memory instructions.
 template<class PL, int MID>
 __device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t kstep)
 {
    if constexpr(MID != MID_NONE) {
+      float2 b[PL::V];
+      if(kstep == 8u) {
 #pragma unroll
-      for(int k = 0; k < PL::V; k++) {
-         const float2 b = f.ld2(voff, k * kstep);
-         r[k] = (MID == MID_MUL) ? cmul(r[k], b) : cmul_conj(r[k], b);
+         for(int m = 0; m < PL::V / 2; m++) {
+            const float4 q = f.ld4(voff, m * 16);
+            b[2 * m] = make_float2(q.x, q.y);
+            b[2 * m + 1] = make_float2(q.z, q.w);
+         }
+      } else {
+#pragma unroll
+         for(int k = 0; k < PL::V; k++) b[k] = f.ld2(voff, k * kstep);
       }
+#pragma unroll
+      for(int k = 0; k < PL::V; k++) r[k] = (MID == MID_MUL) ? cmul(r[k], b[k]) : cmul_conj(r[k], b[k]);
    }
 }
 

@@ -77,6 +77,14 @@ int fufft_plan_radices(int64_t n, int variant, int* radices /* >= 32 */);
  * reversal over the radix widths in pass order.
  * (mixedrev_host, bench_fufft.cu:63-82; chain_rev, verify_kernel.cpp:460-477) */
 int fufft_digit_order(int64_t n, int variant, int32_t* perm);
+
+/* How each pass of the plan (in plan_radices order) generates its stage
+ * twiddles from the base twiddle W^j: FUFFT_CHAIN_SINGLE (W^(jk) =
+ * W^(j(k-1)) W^j, fufft.cuh:436-450) or FUFFT_CHAIN_EVENODD (radix 16: even
+ * and odd chains, fufft.cuh:701-720).  Returns the pass count. */
+#define FUFFT_CHAIN_SINGLE  0
+#define FUFFT_CHAIN_EVENODD 1
+int fufft_plan_chains(int64_t n, int variant, int* chains /* >= 32 */);
 /* Turn a natural-order spectrum or time-domain taps (n complex) into the
  * filter a conv call reads: fp64 DFT for taps, optional 1/n fold, digit-order
  * permutation, optional lane-major layout.  Host memory in and out.

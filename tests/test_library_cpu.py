@@ -41,6 +41,7 @@ def test_plan_and_digit_order_match_oracle(variant, v, n):
     import fufft_amd as ff
     plan = O.kernel_plan(n, v)
     assert ff.plan_radices(n, variant) == plan.radices
+    assert ff.plan_chains(n, variant) == plan.chains
     assert np.array_equal(ff.digit_order(n, variant), O.mixedrev(plan))
 
 
