@@ -63,6 +63,7 @@ def parse():
     p.add_argument("--large-sizes", default="32768,65536",
                    help="four-step sizes timed with --sweep-steps calls each ('' for none)")
     p.add_argument("--no-2d", action="store_true")
+    p.add_argument("--no-vendor", action="store_true", help="skip the rocFFT chain comparison")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--copy-only", action="store_true",
@@ -133,6 +134,33 @@ def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed):
     rel = rel_l2(ys, want)
     secs = time_launches(torch, step, steps, warmup, stream)
     del x, out
+    return secs / steps, rel
+
+
+def bench_vendor_chain(torch, dev, n, pts, steps, warmup, stream, seed):
+    """The vendor-library chain the reference compares against (cuFFT fwd ->
+    pointwise -> inv, bench_fufft.cu:201-213), on MI355X: torch.fft, which
+    calls rocFFT, forward -> multiply -> inverse on the same workload."""
+    batch = pts // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen).view(batch, n)
+    rng = np.random.default_rng(seed)
+    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+    spec = torch.fft.fft(torch.from_numpy(taps).to(dev))
+
+    def step():
+        return torch.fft.ifft(torch.fft.fft(x, dim=1) * spec, dim=1)
+
+    y = step()
+    torch.cuda.synchronize()
+    want = np.fft.ifft(np.fft.fft(x[:4].cpu().numpy().astype(np.complex128), axis=1)
+                       * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    rel = rel_l2(y[:4].cpu().numpy(), want)
+    del y
+    secs = time_launches(torch, step, steps, warmup, stream)
+    del x
+    torch.cuda.empty_cache()
     return secs / steps, rel
 
 
@@ -360,6 +388,12 @@ def main():
                      "copy_ceiling_gbs": round(copy_gbs, 1)},
         "accuracy": {"rel_l2_vs_fp64_sample": rel},
     }
+
+    if not args.no_vendor:
+        vt, vrel = bench_vendor_chain(torch, dev, n, pts, args.sweep_steps, 3, stream, 1234)
+        line["vendor_chain"] = {"what": "torch.fft (rocFFT) forward -> multiply -> inverse, same workload",
+                                "gpoints_s": round(pts / vt / 1e9, 3), "ms": round(vt * 1e3, 5),
+                                "rel_l2": vrel, "fused_speedup": round(vt / avg, 3)}
 
     sweep = {}
     for s in [int(v) for v in args.sweep.split(",") if v.strip()]:
