@@ -63,6 +63,7 @@ def parse():
     p.add_argument("--large-sizes", default="32768,65536",
                    help="four-step sizes timed with --sweep-steps calls each ('' for none)")
     p.add_argument("--no-2d", action="store_true")
+    p.add_argument("--no-c2c", action="store_true", help="skip the natural-order C2C line")
     p.add_argument("--no-vendor", action="store_true", help="skip the rocFFT chain comparison")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
@@ -162,6 +163,45 @@ def bench_vendor_chain(torch, dev, n, pts, steps, warmup, stream, seed):
     del x
     torch.cuda.empty_cache()
     return secs / steps, rel
+
+
+def bench_c2c(torch, ff, dev, n, pts, steps, warmup, stream, seed):
+    """Natural-order batched forward C2C (fufft_c2c_f32) and rocFFT's
+    (torch.fft.fft) on the same 2^27-point batch: 16 B/pt, read + write."""
+    batch = pts // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
+    out = torch.empty_like(x)
+
+    def ours():
+        ff.c2c(x, out, n=n, batch=batch, direction=ff.FORWARD, variant="auto", stream=stream)
+
+    ours()
+    torch.cuda.synchronize()
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
+    want = np.fft.fft(x.view(batch, n)[idx].cpu().numpy().astype(np.complex128), axis=1)
+    rel = rel_l2(out.view(batch, n)[idx].cpu().numpy(), want)
+    t_ours = time_launches(torch, ours, steps, warmup, stream) / steps
+    xv = x.view(batch, n)
+
+    def vendor():
+        return torch.fft.fft(xv, dim=1)
+
+    y = vendor()
+    torch.cuda.synchronize()
+    vrel = rel_l2(y.view(batch, n)[idx].cpu().numpy(), want)
+    del y
+    t_vendor = time_launches(torch, vendor, steps, warmup, stream) / steps
+    del x, out, xv
+    torch.cuda.empty_cache()
+    return {"n": n, "batch": batch, "direction": "forward", "variant": ff.resolve_variant(n, "auto"),
+            "gpoints_s": round(pts / t_ours / 1e9, 3), "ms": round(t_ours * 1e3, 5),
+            "achieved_16B_gbs": round(16.0 * pts / t_ours / 1e9, 1),
+            "frac_16B": round(16.0 * pts / t_ours / 1e9 / HBM_PEAK_GBS, 4), "rel_l2": rel,
+            "rocfft": {"what": "torch.fft.fft (rocFFT), same batch", "gpoints_s": round(pts / t_vendor / 1e9, 3),
+                       "ms": round(t_vendor * 1e3, 5), "rel_l2": vrel},
+            "speedup_vs_rocfft": round(t_vendor / t_ours, 3)}
 
 
 def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed):
@@ -443,6 +483,13 @@ def main():
                          "rel_l2": r}
     if large:
         line["large"] = large
+
+    if not args.no_c2c:
+        c2c = bench_c2c(torch, ff, dev, n, pts, args.sweep_steps, 3, stream, 21)
+        if not c2c["rel_l2"] <= 2e-6:
+            print(json.dumps({"error": f"C2C accuracy check failed: rel L2 {c2c['rel_l2']:.3e}"}))
+            sys.exit(1)
+        line["c2c"] = c2c
 
     if not args.no_2d:
         d2 = bench_2d(torch, ff, dev, pts, args.sweep_steps, 3, stream, 11)

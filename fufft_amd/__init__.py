@@ -28,6 +28,7 @@ MID = {"mul": 0, "conj": 1, "none": 2}
 VARIANT = {"v16": 0, "r8": 1, "auto": 2}
 LAYOUT = {"dr": 0, "lane": 1}
 FILTER_SPECTRUM, FILTER_TAPS = 0, 1
+FORWARD, INVERSE = -1, 1
 BFP_BLOCK = 64
 VALUES_PER_LANE = {"v16": 16, "r8": 8}
 
@@ -79,6 +80,10 @@ def _load() -> C.CDLL:
         "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp], i32),
         "fufft_fwd2d_f32": ([vp, vp, i64, i64, i64, vp], i32),
         "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_c2c_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_plan_filter_device_f32": ([vp, vp, i64, i64, i32, i32, i32, i32, vp], i32),
+        "fufft_plan_filter_large_device_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_plan_filter2d_device_f32": ([vp, vp, i64, i64, i64, i32, i32, vp], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name, None)
@@ -198,6 +203,35 @@ def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int 
     check(lib.fufft_conv_bfp16(_ptr(qin), _ptr(ein), _ptr(filt), filt_stride, _ptr(qout),
                                _ptr(eout), n, batch, MID[mid], VARIANT[variant], LAYOUT[layout],
                                _stream(stream)), "fufft_conv_bfp16")
+
+
+def c2c(inp, out, n: int, batch: int, direction: int = FORWARD, variant: str = "auto",
+        stream=None) -> None:
+    """Natural-order batched C2C: forward, or the unnormalised inverse."""
+    check(lib.fufft_c2c_f32(_ptr(inp), _ptr(out), n, batch, direction, VARIANT[variant],
+                            _stream(stream)), "fufft_c2c_f32")
+
+
+def plan_filter_device(inp, out, n: int, count: int = 1, variant: str = "v16", layout: str = "dr",
+                       kind: int = FILTER_SPECTRUM, fold_inv_n: bool = True, stream=None) -> None:
+    """fufft_plan_filter_f32 on device memory, for count filters."""
+    check(lib.fufft_plan_filter_device_f32(_ptr(inp), _ptr(out), n, count, VARIANT[variant],
+                                           LAYOUT[layout], kind, int(fold_inv_n), _stream(stream)),
+          "fufft_plan_filter_device_f32")
+
+
+def plan_filter_large_device(inp, out, n: int, count: int = 1, kind: int = FILTER_SPECTRUM,
+                             fold_inv_n: bool = True, stream=None) -> None:
+    check(lib.fufft_plan_filter_large_device_f32(_ptr(inp), _ptr(out), n, count, kind,
+                                                 int(fold_inv_n), _stream(stream)),
+          "fufft_plan_filter_large_device_f32")
+
+
+def plan_filter2d_device(inp, out, h: int, w: int, count: int = 1, kind: int = FILTER_SPECTRUM,
+                         fold_inv_n: bool = True, stream=None) -> None:
+    check(lib.fufft_plan_filter2d_device_f32(_ptr(inp), _ptr(out), h, w, count, kind,
+                                             int(fold_inv_n), _stream(stream)),
+          "fufft_plan_filter2d_device_f32")
 
 
 # ---- four-step large N -------------------------------------------------------------------

@@ -408,6 +408,72 @@ int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
    return run_conv1d(K_CONV_R2, (int)n, vl, p, stream);
 }
 
+// ---- natural-order C2C --------------------------------------------------------------
+
+int fufft_c2c_f32(const void* in, void* out, int64_t n, int64_t batch, int direction,
+                  int variant, void* stream)
+{
+   int v = 0;
+   int st = check_1d(n, batch, variant, FUFFT_MID_NONE, FUFFT_LAYOUT_DR, &v);
+   if(st != FUFFT_OK) return st;
+   if(direction != FUFFT_FORWARD && direction != FUFFT_INVERSE) return FUFFT_ERR_INVALID;
+   if(!in || !out) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   Conv1dParams p{};
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.in0 = in; p.out0 = out; p.ntrans = (uint32_t)batch;
+   p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR;
+   return run_conv1d(direction == FUFFT_FORWARD ? K_C2C_FWD : K_C2C_INV, (int)n, v, p, stream);
+}
+
+// ---- filter planning on the device -------------------------------------------------------
+
+static GatherDigits digits_of(const int* radices, int np)
+{
+   GatherDigits d{};
+   d.np = np;
+   for(int i = 0; i < np; i++) {
+      int w = 0;
+      while((1 << w) < radices[i]) w++;
+      d.w[i] = (uint8_t)w;
+      d.bits += w;
+   }
+   return d;
+}
+
+static int check_plan_kind(int filter_kind)
+{
+   if(filter_kind != FUFFT_FILTER_SPECTRUM && filter_kind != FUFFT_FILTER_TAPS) return FUFFT_ERR_INVALID;
+   return FUFFT_OK;
+}
+
+int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t count, int variant,
+                                 int layout, int filter_kind, int fold_inv_n, void* stream)
+{
+   int v = 0;
+   int st = check_1d(n, count, variant, FUFFT_MID_NONE, layout, &v);
+   if(st != FUFFT_OK) return st;
+   if((st = check_plan_kind(filter_kind)) != FUFFT_OK) return st;
+   if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   const float scale = fold_inv_n ? 1.0f / (float)n : 1.0f;   // a power of two: exact
+   if(filter_kind == FUFFT_FILTER_SPECTRUM) {
+      int r[64];
+      GatherParams g{};
+      g.in = static_cast<const float2*>(in); g.out = static_cast<float2*>(out);
+      g.total = (uint64_t)count * (uint64_t)n;
+      g.lane_v = layout == FUFFT_LAYOUT_LANE ? v : 0;
+      g.scale = scale;
+      g.dw = digits_of(r, factor(n, v, r));
+      return status_of(launch_gather(g, static_cast<hipStream_t>(stream)));
+   }
+   Conv1dParams p{};
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.in0 = in; p.out0 = out; p.ntrans = (uint32_t)count;
+   p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = layout; p.scale = scale;
+   return run_conv1d(K_PLAN_TAPS, (int)n, v, p, stream);
+}
+
 // ---- BFP fused conv ------------------------------------------------------------------
 
 int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
@@ -540,6 +606,44 @@ int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n, cons
       out[2 * i + 1] = (float)s[2 * bin + 1];
    }
    return FUFFT_OK;
+}
+
+int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int64_t count,
+                                       int filter_kind, int fold_inv_n, void* stream)
+{
+   int r[64], lout = 0, mn = 0;
+   const int np = large_radices(n, &lout, &mn, r);
+   if(np < 0) return np;
+   int st = check_plan_kind(filter_kind);
+   if(st != FUFFT_OK) return st;
+   if(count < 0 || count * (n / 16) > 0xffffffffll) return FUFFT_ERR_INVALID;
+   if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   const float2* tw = nullptr;
+   if((st = current_table(&tw)) != FUFFT_OK) return st;
+   if(count == 0) return FUFFT_OK;
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   const float scale = fold_inv_n ? 1.0f / (float)n : 1.0f;
+   if(filter_kind == FUFFT_FILTER_SPECTRUM) {
+      GatherParams g{};
+      g.in = static_cast<const float2*>(in); g.out = static_cast<float2*>(out);
+      g.total = (uint64_t)count * (uint64_t)n;
+      g.scale = scale;
+      g.dw = digits_of(r, np);
+      return status_of(launch_gather(g, s));
+   }
+   // taps: the forward half of the four-step chain, in place on out
+   if(in != out && hipMemcpyAsync(out, in, (size_t)count * n * 8, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return FUFFT_ERR_HIP;
+   for(int l = 0; l < lout; l++) {
+      const hipError_t e = launch_outer_pass(static_cast<float2*>(out), n, count, n >> (4 * (l + 1)), false, tw, s);
+      if(e != hipSuccess) return status_of(e);
+   }
+   Conv1dParams p{};
+   p.tw = tw; p.in0 = out; p.out0 = out;
+   p.ntrans = (uint32_t)(count * (n / mn));
+   p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR; p.scale = scale;
+   return run_conv1d(K_PLAN_TAPS, mn, values_per_lane(resolve_variant(mn, FUFFT_AUTO)), p, stream);
 }
 
 int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64_t n,
@@ -687,6 +791,39 @@ int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind, int fold_inv_
       }
    }
    return FUFFT_OK;
+}
+
+int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t w, int64_t count,
+                                   int filter_kind, int fold_inv_n, void* stream)
+{
+   Plan2d pl;
+   int st = check_2d(h, w, count, &pl);
+   if(st != FUFFT_OK) return st;
+   if((st = check_plan_kind(filter_kind)) != FUFFT_OK) return st;
+   if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   const float2* tw = nullptr;
+   if((st = current_table(&tw)) != FUFFT_OK) return st;
+   if(count == 0) return FUFFT_OK;
+   hipStream_t s = static_cast<hipStream_t>(stream);
+   const float scale = fold_inv_n ? 1.0f / (float)(h * w) : 1.0f;
+   if(filter_kind == FUFFT_FILTER_SPECTRUM) {
+      GatherParams g{};
+      g.in = static_cast<const float2*>(in); g.out = static_cast<float2*>(out);
+      g.total = (uint64_t)count * (uint64_t)(h * w);
+      g.scale = scale;
+      g.dh = digits_of(pl.rc, pl.nc);
+      g.dw = digits_of(pl.rr, pl.nr);
+      return status_of(launch_gather(g, s));
+   }
+   // taps: rows DIF (scaled) into out, then columns DIF in place -- the
+   // forward half of fufft_conv2d_f32
+   Conv1dParams r = rows_params(tw, h, count);
+   r.in0 = in; r.out0 = out; r.scale = scale;
+   if((st = run_conv1d(K_PLAN_TAPS, (int)w, pl.vr, r, stream)) != FUFFT_OK) return st;
+   ColParams c = col_params(tw, w, count);
+   c.in = out; c.out = out;
+   return status_of(launch_col(COL_FWD, (int)h, c, s));
 }
 
 int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride, void* out,

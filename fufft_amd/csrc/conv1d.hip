@@ -5,7 +5,8 @@
 // Replaces the reference kernels fufft_pipeline_v16 / _v16f / _wide
 // (fufft.cuh:1499-1534, 1703-1734), fufft_pipeline_ip / _fused
 // (fufft.cuh:1757-1791), fufft_pipeline_fwd / _apply (fufft.cuh:1343-1407) and
-// fufft_conv_r2 (fufft.cuh:1273-1330).
+// fufft_conv_r2 (fufft.cuh:1273-1330), and the natural-order batched C2C
+// fufft_c2c (fufft.cuh:879-904).
 //
 // Mapping to CDNA4.  A transform of N points is held by T = N/V lanes with V
 // values each (V = 16: radix-16 passes; V = 8: radix-8 passes).  T <= 64
@@ -42,6 +43,9 @@ conv1d_kernel(const Conv1dParams p)
    constexpr bool REAL_OUT  = KIND == K_CONV_R2 || KIND == K_APPLY_R2;
    constexpr bool FROM_SPEC = KIND == K_APPLY || KIND == K_APPLY_R2;
    constexpr bool TO_SPEC   = KIND == K_FWD || KIND == K_FWD_R2;
+   constexpr bool C2C_FWD   = KIND == K_C2C_FWD;
+   constexpr bool C2C_INV   = KIND == K_C2C_INV;
+   constexpr bool PLAN      = KIND == K_PLAN_TAPS;
    constexpr int  EL_IN     = REAL_IN ? 4 : 8;
    constexpr int  EL_OUT    = REAL_OUT ? 4 : 8;
 
@@ -85,10 +89,31 @@ conv1d_kernel(const Conv1dParams p)
 #pragma unroll
          for(int q = 0; q < V; q++) r[q] = xb.ld2(lane_pos * 8u, q * T * 8);
       }
-      forward_dif<PL, LD, LANES>(r, A, L, tw);
+      if constexpr(C2C_INV) natural_to_digit<PL, LD, LANES, true>(r, A, L);
+      else                  forward_dif<PL, LD, LANES>(r, A, L, tw);
    }
 
-   if constexpr(TO_SPEC) {
+   if constexpr(C2C_FWD) {
+      digit_to_natural<PL, LD, LANES>(r, A, L);
+      const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
+#pragma unroll
+      for(int q = 0; q < V; q++) ob.st2(r[q], lane_pos * 8u, q * T * 8);
+      return;
+   } else if constexpr(PLAN) {
+      const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
+#pragma unroll
+      for(int k = 0; k < V; k++) r[k] = make_float2(r[k].x * p.scale, r[k].y * p.scale);
+      if(p.fl == FLT_DR) {
+         const uint32_t so = ((t - t0) * N + L * V) * 8u;
+#pragma unroll
+         for(int m = 0; m < V / 2; m++)
+            ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * 16);
+      } else {
+#pragma unroll
+         for(int k = 0; k < V; k++) ob.st2(r[k], lane_pos * 8u, k * T * 8);
+      }
+      return;
+   } else if constexpr(TO_SPEC) {
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
       const uint32_t so = ((t - t0) * N + L * V) * 8u;
 #pragma unroll
@@ -96,7 +121,7 @@ conv1d_kernel(const Conv1dParams p)
          ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * 16);
       return;
    } else {
-      {
+      if constexpr(!C2C_INV) {
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
          const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
          mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
@@ -284,6 +309,9 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
          // only the 2D two-for-one path uses it, as the row inverse
          return p.mid == MID_NONE ? launch_one<N, V, LAYOUT, K_APPLY_R2, MID_NONE>(p, s)
                                   : hipErrorInvalidValue;
+      case K_C2C_FWD:   return launch_one<N, V, LAYOUT, K_C2C_FWD, MID_NONE>(p, s);
+      case K_C2C_INV:   return launch_one<N, V, LAYOUT, K_C2C_INV, MID_NONE>(p, s);
+      case K_PLAN_TAPS: return launch_one<N, V, LAYOUT, K_PLAN_TAPS, MID_NONE>(p, s);
       default:        return hipErrorInvalidValue;
    }
 }

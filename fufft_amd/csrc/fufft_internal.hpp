@@ -9,8 +9,13 @@ namespace fufft {
 
 // ---- 1D fused pipeline (conv1d.hip) ------------------------------------------------
 // K_FWD_R2 / K_APPLY_R2: the forward half reading two real arrays, the
-// inverse half writing two real arrays (2D two-for-one rows)
-enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5 };
+// inverse half writing two real arrays (2D two-for-one rows).
+// K_C2C_FWD / K_C2C_INV: natural order in and out (forward DIF + digit ->
+// natural exchange; natural -> digit exchange + inverse DIT, unnormalised).
+// K_PLAN_TAPS: forward DIF of filter taps, times scale, stored in the filter
+// layout fl (digit order or lane-major).
+enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5,
+       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8 };
 
 struct Conv1dParams {
    const void*   in0;      // complex input, or real x (K_CONV_R2)
@@ -24,11 +29,28 @@ struct Conv1dParams {
    uint32_t      fcount;   // transform t uses filter (t % fcount)
    uint32_t      scount;   // transform t uses spectrum (t % scount)
    int32_t       mid;      // MID_MUL / MID_CONJ / MID_NONE
-   int32_t       fl;       // FLT_DR / FLT_LANE
+   int32_t       fl;       // FLT_DR / FLT_LANE (filter read; K_PLAN_TAPS: layout written)
+   float         scale;    // K_PLAN_TAPS: factor applied to the spectrum
 };
 
 bool       conv1d_supported(int n, int v);
 hipError_t launch_conv1d(int kind, int n, int v, int layout, const Conv1dParams& p, hipStream_t s);
+
+// ---- filter planning on the device (plan.hip) ----------------------------------------
+struct GatherDigits {
+   int32_t np;             // digit groups (passes)
+   int32_t bits;           // sum of the widths = log2 of the dimension
+   uint8_t w[32];          // bit width of each group, in pass order
+};
+struct GatherParams {
+   const float2* in;       // natural-order spectra
+   float2*       out;      // planned filters (must not alias in)
+   uint64_t      total;    // points over all items
+   int32_t       lane_v;   // 1D lane-major output: values per lane; 0 = digit order
+   float         scale;
+   GatherDigits  dh, dw;   // rows (dh.np = 0 in 1D) and row digits
+};
+hipError_t launch_gather(const GatherParams& p, hipStream_t s);
 
 // ---- int16 block floating point (bfp.hip) ---------------------------------------------
 struct BfpParams {

@@ -248,6 +248,73 @@ __device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L
    });
 }
 
+// ---- digit order <-> natural order through LDS ------------------------------------------
+// After the forward DIF lane L holds slots L*V + k, and slot L*V + k holds bin
+// lane_bin(L) + k*T: digit p of the slot (weight M_p, radix R_p) becomes digit
+// p of the bin (weight R_0 ... R_{p-1}); the last pass's digit is k itself.
+template<class PL>
+constexpr int digit_weight(int p)
+{
+   int w = 1;
+   for(int i = 0; i < p; i++) w *= PL::radix(i);
+   return w;
+}
+
+template<class PL>
+__device__ __forceinline__ int lane_bin(int L)
+{
+   int f = 0;
+   static_for<PL::NP - 1>([&](auto pi) {
+      constexpr int p = decltype(pi)::value;
+      constexpr int D = PL::stride(p) / PL::V;      // weight of digit p in the lane index
+      f += ((L / D) & (PL::radix(p) - 1)) * digit_weight<PL>(p);
+   });
+   return f;
+}
+
+// LDS slot of logical position base + off, where off is a multiple of V (so
+// the padded layout stays additive)
+template<class LD>
+__device__ __forceinline__ float2* lds_slot(float2* A, int base_phys, int base, int off)
+{
+   if constexpr(LD::additive) return A + base_phys + LD::cphys(off);
+   else                       return A + LD::phys(base + off);
+}
+
+// r[k] = slot L*V + k (forward DIF output)  ->  r[q] = bin L + q*T, so the
+// store that follows is the coalesced natural-order store of the conv kernels.
+// The first barrier orders the last DIF pass's gather before these writes.
+template<class PL, class LD, int LANES>
+__device__ __forceinline__ void digit_to_natural(float2 (&r)[PL::V], float2* A, int L)
+{
+   constexpr int V = PL::V, T = PL::T;
+   const int f = lane_bin<PL>(L);
+   const int fp = LD::phys(f), lp = LD::phys(L);
+   pass_barrier<LANES>();
+#pragma unroll
+   for(int k = 0; k < V; k++) *lds_slot<LD>(A, fp, f, k * T) = r[k];
+   pass_barrier<LANES>();
+#pragma unroll
+   for(int q = 0; q < V; q++) r[q] = *lds_slot<LD>(A, lp, L, q * T);
+}
+
+// r[q] = bin L + q*T (natural-order load)  ->  r[k] = slot L*V + k, what the
+// inverse DIT expects.  With WAR the trailing barrier orders these reads
+// before the next pass's LDS writes.
+template<class PL, class LD, int LANES, bool WAR>
+__device__ __forceinline__ void natural_to_digit(float2 (&r)[PL::V], float2* A, int L)
+{
+   constexpr int V = PL::V, T = PL::T;
+   const int f = lane_bin<PL>(L);
+   const int fp = LD::phys(f), lp = LD::phys(L);
+#pragma unroll
+   for(int q = 0; q < V; q++) *lds_slot<LD>(A, lp, L, q * T) = r[q];
+   pass_barrier<LANES>();
+#pragma unroll
+   for(int k = 0; k < V; k++) r[k] = *lds_slot<LD>(A, fp, f, k * T);
+   if constexpr(WAR) pass_barrier<LANES>();
+}
+
 // ---- the mid operation at the M = 1 boundary -----------------------------------------
 enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
 // filter layouts: DR = digit order, slot i holds bin mixedrev(i) (what the

@@ -127,6 +127,43 @@ int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
                       int64_t filt_stride, float* u, float* v, int64_t n,
                       int64_t batch, int variant, int layout, void* stream);
 
+/* ---- natural-order batched C2C ------------------------------------------------
+ * out = DFT(in) with direction FUFFT_FORWARD (exp(-2 pi i jk/n)) or the
+ * unnormalised inverse with FUFFT_INVERSE (exp(+2 pi i jk/n)), natural order
+ * in and out, batch transforms of n points, one launch, two HBM passes;
+ * in == out is allowed.  Replaces fufft_c2c<N,LOG8N,CPB> (fufft.cuh:879-904),
+ * a forward-only radix-8 Stockham transform for N = 8^k launched with one
+ * workgroup per CPB transforms.  Here the forward DIF of the conv kernels (or
+ * their inverse DIT) runs unchanged and one exchange through LDS moves the
+ * spectrum between digit order and natural order, for every size and
+ * variant fufft_supported accepts. */
+#define FUFFT_FORWARD (-1)
+#define FUFFT_INVERSE   1
+int fufft_c2c_f32(const void* in, void* out, int64_t n, int64_t batch,
+                  int direction, int variant, void* stream);
+
+/* ---- filter planning on the device ----------------------------------------------
+ * The host planning step of the reference (filter spectrum, digit-order
+ * permutation and 1/N fold: bench_fufft.cu:156-170; chain order,
+ * bench_fufft.cu:410-428; 2D order, verify_kernel.cpp:738-748) for `count`
+ * filters already in device memory.  Same arguments and output as
+ * fufft_plan_filter_f32 / _large_ / 2d_ (n, or h*w, complex points per filter).
+ *   FUFFT_FILTER_SPECTRUM: a gather into the conv's digit order (times 1/n
+ *     with fold_inv_n); bit-identical to the host planner.  in != out.
+ *   FUFFT_FILTER_TAPS: the conv kernels' own forward transform in fp32
+ *     (times 1/n, exact since n is a power of two).  The host planner takes
+ *     this DFT in fp64 instead, so the two agree to fp32 transform rounding
+ *     (rel L2 ~3e-7), not bit for bit.  in == out is allowed. */
+int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t count,
+                                 int variant, int layout, int filter_kind,
+                                 int fold_inv_n, void* stream);
+int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n,
+                                       int64_t count, int filter_kind,
+                                       int fold_inv_n, void* stream);
+int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t w,
+                                   int64_t count, int filter_kind, int fold_inv_n,
+                                   void* stream);
+
 /* ---- int16 block floating point ----------------------------------------------
  * A point is two int16 (re in the low halfword, im in the high halfword);
  * every block of FUFFT_BFP_BLOCK consecutive points of a signal shares one

@@ -92,6 +92,26 @@ inline int pipeline_bfp(const void* qin, const int8_t* ein, const void* filt, vo
                            stream);
 }
 
+// fufft_c2c<N, LOG8N, CPB> (fufft.cuh:879-904): natural-order batched C2C; the
+// reference's is forward only, Direction here is FUFFT_FORWARD or FUFFT_INVERSE
+template<int Direction = FUFFT_FORWARD>
+inline int c2c(const void* in, void* out, int64_t n, int64_t batch, void* stream = nullptr,
+               Variant v = Variant::Auto)
+{
+   static_assert(Direction == FUFFT_FORWARD || Direction == FUFFT_INVERSE, "direction is -1 or +1");
+   return fufft_c2c_f32(in, out, n, batch, Direction, (int)v, stream);
+}
+
+// the host planning of bench_fufft.cu:156-170 on device memory, for count filters
+inline int plan_filter_device(const void* natural, void* planned, int64_t n, int64_t count = 1,
+                              void* stream = nullptr, Variant v = Variant::Auto,
+                              int kind = FUFFT_FILTER_TAPS, int layout = FUFFT_LAYOUT_DR,
+                              bool fold_inv_n = true)
+{
+   return fufft_plan_filter_device_f32(natural, planned, n, count, (int)v, layout, kind,
+                                       fold_inv_n ? 1 : 0, stream);
+}
+
 // ---- four-step (run_large, bench_fufft.cu:357-492) ----------------------------------------
 
 template<class Mid = MidMultiply>

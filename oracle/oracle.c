@@ -350,6 +350,37 @@ void or_conv_r2_f32(const float* x, const float* y, const float* filt,
    free(A);
 }
 
+/* ---- natural-order C2C ------------------------------------------------------
+ * The reference's fufft_c2c (fufft.cuh:879-904; CPU transcription kernel_c2c,
+ * verify_kernel.cpp:1183-1203) is a forward radix-8 Stockham transform.  This
+ * build reaches natural order with the in-place passes instead: forward = the
+ * DIF of the conv path, then slot s moved to bin mixedrev(s); inverse = bin
+ * mixedrev(s) moved to slot s, then the DIT with sign +1, unnormalised.  The
+ * permutation is exact, so the transform's rounding is that of the DIF / DIT
+ * passes, which are pinned to the reference's transcription. */
+void or_c2c_f32(const float* in, float* out, int n, int64_t batch,
+                const int* radices, const int* chains, int np, int sign, int twmode)
+{
+   float* A = (float*)malloc(sizeof(float) * 2 * (size_t)n);
+   int* rev = (int*)malloc(sizeof(int) * (size_t)n);
+   for(int s = 0; s < n; s++) rev[s] = or_mixedrev(s, radices, np);
+   for(int64_t t = 0; t < batch; t++) {
+      const float* x = in + 2 * t * n;
+      float* y = out + 2 * t * n;
+      if(sign < 0) {
+         memcpy(A, x, sizeof(float) * 2 * (size_t)n);
+         dif_all(A, n, radices, chains, np, twmode);
+         for(int s = 0; s < n; s++) { y[2 * rev[s]] = A[2 * s]; y[2 * rev[s] + 1] = A[2 * s + 1]; }
+      } else {
+         for(int s = 0; s < n; s++) { A[2 * s] = x[2 * rev[s]]; A[2 * s + 1] = x[2 * rev[s] + 1]; }
+         dit_all(A, n, radices, chains, np, twmode);
+         memcpy(y, A, sizeof(float) * 2 * (size_t)n);
+      }
+   }
+   free(rev);
+   free(A);
+}
+
 /* ---- 2D ------------------------------------------------------------------ */
 
 static void rows_dif(float* A, int h, int w, const int* r, const int* ch, int np, int tw)

@@ -105,6 +105,13 @@ void or_conv_r2_f32(const float* x, const float* y, const float* filt,
                     int64_t batch, const int* radices, const int* chains,
                     int np, int twmode);
 
+/* natural-order C2C: sign -1 forward DIF then slot s -> bin mixedrev(s);
+ * sign +1 bin mixedrev(s) -> slot s then DIT, unnormalised.  in may equal out.
+ * (fufft_c2c, fufft.cuh:879-904, is the forward Stockham counterpart) */
+void or_c2c_f32(const float* in, float* out, int n, int64_t batch,
+                const int* radices, const int* chains, int np, int sign,
+                int twmode);
+
 /* 2D conv of h x w images (row-major): row DIF, column DIF, mid, column DIT,
  * row DIT (verify_kernel.cpp:700-722).  filt slot (r, c) holds spectrum bin
  * (mixedrev_h(r), mixedrev_w(c)). */

@@ -34,6 +34,7 @@ def _load_oracle() -> C.CDLL:
     L.or_fwd_f32.argtypes = [_vp, _vp, _i32, _i64, ip, ip, _i32, _i32]
     L.or_apply_f32.argtypes = [_vp, _i64, _vp, _i64, _vp, _i32, _i64, ip, ip, _i32, _i32, _i32]
     L.or_conv_r2_f32.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _i32, _i64, ip, ip, _i32, _i32]
+    L.or_c2c_f32.argtypes = [_vp, _vp, _i32, _i64, ip, ip, _i32, _i32, _i32]
     L.or_conv2d_f32.argtypes = [_vp, _vp, _i64, _vp, _i32, _i32, _i64, ip, ip, _i32, ip, ip,
                                 _i32, _i32, _i32]
     L.or_fwd2d_f32.argtypes = [_vp, _vp, _i32, _i32, _i64, ip, ip, _i32, ip, ip, _i32, _i32]
@@ -73,6 +74,7 @@ def load_ref() -> C.CDLL | None:
                  "ref_vk_pipeline_apply"):
         getattr(R, name).argtypes = [_i32, _i32, _i32, _i32, _vp, _vp, _vp, _i32]
     R.ref_vk_pipeline_fwd.argtypes = [_i32, _i32, _i32, _i32, _vp, _vp, _i32]
+    R.ref_vk_c2c.argtypes = [_i32, _i32, _vp, _vp, _i32]
     R.ref_vk_conv_foursteps_cfg.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _i32]
     R.ref_vk_conv_monolithic_cfg.argtypes = [_vp, _vp, _i32, _i32, _i32, _i32, _i32]
     R.ref_vk_conv2d.argtypes = [_i32, _i32, _vp, _vp, _vp, _i32]
@@ -180,6 +182,15 @@ def conv_r2(x, y, filt, n: int, plan: Plan, filt_stride: int = 0, tw: int = TW_T
     lib.or_conv_r2_f32(x.ctypes.data, y.ctypes.data, f.ctypes.data, filt_stride, u.ctypes.data,
                        v.ctypes.data, n, x.size // n, plan._r, plan._c, plan.np, tw)
     return u, v
+
+
+def c2c(a, n: int, plan: Plan, sign: int = -1, tw: int = TW_TABLE) -> np.ndarray:
+    """Natural-order C2C: forward (sign -1) or unnormalised inverse (+1)."""
+    a = _c64(a).reshape(-1)
+    out = np.empty_like(a)
+    lib.or_c2c_f32(a.ctypes.data, out.ctypes.data, n, a.size // n, plan._r, plan._c, plan.np,
+                   sign, tw)
+    return out
 
 
 def conv2d(a, filt, h: int, w: int, ph: Plan, pw: Plan, filt_stride: int = 0,

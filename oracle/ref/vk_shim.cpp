@@ -55,6 +55,15 @@ void ref_vk_pipeline_v16f(int N, int lead, int nrv, int cpb, const float* a,
    put(o, out);
 }
 
+// verify_kernel.cpp:1183-1203 (fufft_c2c: forward radix-8 Stockham, N = 8^k)
+void ref_vk_c2c(int N, int cpb, const float* a, float* out, int batch)
+{
+   const size_t n = (size_t)N * batch;
+   std::vector<cf> o;
+   kernel_c2c(N, ilog8(N), cpb, CPP_OPT, vec(a, n), o, batch);
+   put(o, out);
+}
+
 // verify_kernel.cpp:211-244 (fufft_pipeline_ip with MidMultiply)
 void ref_vk_pipeline_ip(int N, int lead, int nr8, int cpb, const float* a,
                         const float* b_dr, float* out, int batch)

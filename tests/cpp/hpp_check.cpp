@@ -21,6 +21,8 @@ int main()
    if(fufft::pipeline<fufft::MidMultiply>(nullptr, nullptr, nullptr, 1000, 1) != FUFFT_ERR_UNSUPPORTED) return 5;
    if(fufft::conv_large<fufft::MidNothing>(nullptr, nullptr, 1024, 1) != FUFFT_ERR_UNSUPPORTED) return 6;
    if(!fufft::supported(n) || fufft::supported(100)) return 7;
+   if(fufft::c2c<FUFFT_INVERSE>(nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID) return 8;
+   if(fufft::plan_filter_device(nullptr, nullptr, n) != FUFFT_ERR_INVALID) return 9;
    std::printf("ok %s\n", fufft::status_string(FUFFT_OK));
    return 0;
 }

@@ -48,4 +48,9 @@ def replay(case: dict) -> dict:
     if kind == "fourstep":
         n, lout, mid = int(case["n"]), int(case["lout"]), int(case["mid"])
         return {"out": O.conv(case["a"], case["bdr"], n, O.large_plan(lout, mid, ref=True), filt_stride=n, tw=O.TW_LIBM)}
+    if kind == "c2c_stockham":
+        # the reference's Stockham C2C rounds in a different order from this
+        # build's DIF + permutation: no bit-exact outputs; test_oracle_c2c
+        # checks it to fp32 rounding
+        return {}
     raise ValueError(kind)

@@ -83,6 +83,13 @@ def main() -> None:
     R.ref_vk_conv_foursteps_cfg(A.ctypes.data, bdr.ctypes.data, n, 1, 16, mid, 1)
     save("fourstep_n4096_mid256", kind="fourstep", n=n, lout=1, mid=mid, a=a, bdr=bdr, out=A.reshape(-1))
 
+    # drawn last so the fixtures above keep their inputs
+    n, batch = 512, 2
+    a = _cu(rng, (batch, n))
+    out = np.empty_like(a)
+    R.ref_vk_c2c(n, 1, a.ctypes.data, out.ctypes.data, batch)
+    save("c2c_stockham_n512", kind="c2c_stockham", n=n, a=a, out=out.reshape(-1))
+
 
 if __name__ == "__main__":
     main()

@@ -176,3 +176,44 @@ def test_wave_local_exchanges(v, n, wl):
     # the plans that matter do drop barriers: R8 4096 keeps 1 of 3 per direction
     if (v, n, wl) == (8, 4096, 64):
         assert local == 2
+
+
+# digit order <-> natural order exchange (digit_to_natural / natural_to_digit,
+# fufft_plan.hpp): lane L writes slot L*V + k to bin lane_bin(L) + k*T and reads
+# bins L + q*T.  The kernel relies on lane_bin being the plan's digit reversal
+# restricted to the lane digits, and on the padded layout staying additive.
+def lane_bin(L, n, v):
+    f, w = 0, 1
+    for (R, M) in plan(n, v)[:-1]:
+        f += ((L // (M // v)) % R) * w
+        w *= R
+    return f
+
+
+def mixedrev(s, n, v):
+    f, w = 0, 1
+    for (R, M) in plan(n, v):
+        f += ((s // M) % R) * w
+        w *= R
+    return f
+
+
+UNSCRAMBLE = PLANS + [(8, 8192)]
+
+
+@pytest.mark.parametrize("v,n", UNSCRAMBLE)
+def test_unscramble_targets_and_conflicts(v, n):
+    T = n // v
+    for L in range(T):
+        f = lane_bin(L, n, v)
+        for k in range(v):
+            assert f + k * T == mixedrev(L * v + k, n, v)
+            assert phys_pad(f + k * T, v) == phys_pad(f, v) + phys_pad(k * T, v)
+    worst = 1
+    for k in range(v):
+        pos = [lane_bin(L, n, v) + k * T for L in range(T)]
+        if len(pos) < 32:
+            pos = [p + r * n for r in range(32 // len(pos)) for p in pos]
+        worst = max(worst, degree([phys_pad(p, v) for p in pos]))
+    # measured bound of the scattered side; the natural side is pass 0's pattern
+    assert worst <= (2 if n <= 4096 and (v, n) != (8, 1024) else 4), worst

@@ -143,6 +143,13 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake, 512, 512, 2, 0, None) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(None, 64, None, None) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(fake, 65, fake, fake) == ff.ERR_INVALID
+    assert L.fufft_c2c_f32(fake, fake, 4096, 1, 0, 2, None) == ff.ERR_INVALID
+    assert L.fufft_c2c_f32(fake, fake, 4097, 1, -1, 2, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_c2c_f32(fake + 8, fake, 4096, 1, -1, 2, None) == ff.ERR_ALIGN
+    assert L.fufft_plan_filter_device_f32(fake, fake, 4096, 1, 2, 0, 0, 1, None) == ff.ERR_INVALID
+    assert L.fufft_plan_filter_device_f32(fake, fake + 16, 4096, 1, 2, 0, 5, 1, None) == ff.ERR_INVALID
+    assert L.fufft_plan_filter_large_device_f32(fake, fake, 4096, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter2d_device_f32(fake, fake, 512, 100, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("pointer")
 
 
