@@ -81,6 +81,8 @@ def _load() -> C.CDLL:
         "fufft_fwd2d_f32": ([vp, vp, i64, i64, i64, vp], i32),
         "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, vp], i32),
         "fufft_c2c_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_transforms_per_workgroup": ([i64, i32], i32),
+        "fufft_conv_timed_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp, i64, vp], i32),
         "fufft_plan_filter_device_f32": ([vp, vp, i64, i64, i32, i32, i32, i32, vp], i32),
         "fufft_plan_filter_large_device_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
         "fufft_plan_filter2d_device_f32": ([vp, vp, i64, i64, i64, i32, i32, vp], i32),
@@ -177,6 +179,43 @@ def conv(inp, filt, out, n: int, batch: int, filt_stride: int = 0, mid: str = "m
          variant: str = "v16", layout: str = "dr", stream=None) -> None:
     check(lib.fufft_conv_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), n, batch, MID[mid],
                              VARIANT[variant], LAYOUT[layout], _stream(stream)), "fufft_conv_f32")
+
+
+TIMER_STRIDE = 12
+PHASES = ("load", "forward", "mid", "inverse", "store")
+
+
+def transforms_per_workgroup(n: int, variant: str = "auto") -> int:
+    k = lib.fufft_transforms_per_workgroup(n, VARIANT[variant])
+    if k < 0:
+        raise FufftError(k, "fufft_transforms_per_workgroup")
+    return k
+
+
+def conv_timed(inp, filt, out, timing, n: int, batch: int, timing_groups: int, filt_stride: int = 0,
+               mid: str = "mul", variant: str = "v16", layout: str = "dr", stream=None) -> None:
+    """fufft_conv_f32 with the in-kernel phase timer; timing is a device buffer
+    of timing_groups * TIMER_STRIDE uint32 words (decode with decode_timing)."""
+    check(lib.fufft_conv_timed_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), n, batch, MID[mid],
+                                   VARIANT[variant], LAYOUT[layout], _ptr(timing), timing_groups,
+                                   _stream(stream)), "fufft_conv_timed_f32")
+
+
+def decode_timing(words: np.ndarray) -> dict:
+    """Phase-timer records -> arrays: xcd, cu, se, start (cycles), and the cycles
+    spent in each phase (differences of consecutive marks)."""
+    w = np.asarray(words, dtype=np.uint32).reshape(-1, TIMER_STRIDE).astype(np.int64)
+    marks = w[:, 6:11] & 0xFFFFFF
+    phase_ids = w[:, 6:11] >> 24
+    if not np.all(phase_ids == np.arange(1, 6)):
+        raise ValueError("timer records carry unexpected phase ids")
+    prev = np.concatenate([np.zeros((len(w), 1), np.int64), marks[:, :-1]], axis=1)
+    return {
+        "hw_id": w[:, 0], "xcd": w[:, 1] & 0xF, "cu": (w[:, 0] >> 8) & 0xF, "simd": (w[:, 0] >> 4) & 0x3,
+        "realtime_ticks": w[:, 3], "start": w[:, 4] | (w[:, 5] << 32), "marks": marks,
+        "phase_cycles": {name: marks[:, i] - prev[:, i] for i, name in enumerate(PHASES)},
+        "total_cycles": marks[:, -1],
+    }
 
 
 def fwd(inp, spec, n: int, batch: int, variant: str = "v16", stream=None) -> None:

@@ -357,6 +357,40 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    return run_conv1d(K_CONV, (int)n, v, p, stream);
 }
 
+static_assert(TIMER_STRIDE == FUFFT_TIMER_STRIDE, "timer record layout");
+
+int fufft_transforms_per_workgroup(int64_t n, int variant)
+{
+   const int v = values_per_lane(resolve_variant(n, variant));
+   if(!v || !fufft_supported(n, variant)) return FUFFT_ERR_UNSUPPORTED;
+   const int64_t T = n / v;
+   return T >= 128 ? 1 : (int)(256 / T);
+}
+
+int fufft_conv_timed_f32(const void* in, const void* filt, int64_t filt_stride, void* out,
+                         int64_t n, int64_t batch, int mid, int variant, int layout,
+                         uint32_t* timing, int64_t timing_groups, void* stream)
+{
+   int v = 0;
+   int st = check_1d(n, batch, variant, mid, layout, &v);
+   if(st != FUFFT_OK) return st;
+   if(!in || !out || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
+   if(timing_groups < 0 || timing_groups > 0xffffffffll || (timing_groups > 0 && !timing))
+      return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt)) || !aligned4(timing))
+      return FUFFT_ERR_ALIGN;
+   // one launch only, so record g is workgroup g of the whole call
+   if(lds_layout() != LAYOUT_PAD) return FUFFT_ERR_UNSUPPORTED;
+   Conv1dParams p{};
+   if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   if((uint64_t)p.fcount * (uint64_t)n * 8 > 0xffffffffull) return FUFFT_ERR_UNSUPPORTED;
+   if((st = current_table(&p.tw)) != FUFFT_OK) return st;
+   p.in0 = in; p.filt = filt; p.out0 = out;
+   p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
+   p.timing = timing; p.timing_groups = (uint32_t)timing_groups;
+   return run_conv1d(K_CONV_TIMED, (int)n, v, p, stream);
+}
+
 int fufft_fwd_f32(const void* in, void* spec, int64_t n, int64_t batch,
                   int variant, void* stream)
 {

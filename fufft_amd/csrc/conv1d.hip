@@ -46,6 +46,7 @@ conv1d_kernel(const Conv1dParams p)
    constexpr bool C2C_FWD   = KIND == K_C2C_FWD;
    constexpr bool C2C_INV   = KIND == K_C2C_INV;
    constexpr bool PLAN      = KIND == K_PLAN_TAPS;
+   constexpr bool TIMED     = KIND == K_CONV_TIMED;
    constexpr int  EL_IN     = REAL_IN ? 4 : 8;
    constexpr int  EL_OUT    = REAL_OUT ? 4 : 8;
 
@@ -61,6 +62,19 @@ conv1d_kernel(const Conv1dParams p)
    const uint32_t lane_pos = (t - t0) * N + L;
 
    float2* A = lds + slot * SLOT;
+   // phase timer: every memory operation retired and every wavefront of the
+   // workgroup arrived, then the shader clock (reads only; thread 0 writes the
+   // record with ordinary vector stores at the end)
+   uint64_t ts[TIMER_MARKS + 1], rt0 = 0;
+   auto stamp = [&](int i) {
+      if constexpr(TIMED) {
+         __builtin_amdgcn_s_waitcnt(0);
+         __syncthreads();
+         ts[i] = __builtin_amdgcn_s_memtime();
+      }
+   };
+   stamp(0);
+   if constexpr(TIMED) rt0 = __builtin_amdgcn_s_memrealtime();
    Twiddles<PL> tw;
    tw.load(p.tw, L);
    float2 r[V];
@@ -89,8 +103,10 @@ conv1d_kernel(const Conv1dParams p)
 #pragma unroll
          for(int q = 0; q < V; q++) r[q] = xb.ld2(lane_pos * 8u, q * T * 8);
       }
+      stamp(1);
       if constexpr(C2C_INV) natural_to_digit<PL, LD, LANES, true>(r, A, L);
       else                  forward_dif<PL, LD, LANES>(r, A, L, tw);
+      stamp(2);
    }
 
    if constexpr(C2C_FWD) {
@@ -126,7 +142,9 @@ conv1d_kernel(const Conv1dParams p)
          const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
          mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
       }
+      stamp(3);
       inverse_dit<PL, LD, LANES>(r, A, L, tw);
+      stamp(4);
 
       const size_t wb = (size_t)t0 * N * EL_OUT;
       constexpr uint32_t WB = TPW * N * EL_OUT;
@@ -142,6 +160,25 @@ conv1d_kernel(const Conv1dParams p)
          const Buf ob(static_cast<char*>(p.out0) + wb, WB);
 #pragma unroll
          for(int q = 0; q < V; q++) ob.st2(r[q], lane_pos * 8u, q * T * 8);
+      }
+      if constexpr(TIMED) {
+         stamp(5);
+         const uint64_t rt1 = __builtin_amdgcn_s_memrealtime();
+         if(threadIdx.x == 0 && blockIdx.x < p.timing_groups) {
+            uint32_t* rec = p.timing + (size_t)blockIdx.x * TIMER_STRIDE;
+            rec[0] = __builtin_amdgcn_s_getreg((31 << 11) | 4);     // HW_REG_HW_ID
+            rec[1] = __builtin_amdgcn_s_getreg((31 << 11) | 20);    // HW_REG_XCC_ID
+            rec[2] = TIMER_MARKS;
+            rec[3] = (uint32_t)(rt1 - rt0);    // constant 100 MHz clock across the marks
+            rec[4] = (uint32_t)ts[0];
+            rec[5] = (uint32_t)(ts[0] >> 32);
+#pragma unroll
+            for(int i = 1; i <= TIMER_MARKS; i++) {
+               const uint64_t d = ts[i] - ts[0];
+               rec[5 + i] = ((uint32_t)i << 24) | (uint32_t)(d > 0xffffffull ? 0xffffffull : d);
+            }
+            rec[11] = 0;
+         }
       }
    }
 }
@@ -312,6 +349,18 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
       case K_C2C_FWD:   return launch_one<N, V, LAYOUT, K_C2C_FWD, MID_NONE>(p, s);
       case K_C2C_INV:   return launch_one<N, V, LAYOUT, K_C2C_INV, MID_NONE>(p, s);
       case K_PLAN_TAPS: return launch_one<N, V, LAYOUT, K_PLAN_TAPS, MID_NONE>(p, s);
+      case K_CONV_TIMED:
+         // the timed build exists for the default (padded) LDS layout only
+         if constexpr(LAYOUT == LAYOUT_PAD) {
+            switch(p.mid) {
+               case MID_MUL:  return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_MUL>(p, s);
+               case MID_CONJ: return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_CONJ>(p, s);
+               case MID_NONE: return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_NONE>(p, s);
+               default:       return hipErrorInvalidValue;
+            }
+         } else {
+            return hipErrorInvalidValue;
+         }
       default:        return hipErrorInvalidValue;
    }
 }

@@ -14,8 +14,17 @@ namespace fufft {
 // natural exchange; natural -> digit exchange + inverse DIT, unnormalised).
 // K_PLAN_TAPS: forward DIF of filter taps, times scale, stored in the filter
 // layout fl (digit order or lane-major).
+// K_CONV_TIMED: K_CONV with the phase timer (a timestamp after the load, the
+// forward DIF, the mid operation, the inverse DIT and the store).
 enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5,
-       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8 };
+       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9 };
+
+// phase timer record of one workgroup (K_CONV_TIMED), TIMER_STRIDE words:
+// [0] HW_ID, [1] XCC_ID, [2] marks, [3] s_memrealtime ticks (100 MHz) from
+// the first mark to the last, [4..5] start (s_memtime, lo / hi),
+// [6..10] one word per phase: phase id << 24 | cycles since start (saturated
+// at 2^24 - 1), phases 1 load, 2 forward, 3 mid, 4 inverse, 5 store
+enum { TIMER_STRIDE = 12, TIMER_MARKS = 5 };
 
 struct Conv1dParams {
    const void*   in0;      // complex input, or real x (K_CONV_R2)
@@ -31,6 +40,8 @@ struct Conv1dParams {
    int32_t       mid;      // MID_MUL / MID_CONJ / MID_NONE
    int32_t       fl;       // FLT_DR / FLT_LANE (filter read; K_PLAN_TAPS: layout written)
    float         scale;    // K_PLAN_TAPS: factor applied to the spectrum
+   uint32_t*     timing;   // K_CONV_TIMED: TIMER_STRIDE words per workgroup
+   uint32_t      timing_groups;   // workgroups that write a record
 };
 
 bool       conv1d_supported(int n, int v);

@@ -107,6 +107,36 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
                    void* out, int64_t n, int64_t batch, int mid, int variant,
                    int layout, void* stream);
 
+/* ---- in-kernel phase timer -----------------------------------------------------
+ * fufft_conv_f32 with a timestamp after each phase, for per-phase evidence of
+ * where a fused launch spends its time.  The reference's FUFFT_TIMER_* marks
+ * (fufft.cuh:86-176, K_LOAD / K_FWD / K_MULT / K_INV / K_STORE, %smid) as a
+ * separate entry point instead of a compile-time switch.  Each mark waits for
+ * the workgroup's outstanding memory operations and a workgroup barrier, then
+ * reads the shader clock (s_memtime), so the timed launch is slower than the
+ * untimed one; read proportions and confirm totals against fufft_conv_f32.
+ * The output is bit-identical to fufft_conv_f32.
+ * Workgroup g (transforms [g*tpw, (g+1)*tpw), tpw from
+ * fufft_transforms_per_workgroup) writes, for g < timing_groups, the
+ * FUFFT_TIMER_STRIDE words at timing + g*FUFFT_TIMER_STRIDE (device memory):
+ *   [0] HW_ID register of the wavefront that wrote the record (gfx9 layout:
+ *       wave [3:0], SIMD [5:4], CU [11:8], shader array and engine above),
+ *   [1] XCC_ID register (XCD [3:0]), [2] number of marks (5),
+ *   [3] ticks of the constant 100 MHz clock (s_memrealtime) from the start
+ *       to the last mark, so [10]'s cycles / ([3] / 100 MHz) is the shader
+ *       clock the workgroup ran at,
+ *   [4], [5] start time (s_memtime), low and high word,
+ *   [6 .. 10] phase << 24 | cycles since start (saturated at 2^24 - 1) for
+ *   phases 1 load, 2 forward DIF, 3 mid operation, 4 inverse DIT, 5 store.
+ * Padded LDS layout only (the default); a call that would need more than one
+ * launch (per-signal filters beyond 4 GiB) returns FUFFT_ERR_UNSUPPORTED. */
+#define FUFFT_TIMER_STRIDE 12
+int fufft_transforms_per_workgroup(int64_t n, int variant);
+int fufft_conv_timed_f32(const void* in, const void* filt, int64_t filt_stride,
+                         void* out, int64_t n, int64_t batch, int mid, int variant,
+                         int layout, uint32_t* timing, int64_t timing_groups,
+                         void* stream);
+
 /* ---- split path: one signal against many filters ----------------------------
  * fwd: natural-order signal -> digit-order spectrum (fufft_pipeline_fwd,
  * fufft.cuh:1343-1370).  apply: spectrum (spec_stride 0 = one spectrum for
