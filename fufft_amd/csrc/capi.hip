@@ -61,18 +61,23 @@ int lds_layout()
 }
 
 // Items (transforms, images) per sub-batch of the multi-launch paths (four-
-// step, 2D), for item_bytes per item.  A sub-batch of 256 MiB -- MI355X's
-// last-level (Infinity) cache -- keeps the data one launch writes resident for
-// the next launch: measured on the four-step N = 32768 path, 109 Gpt/s
-// without sub-batches, 130 at 256 MiB, 113-127 at 64/192/384/512 MiB, and
-// launch overhead dominates below 32 MiB.  FUFFT_SUBBATCH_MB overrides the
-// size; 0 disables sub-batching.
-int64_t subbatch_items(int64_t item_bytes, int64_t batch)
+// step, 2D), for item_bytes per item.  A sub-batch about the size of MI355X's
+// last-level (Infinity) cache, 256 MiB, keeps the data one launch writes
+// resident for the next launch.  Measured (Gpt/s or G px/s at 32 / 64 / 128 /
+// 192 / 256 MiB): four-step N = 32768 98 / 113 / 124 / 128 / 131 (109 without
+// sub-batches); 2D 512^2 two-for-one 170 / 197 / 214 / 210 / 201, whose
+// launches touch two arrays of the sub-batch's size (two real inputs and a
+// complex work array), so it runs at 128 MiB.  FUFFT_SUBBATCH_MB overrides
+// both; 0 disables sub-batching.
+enum { SUBBATCH_FOURSTEP_MB = 256, SUBBATCH_2D_MB = 128 };
+
+int64_t subbatch_items(int64_t item_bytes, int64_t batch, int64_t default_mb)
 {
-   static const int64_t mb = [] {
+   static const int64_t env_mb = [] {
       const char* e = std::getenv("FUFFT_SUBBATCH_MB");
-      return e ? (int64_t)std::atoll(e) : (int64_t)256;
+      return e ? (int64_t)std::atoll(e) : (int64_t)-1;
    }();
+   const int64_t mb = env_mb >= 0 ? env_mb : default_mb;
    if(mb <= 0) return batch > 0 ? batch : 1;
    const int64_t items = (mb << 20) / item_bytes;
    return items > 0 ? items : 1;
@@ -699,7 +704,7 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
    hipStream_t s = static_cast<hipStream_t>(stream);
    // The three stages run over sub-batches small enough for the data to stay
    // in the last-level cache from one stage to the next.
-   const int64_t sub = subbatch_items(n * 8, batch);
+   const int64_t sub = subbatch_items(n * 8, batch, SUBBATCH_FOURSTEP_MB);
    for(int64_t t0 = 0; t0 < batch; t0 += sub) {
       const int64_t nb = batch - t0 < sub ? batch - t0 : sub;
       float2* a = static_cast<float2*>(buf) + t0 * n;
@@ -874,7 +879,7 @@ int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride, void
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
    hipStream_t s = static_cast<hipStream_t>(stream);
-   const int64_t np = h * w, sub = subbatch_items(np * 8, batch);
+   const int64_t np = h * w, sub = subbatch_items(np * 8, batch, SUBBATCH_2D_MB);
    for(int64_t i0 = 0; i0 < batch; i0 += sub) {
       const int64_t nb = batch - i0 < sub ? batch - i0 : sub;
       const char* src = static_cast<const char*>(in) + i0 * np * 8;
@@ -913,7 +918,7 @@ int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt, int64_
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
    hipStream_t s = static_cast<hipStream_t>(stream);
-   const int64_t np = h * w, sub = subbatch_items(np * 8, batch);
+   const int64_t np = h * w, sub = subbatch_items(np * 8, batch, SUBBATCH_2D_MB);
    for(int64_t i0 = 0; i0 < batch; i0 += sub) {
       const int64_t nb = batch - i0 < sub ? batch - i0 : sub;
       char* wk = static_cast<char*>(work) + i0 * np * 8;
@@ -945,7 +950,7 @@ int fufft_fwd2d_f32(const void* in, void* spec, int64_t h, int64_t w, int64_t ba
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
-   const int64_t np = h * w, sub = subbatch_items(np * 8, batch);
+   const int64_t np = h * w, sub = subbatch_items(np * 8, batch, SUBBATCH_2D_MB);
    for(int64_t i0 = 0; i0 < batch; i0 += sub) {
       const int64_t nb = batch - i0 < sub ? batch - i0 : sub;
       char* dst = static_cast<char*>(spec) + i0 * np * 8;
@@ -977,7 +982,7 @@ int fufft_apply2d_f32(const void* spec, int64_t spec_stride, const void* filt, i
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
-   const int64_t sub = subbatch_items(np * 8, batch);
+   const int64_t sub = subbatch_items(np * 8, batch, SUBBATCH_2D_MB);
    for(int64_t i0 = 0; i0 < batch; i0 += sub) {
       const int64_t nb = batch - i0 < sub ? batch - i0 : sub;
       char* dst = static_cast<char*>(out) + i0 * np * 8;

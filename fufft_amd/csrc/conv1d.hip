@@ -20,7 +20,6 @@
 #include "fufft_plan.hpp"
 #include "fufft_internal.hpp"
 
-#include <cstdlib>
 
 namespace fufft {
 
@@ -183,110 +182,6 @@ conv1d_kernel(const Conv1dParams p)
    }
 }
 
-// Persistent variant of K_CONV: a fixed grid of workgroups walks the batch,
-// and while one transform is in the FFT passes the next one's signal is
-// already on its way into registers.  The loop needs no barrier between
-// transforms: DIF pass 0 scatters exactly the LDS positions the same lane
-// gathered in the previous transform's last DIT pass.
-template<int N, int V, int LAYOUT, int MID>
-__global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
-conv1d_persistent(const Conv1dParams p)
-{
-   using PL = Plan<N, V>;
-   using LD = Lds<V, LAYOUT>;
-   constexpr int T     = PL::T;
-   constexpr int CPB   = cpb_for(T);
-   constexpr int SLOT  = LD::size(N);
-   constexpr int LANES = T < 64 ? 64 : T;
-   constexpr int TPW   = T < 64 ? 64 / T : 1;
-
-   extern __shared__ float2 lds[];
-   const int slot = threadIdx.x / T;
-   const int L    = threadIdx.x % T;
-   const uint32_t stride = gridDim.x * CPB;
-   uint32_t t = blockIdx.x * CPB + slot;
-   if(t >= p.ntrans) return;
-
-   const uint32_t wave_first = (T >= 64) ? 0u : (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
-   float2* A = lds + slot * SLOT;
-   Twiddles<PL> tw;
-   tw.load(p.tw, L);
-   const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
-   const uint32_t fl_off = (p.fl == FLT_DR ? L * V : L) * 8u;
-   const uint32_t fl_step = (p.fl == FLT_DR ? 1 : T) * 8u;
-
-   // the wavefront's first transform of an iteration is uniform; t - t0 is
-   // this lane's offset from it
-   auto wave_t0 = [&](uint32_t tt) -> uint32_t {
-      return (T >= 64) ? (uint32_t)uniform((int)tt) : (tt - slot) + wave_first;
-   };
-
-   float2 pf[V];
-   {
-      const uint32_t t0 = wave_t0(t);
-      const Buf xb(static_cast<const char*>(p.in0) + (size_t)t0 * N * 8, TPW * N * 8);
-      const uint32_t lo = ((t - t0) * N + L) * 8u;
-#pragma unroll
-      for(int q = 0; q < V; q++) pf[q] = xb.ld2(lo, q * T * 8);
-   }
-   while(true) {
-      // Opaque copies of the lane index and base twiddles: without them the
-      // compiler hoists every twiddle chain and LDS address out of the loop
-      // and keeps them live across transforms, which costs ~120 VGPRs.
-      int Li = L;
-      asm volatile("" : "+v"(Li));
-      Twiddles<PL> twi = tw;
-#pragma unroll
-      for(int i = 0; i < Twiddles<PL>::COUNT; i++) asm volatile("" : "+v"(twi.w[i].x), "+v"(twi.w[i].y));
-      float2 r[V];
-#pragma unroll
-      for(int q = 0; q < V; q++) r[q] = pf[q];
-      const uint32_t tn = t + stride;
-      if(tn < p.ntrans) {
-         const uint32_t t0 = wave_t0(tn);
-         const Buf xb(static_cast<const char*>(p.in0) + (size_t)t0 * N * 8, TPW * N * 8);
-         const uint32_t lo = ((tn - t0) * N + L) * 8u;
-#pragma unroll
-         for(int q = 0; q < V; q++) pf[q] = xb.ld2(lo, q * T * 8);
-      }
-      forward_dif<PL, LD, LANES>(r, A, Li, twi);
-      mid_op<PL, MID>(r, fb, (t % p.fcount) * N * 8u + fl_off, fl_step);
-      inverse_dit<PL, LD, LANES>(r, A, Li, twi);
-      {
-         const uint32_t t0 = wave_t0(t);
-         const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
-         const uint32_t lo = ((t - t0) * N + L) * 8u;
-#pragma unroll
-         for(int q = 0; q < V; q++) ob.st2(r[q], lo, q * T * 8);
-      }
-      if(tn >= p.ntrans) break;
-      t = tn;
-   }
-}
-
-template<int N, int V, int LAYOUT, int MID>
-static hipError_t launch_persistent(const Conv1dParams& p, hipStream_t s)
-{
-   constexpr int T = N / V, CPB = cpb_for(T);
-   const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
-   const void* k = reinterpret_cast<const void*>(&conv1d_persistent<N, V, LAYOUT, MID>);
-   if(shm > 65536) {
-      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-      if(e != hipSuccess) return e;
-   }
-   int per_cu = 0, dev = 0, cus = 0;
-   hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, CPB * T, shm);
-   if(e != hipSuccess) return e;
-   if((e = hipGetDevice(&dev)) != hipSuccess) return e;
-   if((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-   const uint32_t groups = (p.ntrans + CPB - 1) / CPB;
-   const uint32_t cap = (uint32_t)(per_cu > 0 ? per_cu : 1) * (uint32_t)cus;
-   const dim3 grid(groups < cap ? groups : cap), block(CPB * T);
-   Conv1dParams arg = p;
-   void* argv[] = { &arg };
-   return hipLaunchKernel(k, grid, block, argv, shm, s);
-}
-
 template<int N, int V, int LAYOUT, int KIND, int MID>
 static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
 {
@@ -303,28 +198,9 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
    return hipLaunchKernel(k, grid, block, argv, shm, s);
 }
 
-int persistent_mode()
-{
-   static const int mode = [] {
-      const char* e = std::getenv("FUFFT_PERSISTENT");
-      return (e && e[0] == '1') ? 1 : 0;
-   }();
-   return mode;
-}
-
 template<int N, int V, int LAYOUT, int KIND>
 static hipError_t launch_mid(const Conv1dParams& p, hipStream_t s)
 {
-   if constexpr(KIND == K_CONV) {
-      if(persistent_mode()) {
-         switch(p.mid) {
-            case MID_MUL:  return launch_persistent<N, V, LAYOUT, MID_MUL>(p, s);
-            case MID_CONJ: return launch_persistent<N, V, LAYOUT, MID_CONJ>(p, s);
-            case MID_NONE: return launch_persistent<N, V, LAYOUT, MID_NONE>(p, s);
-            default:       return hipErrorInvalidValue;
-         }
-      }
-   }
    switch(p.mid) {
       case MID_MUL:  return launch_one<N, V, LAYOUT, KIND, MID_MUL>(p, s);
       case MID_CONJ: return launch_one<N, V, LAYOUT, KIND, MID_CONJ>(p, s);

@@ -1,0 +1,96 @@
+"""Static checks of this build's own gfx950 code (fufft_amd/isa_report.py).
+
+- No kernel of the library spills registers or uses scratch.
+- The analytic operation model (fp32 arithmetic, LDS traffic and
+  vector-memory instructions per pass plan) matches the compiled kernels:
+  the kernels are straight-line code, so static counts are what each
+  wavefront executes (plus the untaken side of the filter-layout branch).
+- The same counts match what rocprofv3 measured per wavefront for the
+  headline kernel (profiles/conv_f32_n4096.md): model, ISA and hardware
+  counters agree.
+- Occupancy: radix-8 lanes give 8 wavefronts per SIMD where radix-16 lanes
+  are held to 4 by LDS -- the reason FUFFT_AUTO picks radix 8.
+"""
+import re
+from pathlib import Path
+
+import pytest
+
+from fufft_amd import isa_report as R
+
+ROOT = Path(__file__).resolve().parent.parent
+pytestmark = pytest.mark.skipif(not R.tools_available() or not list(R.OBJ.glob("*.o")),
+                                reason="needs this build's objects and the ROCm LLVM tools")
+
+
+@pytest.fixture(scope="module")
+def rows():
+    return R.load()
+
+
+@pytest.fixture(scope="module")
+def conv(rows):
+    return R.conv_rows(rows)
+
+
+def pick(conv, kind, n, v, layout="pad", mid="mul"):
+    got = [r for r in conv if r["family"] == "conv1d" and r["kind"] == kind and r["n"] == n and r["v"] == v
+           and r["layout"] == layout and r["mid"] == mid]
+    assert len(got) == 1, (kind, n, v)
+    return got[0]
+
+
+SIZES = [(n, 16) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + [(n, 8) for n in (512, 1024, 2048, 4096, 8192)]
+
+
+def test_no_kernel_spills_or_uses_scratch(rows):
+    """Every kernel of the default (padded) LDS layout is spill-free.  The
+    opt-in XOR layout (FUFFT_LDS_LAYOUT=xor) keeps one address register per
+    tap; at N = 16384 (1024 threads, so at most 128 VGPRs) it spills, which is
+    one more reason the padded layout is the default."""
+    assert len(rows) > 100
+    bad, xor16k = [], []
+    for r in rows:
+        m = r["meta"]
+        if m.get("private_segment_fixed_size", 0) or m.get("vgpr_spill_count", 0) or m.get("sgpr_spill_count", 0):
+            d = r["decoded"]
+            (xor16k if d and d["layout"] == "xor" and d["n"] == 16384 else bad).append(r["name"])
+    assert not bad, bad[:3]
+    assert len(xor16k) <= 8
+
+
+@pytest.mark.parametrize("n,v", SIZES)
+@pytest.mark.parametrize("kind,mid", [("conv", "mul"), ("conv", "conj"), ("c2c_fwd", "none"),
+                                      ("c2c_inv", "none"), ("plan_taps", "none"), ("fwd", "none")])
+def test_model_matches_compiled_kernel(conv, n, v, kind, mid):
+    r = pick(conv, kind, n, v, mid=mid)
+    m = r["model"]
+    # the compiler may fold a few products into constants, never add arithmetic
+    assert 0.985 * m["fp32_arith_per_lane"] <= r["fp32_arith"] <= m["fp32_arith_per_lane"], r
+    assert r["lds_access_8B"] == m["lds_access_8B_per_lane"], r
+    assert r["vmem_load"] == m["vmem_loads_per_wave"] + m["untaken_branch"]["loads"], r
+    assert r["vmem_store"] == m["vmem_stores_per_wave"] + m["untaken_branch"]["stores"], r
+
+
+def test_occupancy_radix8_vs_radix16(conv):
+    for n in (512, 1024, 2048, 4096, 8192):
+        assert pick(conv, "conv", n, 8)["waves_per_simd"] == 8, n
+    r16 = pick(conv, "conv", 4096, 16)
+    assert r16["waves_per_simd"] == 4 and r16["limited_by"] == "LDS"
+
+
+def test_counters_agree_with_model_and_isa(conv):
+    """profiles/conv_f32_n4096.md: SQ_INSTS_VALU, SQ_INSTS_LDS and SQ_INSTS_VMEM
+    per wavefront of conv1d_kernel<4096, 8, pad, conv, mul>."""
+    text = (ROOT / "profiles" / "conv_f32_n4096.md").read_text()
+
+    def per_wave(counter):
+        m = re.search(rf"\|\s*{counter}\s*\|\s*\d+\s*\|\s*([0-9.]+)\s*\|", text)
+        assert m, counter
+        return float(m.group(1))
+
+    r = pick(conv, "conv", 4096, 8)
+    m = r["model"]
+    assert abs(per_wave("SQ_INSTS_VALU") - r["valu"]) <= 2
+    assert per_wave("SQ_INSTS_LDS") == r["lds"]
+    assert per_wave("SQ_INSTS_VMEM") == m["vmem_loads_per_wave"] + m["vmem_stores_per_wave"]
