@@ -125,17 +125,19 @@ bfp_kernel(const BfpParams p)
    Twiddles<PL> tw;
    tw.load(p.tw, L);
 
-   // this wavefront's V input exponents: block w + q*T/64 of transform t
-   const Buf eb(p.ein + (size_t)tu * NB, NB);
-   const int my_e = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(
-      eb.r, (uint32_t)(w + (lane < V ? lane : 0) * (T / 64)), 0, 0);
+   // this wavefront's V input exponents, blocks w + q*T/64 of transform t: the
+   // address is uniform and nothing in the kernel has stored yet, so these are
+   // scalar loads (dwords of the transform's NB exponent bytes, 4-byte aligned
+   // by the entry point's contract) and the bytes are picked apart in SALU
+   const uint32_t* ew = reinterpret_cast<const uint32_t*>(p.ein) + (size_t)tu * (NB / 4);
 
    const Buf qb(static_cast<const char*>(p.qin) + (size_t)tu * N * 4, N * 4);
    float2 r[V];
 #pragma unroll
    for(int q = 0; q < V; q++) {
       const uint32_t word = qb.ldu((uint32_t)L * 4u, q * T * 4);
-      const int e = __builtin_amdgcn_readlane(my_e, q);
+      const int byte = w + q * (T / 64);
+      const int e = (int)(int8_t)(ew[byte >> 2] >> (8 * (byte & 3)));
       r[q] = make_float2(__builtin_amdgcn_ldexpf((float)(int)(int16_t)(word & 0xffffu), e),
                          __builtin_amdgcn_ldexpf((float)((int)word >> 16), e));
    }
@@ -155,17 +157,38 @@ bfp_kernel(const BfpParams p)
       m[q] = __builtin_bit_cast(uint32_t, __builtin_fmaxf(__builtin_fabsf(r[q].x), __builtin_fabsf(r[q].y)));
    const int e_lane = bfp_exponent_bits(block_maxima<V>(m, (uint32_t)lane));   // block lane % V
    const Buf ob(static_cast<char*>(p.qout) + (size_t)tu * N * 4, N * 4);
+   int eq[V];
+   int emin = 127;
 #pragma unroll
    for(int q = 0; q < V; q++) {
-      const int e = __builtin_amdgcn_readlane(e_lane, q);
-      // adding 1.5 * 2^23 rounds |v| < 2^22 to the nearest integer, ties to
-      // even (= rint), and leaves it in the low mantissa bits
-      const float yr = __builtin_amdgcn_ldexpf(r[q].x, -e) + 12582912.0f;
-      const float yi = __builtin_amdgcn_ldexpf(r[q].y, -e) + 12582912.0f;
-      // low halfwords of yr (bytes 0-1) and yi (bytes 4-5 of {yi, yr}) -> {im, re}
+      eq[q] = __builtin_amdgcn_readlane(e_lane, q);
+      emin = eq[q] < emin ? eq[q] : emin;
+   }
+   // low halfwords of yr (bytes 0-1) and yi (bytes 4-5 of {yi, yr}) -> {im, re}
+   auto store = [&](int q, float yr, float yi) {
       const uint32_t word = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, yi),
                                                   __builtin_bit_cast(uint32_t, yr), 0x05040100u);
       ob.stu(word, (uint32_t)L * 4u, q * T * 4);
+   };
+   // Adding 1.5 * 2^23 rounds |v| < 2^22 to the nearest integer, ties to even
+   // (= rint), and leaves it in the low mantissa bits.  With the exact scale
+   // 2^-e as a float (127 - e in [1, 254]; e is at most 114 for a finite
+   // block) one fma does both steps: v * 2^-e is exact, so rounding
+   // v * 2^-e + 1.5 * 2^23 once equals rounding ldexp(v, -e) + 1.5 * 2^23 (a
+   // product below 2^-126 rounds to q = 0 either way).  e = -128 has no float
+   // 2^128: a wavefront with such a block takes the two-step form for all of
+   // its registers (the branch is uniform).
+   if(emin > -128) {
+#pragma unroll
+      for(int q = 0; q < V; q++) {
+         const float sc = __builtin_bit_cast(float, (uint32_t)(127 - eq[q]) << 23);
+         store(q, __builtin_fmaf(r[q].x, sc, 12582912.0f), __builtin_fmaf(r[q].y, sc, 12582912.0f));
+      }
+   } else {
+#pragma unroll
+      for(int q = 0; q < V; q++)
+         store(q, __builtin_amdgcn_ldexpf(r[q].x, -eq[q]) + 12582912.0f,
+               __builtin_amdgcn_ldexpf(r[q].y, -eq[q]) + 12582912.0f);
    }
    if(lane < V) {
       const Buf xb(p.eout + (size_t)tu * NB, NB);

@@ -526,7 +526,9 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
    if(batch < 0 || batch > 0xffffffffll) return FUFFT_ERR_INVALID;
    if(!pow2(n) || n > 16384 || !bfp_supported((int)n, v)) return FUFFT_ERR_UNSUPPORTED;
    if(!qin || !ein || !qout || !eout || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
-   if(!aligned4(qin) || !aligned4(qout) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
+   // exponents are read as aligned dwords through the scalar cache
+   if(!aligned4(qin) || !aligned4(qout) || !aligned4(ein) || !aligned4(eout) || (filt && !aligned16(filt)))
+      return FUFFT_ERR_ALIGN;
    BfpParams p{};
    int st;
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;

@@ -212,7 +212,7 @@ int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float*
  * qin / qout: n*batch points (4 bytes each); ein / eout: n*batch/64 exponents;
  * filt: fp32 filter planned for the same variant.  Needs n/V >= 64 lanes:
  * FUFFT_R8 512..8192, FUFFT_V16 1024..16384.  qin == qout and ein == eout are
- * allowed. */
+ * allowed.  qin, qout, ein and eout must be 4-byte aligned (FUFFT_ERR_ALIGN). */
 int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
                      int64_t filt_stride, void* qout, int8_t* eout, int64_t n,
                      int64_t batch, int mid, int variant, int layout, void* stream);
