@@ -142,13 +142,14 @@ bfp_kernel(const BfpParams p)
                          __builtin_amdgcn_ldexpf((float)((int)word >> 16), e));
    }
 
-   forward_dif<PL, LD, (T < 64 ? 64 : T)>(r, A, L, tw);
+   KeptChain<PL> kc;
+   forward_dif<PL, LD, (T < 64 ? 64 : T), 64, KEEP_STORE>(r, A, L, tw, kc);
    {
       const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
       const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
       mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
    }
-   inverse_dit<PL, LD, (T < 64 ? 64 : T)>(r, A, L, tw);
+   inverse_dit<PL, LD, (T < 64 ? 64 : T), 64, KEEP_USE>(r, A, L, tw, kc);
 
    // quantise: register q of this wavefront is block w + q*T/64
    uint32_t m[V];

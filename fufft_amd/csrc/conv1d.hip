@@ -76,6 +76,10 @@ conv1d_kernel(const Conv1dParams p)
    if constexpr(TIMED) rt0 = __builtin_amdgcn_s_memrealtime();
    Twiddles<PL> tw;
    tw.load(p.tw, L);
+   // both halves in this launch: the forward's last twiddled chain serves the inverse
+   constexpr int KEEP_F = (KIND == K_CONV || KIND == K_CONV_R2 || TIMED) ? KEEP_STORE : KEEP_NONE;
+   constexpr int KEEP_I = KEEP_F == KEEP_STORE ? KEEP_USE : KEEP_NONE;
+   KeptChain<PL> kc;
    float2 r[V];
 
    if constexpr(FROM_SPEC) {
@@ -104,7 +108,7 @@ conv1d_kernel(const Conv1dParams p)
       }
       stamp(1);
       if constexpr(C2C_INV) natural_to_digit<PL, LD, LANES, true>(r, A, L);
-      else                  forward_dif<PL, LD, LANES>(r, A, L, tw);
+      else                  forward_dif<PL, LD, LANES, 64, KEEP_F>(r, A, L, tw, kc);
       stamp(2);
    }
 
@@ -142,7 +146,7 @@ conv1d_kernel(const Conv1dParams p)
          mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
       }
       stamp(3);
-      inverse_dit<PL, LD, LANES>(r, A, L, tw);
+      inverse_dit<PL, LD, LANES, 64, KEEP_I>(r, A, L, tw, kc);
       stamp(4);
 
       const size_t wb = (size_t)t0 * N * EL_OUT;

@@ -48,6 +48,9 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
    float2* A = lds + col * SLOTC;
    Twiddles<PL> tw;
    tw.load(p.tw, L);
+   constexpr int KEEP_F = KIND == COL_CONV ? KEEP_STORE : KEEP_NONE;
+   constexpr int KEEP_I = KIND == COL_CONV ? KEEP_USE : KEEP_NONE;
+   KeptChain<PL> kc;
    float2 r[V];
 
    if constexpr(KIND == COL_APPLY) {
@@ -58,7 +61,7 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
       const Buf ib(static_cast<const char*>(p.in) + (size_t)img * ibytes, ibytes);
 #pragma unroll
       for(int q = 0; q < V; q++) r[q] = ib.ld2(nat, q * T * W8);
-      forward_dif<PL, LD, C * T, 64 / C>(r, A, L, tw);
+      forward_dif<PL, LD, C * T, 64 / C, KEEP_F>(r, A, L, tw, kc);
    }
 
    const Buf ob(static_cast<char*>(p.out) + (size_t)img * ibytes, ibytes);
@@ -70,7 +73,7 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
          const Buf fb(static_cast<const char*>(p.filt) + (size_t)(img % p.fcount) * ibytes, ibytes);
          mid_op<PL, MID>(r, fb, dro, W8);
       }
-      inverse_dit<PL, LD, C * T, 64 / C>(r, A, L, tw);
+      inverse_dit<PL, LD, C * T, 64 / C, KEEP_I>(r, A, L, tw, kc);
 #pragma unroll
       for(int q = 0; q < V; q++) ob.st2(r[q], nat, q * T * W8);
    }

@@ -194,6 +194,27 @@ __device__ __forceinline__ void tw_single(float2 (&r)[NR], float2 w1)
    for(int k = 2; k < R; k++) { w = cmul(w, w1); r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], w); }
 }
 
+// the single chain that also hands back the powers it generated, w[k] = W^(jk)
+template<int R, int OFF, int STRIDE, int NR>
+__device__ __forceinline__ void tw_single_keep(float2 (&r)[NR], float2 w1, float2 (&w)[R])
+{
+   w[1] = w1;
+   r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w1);
+#pragma unroll
+   for(int k = 2; k < R; k++) { w[k] = cmul(w[k - 1], w1); r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], w[k]); }
+}
+
+// Multiply by the conjugates of powers a forward chain generated.  The forward
+// chain runs on conj(W^j), the inverse's on W^j, and a product of conjugates
+// is the conjugate of the product bit for bit (each fma only changes sign), so
+// conj(w[k]) equals the inverse chain's W^(jk) exactly.
+template<int R, int OFF, int STRIDE, int NR>
+__device__ __forceinline__ void tw_kept_conj(float2 (&r)[NR], const float2 (&w)[R])
+{
+#pragma unroll
+   for(int k = 1; k < R; k++) r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], make_float2(w[k].x, -w[k].y));
+}
+
 // radix 16: even outputs by (W^2)^m, odd by W (W^2)^m -- two 7-step chains
 // (fufft.cuh:701-720)
 template<int OFF, int STRIDE, int NR>

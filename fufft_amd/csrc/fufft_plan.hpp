@@ -178,19 +178,50 @@ struct Twiddles {
    }
 };
 
+// Stage twiddles carried from the forward DIF to the inverse DIT.  The
+// forward's last twiddled pass (NP - 2: the last pass runs at M = 1) and the
+// inverse's first twiddled pass are the same pass -- same lanes, same groups,
+// same W^j -- and only the mid operation and the M = 1 butterflies lie between
+// them, so the chain the forward pass generated is kept in registers and the
+// inverse pass reads its conjugates instead of rebuilding it (R - 2 complex
+// products per group).  Done for radix-8 lanes (one group per lane, 7 powers),
+// which run at 8 wavefronts per SIMD with VGPRs to spare for the short live
+// range.  Results are unchanged bit for bit (tw_kept_conj).  Only for pure
+// powers of 8: there the kernels stay within 64 VGPRs (8 wavefronts per SIMD);
+// with a leading radix-2/4 pass (N = 1024, 2048, 8192) the kept chain pushed
+// them to 66-74 VGPRs, i.e. 6-7 wavefronts, which costs more than it saves.
+template<class PL>
+struct KeptChain {
+   static constexpr int P = PL::NP >= 2 ? PL::NP - 2 : 0;
+   static constexpr int R = PL::radix(P);
+   static constexpr bool enabled = PL::NP >= 2 && PL::V == 8 && PL::LEAD == 1 && R == 8 && PL::stride(P) > 1;
+   float2 w[enabled ? R : 1];
+};
+
+// KEEP: 0 plain; 1 forward pass that stores its chain in kc; 2 inverse pass
+// that applies conj(kc)
+enum { KEEP_NONE = 0, KEEP_STORE = 1, KEEP_USE = 2 };
+
 // Butterflies + stage twiddles of pass P for all groups of the lane.
-template<class PL, int P, int SIGN, bool DIT>
-__device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<PL>& tw)
+template<class PL, int P, int SIGN, bool DIT, int KEEP = KEEP_NONE>
+__device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<PL>& tw, KeptChain<PL>& kc)
 {
    constexpr int R = PL::radix(P), M = PL::stride(P), G = PL::V / R;
+   constexpr bool keep = KeptChain<PL>::enabled && P == KeptChain<PL>::P && KEEP != KEEP_NONE;
    static_for<G>([&](auto gi) {
       constexpr int g = decltype(gi)::value;
       if constexpr(M > 1) {
          const float2 b = tw.w[Twiddles<PL>::slots_before(P) + g];
          const float2 w1 = SIGN < 0 ? make_float2(b.x, -b.y) : b;
-         if constexpr(DIT) twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
+         if constexpr(DIT) {
+            if constexpr(keep && KEEP == KEEP_USE) tw_kept_conj<R, g, G>(r, kc.w);
+            else                                   twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
+         }
          dftR<R, SIGN, g, G>(r);
-         if constexpr(!DIT) twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
+         if constexpr(!DIT) {
+            if constexpr(keep && KEEP == KEEP_STORE) tw_single_keep<R, g, G>(r, w1, kc.w);
+            else                                     twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
+         }
       } else {
          dftR<R, SIGN, g, G>(r);
       }
@@ -224,28 +255,46 @@ __device__ __forceinline__ void exchange_sync()
 
 // Forward DIF of the lane's registers: r holds positions L + q*T on entry and
 // the digit-order spectrum positions L*V + k on exit (last pass at M = 1).
-template<class PL, class LD, int LANES, int WL = 64>
-__device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
+// With kc, the last twiddled pass leaves its chain there for inverse_dit.
+template<class PL, class LD, int LANES, int WL = 64, int KEEP = KEEP_NONE>
+__device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw,
+                                            KeptChain<PL>& kc)
 {
    static_for<PL::NP>([&](auto pi) {
       constexpr int p = decltype(pi)::value;
       if constexpr(p > 0) { exchange_sync<PL, p - 1, LANES, WL>(); lds_gather<PL, p, LD>(r, A, L); }
-      compute_pass<PL, p, -1, false>(r, tw);
+      compute_pass<PL, p, -1, false, KEEP>(r, tw, kc);
       if constexpr(p < PL::NP - 1) lds_scatter<PL, p, LD>(r, A, L);
    });
 }
 
-// Inverse DIT: r holds spectrum positions L*V + k on entry and natural-order
-// positions L + q*T on exit.
 template<class PL, class LD, int LANES, int WL = 64>
-__device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
+__device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
+{
+   KeptChain<PL> none;
+   forward_dif<PL, LD, LANES, WL, KEEP_NONE>(r, A, L, tw, none);
+}
+
+// Inverse DIT: r holds spectrum positions L*V + k on entry and natural-order
+// positions L + q*T on exit.  With kc, the first twiddled pass applies the
+// chain forward_dif kept.
+template<class PL, class LD, int LANES, int WL = 64, int KEEP = KEEP_NONE>
+__device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw,
+                                            KeptChain<PL>& kc)
 {
    static_for<PL::NP>([&](auto qi) {
       constexpr int p = PL::NP - 1 - decltype(qi)::value;
       if constexpr(p < PL::NP - 1) lds_gather<PL, p, LD>(r, A, L);
-      compute_pass<PL, p, +1, true>(r, tw);
+      compute_pass<PL, p, +1, true, KEEP>(r, tw, kc);
       if constexpr(p > 0) { lds_scatter<PL, p, LD>(r, A, L); exchange_sync<PL, p - 1, LANES, WL>(); }
    });
+}
+
+template<class PL, class LD, int LANES, int WL = 64>
+__device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L, const Twiddles<PL>& tw)
+{
+   KeptChain<PL> none;
+   inverse_dit<PL, LD, LANES, WL, KEEP_NONE>(r, A, L, tw, none);
 }
 
 // ---- digit order <-> natural order through LDS ------------------------------------------
