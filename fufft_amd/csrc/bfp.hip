@@ -203,10 +203,8 @@ static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
    constexpr int T = N / V, CPB = bfp_cpb(T);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
    const void* k = reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID>);
-   if(shm > 65536) {
-      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-      if(e != hipSuccess) return e;
-   }
+   static std::atomic<uint64_t> lds_ok{0};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
    BfpParams arg = p;
    void* argv[] = { &arg };

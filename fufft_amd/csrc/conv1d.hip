@@ -192,10 +192,8 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
    constexpr int T = N / V, CPB = cpb_for(T);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
    const void* k = reinterpret_cast<const void*>(&conv1d_kernel<N, V, LAYOUT, KIND, MID>);
-   if(shm > 65536) {
-      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-      if(e != hipSuccess) return e;
-   }
+   static std::atomic<uint64_t> lds_ok{0};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
    Conv1dParams arg = p;
    void* argv[] = { &arg };

@@ -86,10 +86,8 @@ static hipError_t launch_col_one(const ColParams& p, hipStream_t s)
    constexpr int SLOTC = Lds<V, LAYOUT_PAD>::size(H) + 32 / C;
    const size_t shm = (size_t)C * SLOTC * sizeof(float2);
    const void* k = reinterpret_cast<const void*>(&col_kernel<H, V, LAYOUT_PAD, KIND, MID, C>);
-   if(shm > 65536) {
-      const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-      if(e != hipSuccess) return e;
-   }
+   static std::atomic<uint64_t> lds_ok{0};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    if(p.w % C || p.fcount == 0 || p.scount == 0) return hipErrorInvalidValue;
    const uint64_t blocks = (uint64_t)p.nimg * (p.w / C);
    if(blocks > 0x7fffffffu) return hipErrorInvalidValue;

@@ -5,7 +5,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace fufft {
+
+// Dynamic LDS above 64 KiB must be allowed per kernel (and per device) before
+// a launch.  Done once per (kernel, device) -- mask holds one bit per device
+// -- so repeated launches, including launches under stream capture, make no
+// attribute call.
+inline hipError_t ensure_dynamic_lds(const void* kernel, size_t bytes, std::atomic<uint64_t>& mask)
+{
+   if(bytes <= 65536) return hipSuccess;
+   int dev = 0;
+   const hipError_t g = hipGetDevice(&dev);
+   if(g != hipSuccess) return g;
+   const uint64_t bit = 1ull << (dev & 63);
+   if(mask.load(std::memory_order_acquire) & bit) return hipSuccess;
+   const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+   if(e == hipSuccess) mask.fetch_or(bit, std::memory_order_acq_rel);
+   return e;
+}
 
 // ---- 1D fused pipeline (conv1d.hip) ------------------------------------------------
 // K_FWD_R2 / K_APPLY_R2: the forward half reading two real arrays, the
