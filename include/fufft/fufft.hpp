@@ -112,6 +112,29 @@ inline int plan_filter_device(const void* natural, void* planned, int64_t n, int
                                        fold_inv_n ? 1 : 0, stream);
 }
 
+// the reference's FUFFT_TIMER_* in-kernel phase marks (fufft.cuh:86-176) around a fused conv:
+// timing receives FUFFT_TIMER_STRIDE words per workgroup for the first timing_groups workgroups
+template<class Mid = MidMultiply>
+inline int pipeline_timed(const void* in, const void* filt, void* out, int64_t n, int64_t batch,
+                          uint32_t* timing, int64_t timing_groups, void* stream = nullptr,
+                          int64_t filt_stride = 0, Variant v = Variant::Auto, int layout = FUFFT_LAYOUT_DR)
+{
+   return fufft_conv_timed_f32(in, filt, filt_stride, out, n, batch, Mid::id, (int)v, layout, timing,
+                               timing_groups, stream);
+}
+
+inline int plan_filter_large_device(const void* natural, void* planned, int64_t n, int64_t count = 1,
+                                    void* stream = nullptr, int kind = FUFFT_FILTER_TAPS, bool fold_inv_n = true)
+{
+   return fufft_plan_filter_large_device_f32(natural, planned, n, count, kind, fold_inv_n ? 1 : 0, stream);
+}
+
+inline int plan_filter2d_device(const void* natural, void* planned, int64_t h, int64_t w, int64_t count = 1,
+                                void* stream = nullptr, int kind = FUFFT_FILTER_TAPS, bool fold_inv_n = true)
+{
+   return fufft_plan_filter2d_device_f32(natural, planned, h, w, count, kind, fold_inv_n ? 1 : 0, stream);
+}
+
 // ---- four-step (run_large, bench_fufft.cu:357-492) ----------------------------------------
 
 template<class Mid = MidMultiply>

@@ -23,6 +23,10 @@ int main()
    if(!fufft::supported(n) || fufft::supported(100)) return 7;
    if(fufft::c2c<FUFFT_INVERSE>(nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID) return 8;
    if(fufft::plan_filter_device(nullptr, nullptr, n) != FUFFT_ERR_INVALID) return 9;
+   if(fufft::pipeline_timed<fufft::MidMultiply>(nullptr, nullptr, nullptr, n, 1, nullptr, 0) != FUFFT_ERR_INVALID) return 10;
+   if(fufft::plan_filter_large_device(nullptr, nullptr, 4096) != FUFFT_ERR_UNSUPPORTED) return 11;
+   if(fufft::plan_filter2d_device(nullptr, nullptr, 512, 512) != FUFFT_ERR_INVALID) return 12;
+   if(fufft_transforms_per_workgroup(4096, FUFFT_R8) != 1 || fufft_transforms_per_workgroup(512, FUFFT_R8) != 4) return 13;
    std::printf("ok %s\n", fufft::status_string(FUFFT_OK));
    return 0;
 }
