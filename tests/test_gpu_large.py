@@ -36,7 +36,7 @@ def run_large(dev, a, filt, n, filt_stride=0, mid="mul"):
     return buf.cpu().numpy().reshape(-1)
 
 
-@pytest.mark.parametrize("n,batch", [(8192, 4), (16384, 3), (32768, 4), (65536, 2), (131072, 2)])
+@pytest.mark.parametrize("n,batch", [(8192, 4), (16384, 3), (32768, 4), (65536, 2), (131072, 2), (262144, 1), (1048576, 1)])
 @pytest.mark.parametrize("mid", ["mul", "conj", "none"])
 def test_large_matches_oracle(dev, n, batch, mid, rng):
     import fufft_amd as ff
