@@ -62,6 +62,9 @@ def _load() -> C.CDLL:
         "fufft_plan_chains": ([i64, i32, C.POINTER(C.c_int)], i32),
         "fufft_plan_filter_f32": ([i64, i32, i32, i32, i32, vp, vp], i32),
         "fufft_twiddle_table_host": ([i32, vp], i32),
+        "fufft_twiddle_table_host_source": ([i32, i32, vp], i32),
+        "fufft_set_twiddles": ([i32, i32], i32),
+        "fufft_get_twiddles": ([i32, C.POINTER(C.c_int)], i32),
         "fufft_conv_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp], i32),
         "fufft_fwd_f32": ([vp, vp, i64, i64, i32, vp], i32),
         "fufft_apply_f32": ([vp, i64, vp, i64, vp, i64, i64, i32, i32, i32, vp], i32),
@@ -167,10 +170,27 @@ def plan_filter(x: np.ndarray, n: int, variant: str = "v16", layout: str = "dr",
     return out
 
 
-def twiddle_table_host(log_max: int) -> np.ndarray:
+TWIDDLES = {"accurate": 0, "reference": 1}
+
+
+def twiddle_table_host(log_max: int, source: str = "accurate") -> np.ndarray:
     out = np.empty(2 << log_max, dtype=np.complex64)
-    check(lib.fufft_twiddle_table_host(log_max, out.ctypes.data), "fufft_twiddle_table_host")
+    check(lib.fufft_twiddle_table_host_source(log_max, TWIDDLES[source], out.ctypes.data),
+          "fufft_twiddle_table_host_source")
     return out
+
+
+def set_twiddles(source: str, device: int = 0) -> None:
+    """Base-twiddle source of the device table: "accurate" (default, fp64
+    evaluated) or "reference" (the reference's fp32-angle cosf/sinf, with which
+    the fp32 kernels reproduce its CPU transcription bit for bit)."""
+    check(lib.fufft_set_twiddles(device, TWIDDLES[source]), "fufft_set_twiddles")
+
+
+def get_twiddles(device: int = 0) -> str:
+    v = C.c_int(-1)
+    check(lib.fufft_get_twiddles(device, C.byref(v)), "fufft_get_twiddles")
+    return {i: k for k, i in TWIDDLES.items()}[v.value]
 
 
 # ---- launches ------------------------------------------------------------------------

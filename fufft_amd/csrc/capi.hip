@@ -17,7 +17,9 @@ namespace fufft {
 // ---- twiddle table ----------------------------------------------------------------
 // Static device memory: every GPU the library runs on holds one copy, filled
 // once by fufft_init.  Level P = 2^p (1 <= p <= FUFFT_TW_LOG_MAX) occupies
-// entries [P, 2P): (cos, sin)(2*pi*t/P) rounded to fp32.
+// entries [P, 2P): (cos, sin)(2*pi*t/P) rounded to fp32 by default, or, with
+// fufft_set_twiddles(FUFFT_TWIDDLES_REFERENCE), the reference's fp32-angle
+// values.
 __device__ float2 g_twiddle[FUFFT_TW_ENTRIES];
 
 namespace {
@@ -26,6 +28,7 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceState {
    std::atomic<int> ready{0};
+   std::atomic<int> source{FUFFT_TWIDDLES_ACCURATE};
    const float2*    tw = nullptr;
 };
 DeviceState g_dev[kMaxDevices];
@@ -40,13 +43,44 @@ void table_entry(int P, int64_t t, float* c, float* s)
    *s = (float)sin(th);
 }
 
-void fill_table(int log_max, float* out)
+// The reference's base twiddle: cosf / sinf of the fp32 angle step * j with
+// step = 2*pi/P in fp32 (verify_kernel.cpp:31, 93, 99; the device code's
+// __sincosf(step * j), fufft.cuh:362-371).  The forward passes use
+// step = -2*pi/P; that angle is the exact negation of this one and libm's
+// cosf / sinf are even / odd bit for bit, so negating the stored sine gives
+// the forward twiddle exactly as the reference computes it.
+void table_entry_reference(int P, int64_t t, float* c, float* s)
+{
+   const float step = 6.28318530717958647692f / (float)P;
+   const float ang  = step * (float)t;
+   *c = cosf(ang);
+   *s = sinf(ang);
+}
+
+void fill_table(int log_max, float* out, int source = FUFFT_TWIDDLES_ACCURATE)
 {
    out[0] = out[1] = out[2] = out[3] = 0.0f;
    for(int p = 1; p <= log_max; p++) {
       const int P = 1 << p;
-      for(int t = 0; t < P; t++) table_entry(P, t, &out[2 * (P + t)], &out[2 * (P + t) + 1]);
+      for(int t = 0; t < P; t++) {
+         float* e = &out[2 * (P + t)];
+         if(source == FUFFT_TWIDDLES_REFERENCE) table_entry_reference(P, t, e, e + 1);
+         else                                   table_entry(P, t, e, e + 1);
+      }
    }
+}
+
+// Fill the whole table from `source` and copy it to the current device
+// (synchronous).  Returns the table's device address through addr.
+int upload_table(int source, void** addr)
+{
+   std::vector<float> host(2 * (size_t)FUFFT_TW_ENTRIES);
+   fill_table(FUFFT_TW_LOG_MAX, host.data(), source);
+   if(hipMemcpyToSymbol(HIP_SYMBOL(g_twiddle), host.data(), host.size() * sizeof(float), 0,
+                        hipMemcpyHostToDevice) != hipSuccess ||
+      hipGetSymbolAddress(addr, HIP_SYMBOL(g_twiddle)) != hipSuccess || *addr == nullptr)
+      return FUFFT_ERR_HIP;
+   return FUFFT_OK;
 }
 
 // LDS layout: padded by default (additive addresses); FUFFT_LDS_LAYOUT=xor
@@ -94,19 +128,34 @@ int init_device(int dev)
    int prev = 0;
    if(hipGetDevice(&prev) != hipSuccess) return FUFFT_ERR_HIP;
    if(prev != dev && hipSetDevice(dev) != hipSuccess) return FUFFT_ERR_HIP;
-   std::vector<float> host(2 * (size_t)FUFFT_TW_ENTRIES);
-   fill_table(FUFFT_TW_LOG_MAX, host.data());
-   int status = FUFFT_OK;
    void* addr = nullptr;
-   if(hipMemcpyToSymbol(HIP_SYMBOL(g_twiddle), host.data(), host.size() * sizeof(float), 0,
-                        hipMemcpyHostToDevice) != hipSuccess ||
-      hipGetSymbolAddress(&addr, HIP_SYMBOL(g_twiddle)) != hipSuccess || addr == nullptr)
-      status = FUFFT_ERR_HIP;
+   const int status = upload_table(FUFFT_TWIDDLES_ACCURATE, &addr);
    if(prev != dev) (void)hipSetDevice(prev);
    if(status != FUFFT_OK) return status;
    d.tw = static_cast<const float2*>(addr);
+   d.source.store(FUFFT_TWIDDLES_ACCURATE, std::memory_order_relaxed);
    d.ready.store(1, std::memory_order_release);
    return FUFFT_OK;
+}
+
+int set_twiddles(int dev, int source)
+{
+   if(source != FUFFT_TWIDDLES_ACCURATE && source != FUFFT_TWIDDLES_REFERENCE) return FUFFT_ERR_INVALID;
+   const int st = init_device(dev);
+   if(st != FUFFT_OK) return st;
+   DeviceState& d = g_dev[dev];
+   std::lock_guard<std::mutex> lock(g_init_mutex);
+   if(d.source.load(std::memory_order_relaxed) == source) return FUFFT_OK;
+   int prev = 0;
+   if(hipGetDevice(&prev) != hipSuccess) return FUFFT_ERR_HIP;
+   if(prev != dev && hipSetDevice(dev) != hipSuccess) return FUFFT_ERR_HIP;
+   // kernels already queued on any stream read the table: let them finish first
+   int status = hipDeviceSynchronize() == hipSuccess ? FUFFT_OK : FUFFT_ERR_HIP;
+   void* addr = nullptr;
+   if(status == FUFFT_OK) status = upload_table(source, &addr);
+   if(prev != dev) (void)hipSetDevice(prev);
+   if(status == FUFFT_OK) d.source.store(source, std::memory_order_relaxed);
+   return status;
 }
 
 // twiddle table of the current device, initialising it on first use
@@ -218,6 +267,17 @@ extern "C" {
 
 int fufft_init(int device) { return init_device(device); }
 
+int fufft_set_twiddles(int device, int source) { return set_twiddles(device, source); }
+
+int fufft_get_twiddles(int device, int* source)
+{
+   if(!source) return FUFFT_ERR_INVALID;
+   const int st = init_device(device);
+   if(st != FUFFT_OK) return st;
+   *source = g_dev[device].source.load(std::memory_order_relaxed);
+   return FUFFT_OK;
+}
+
 const char* fufft_status_string(int status)
 {
    switch(status) {
@@ -288,8 +348,14 @@ int fufft_plan_filter_f32(int64_t n, int variant, int layout, int filter_kind,
 
 int fufft_twiddle_table_host(int log_max, float* out)
 {
+   return fufft_twiddle_table_host_source(log_max, FUFFT_TWIDDLES_ACCURATE, out);
+}
+
+int fufft_twiddle_table_host_source(int log_max, int source, float* out)
+{
    if(!out || log_max < 1 || log_max > FUFFT_TW_LOG_MAX) return FUFFT_ERR_INVALID;
-   fill_table(log_max, out);
+   if(source != FUFFT_TWIDDLES_ACCURATE && source != FUFFT_TWIDDLES_REFERENCE) return FUFFT_ERR_INVALID;
+   fill_table(log_max, out, source);
    return FUFFT_OK;
 }
 

@@ -96,6 +96,29 @@ int fufft_plan_filter_f32(int64_t n, int variant, int layout, int filter_kind,
  * fp32.  out must hold 2 * 2^(log_max+1) floats. */
 int fufft_twiddle_table_host(int log_max, float* out);
 
+/* Source of the base twiddles W^j every kernel reads from the device table.
+ *   FUFFT_TWIDDLES_ACCURATE   (default) (cos, sin)(2*pi*t/P) evaluated in
+ *                             fp64 and rounded to fp32.
+ *   FUFFT_TWIDDLES_REFERENCE  cosf / sinf of the fp32 angle (2*pi/P)*t, the
+ *                             value the reference's device code computes with
+ *                             __sincosf(step*j) and its CPU transcription with
+ *                             cosf/sinf (fufft.cuh:362-371, 731;
+ *                             verify_kernel.cpp:31, 93-99).  With it the fp32
+ *                             kernels reproduce that transcription
+ *                             (kernel_pipeline_v16 / _ip / _fwd / _apply,
+ *                             kernel_conv2d, kernel_conv_r2, the four-step
+ *                             chain) bit for bit on the same inputs.
+ * fufft_set_twiddles rewrites the table of `device` (a synchronous copy after
+ * a device-wide synchronisation): call it while no fufft work is queued on
+ * the device and outside stream capture.  The setting holds for every later
+ * call on that device. */
+#define FUFFT_TWIDDLES_ACCURATE   0
+#define FUFFT_TWIDDLES_REFERENCE  1
+int fufft_set_twiddles(int device, int source);
+int fufft_get_twiddles(int device, int* source);
+/* fufft_twiddle_table_host for either source */
+int fufft_twiddle_table_host_source(int log_max, int source, float* out);
+
 /* ---- fp32 fused convolution ------------------------------------------------
  * out = IDFT(DFT(in) mid filt) for batch signals of n points, one launch,
  * three HBM passes.  in == out is allowed.

@@ -47,7 +47,9 @@ def replay(case: dict) -> dict:
         return {"u": u, "v": v}
     if kind == "fourstep":
         n, lout, mid = int(case["n"]), int(case["lout"]), int(case["mid"])
-        return {"out": O.conv(case["a"], case["bdr"], n, O.large_plan(lout, mid, ref=True), filt_stride=n, tw=O.TW_LIBM)}
+        mid_v = int(case["mid_v"]) if "mid_v" in case else 16
+        plan = O.large_plan(lout, mid, mid_v, ref=True)
+        return {"out": O.conv(case["a"], case["bdr"], n, plan, filt_stride=n, tw=O.TW_LIBM)}
     if kind == "c2c_stockham":
         # the reference's Stockham C2C rounds in a different order from this
         # build's DIF + permutation: no bit-exact outputs; test_oracle_c2c

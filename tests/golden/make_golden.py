@@ -90,6 +90,45 @@ def main() -> None:
     R.ref_vk_c2c(n, 1, a.ctypes.data, out.ctypes.data, batch)
     save("c2c_stockham_n512", kind="c2c_stockham", n=n, a=a, out=out.reshape(-1))
 
+    # Fixtures at sizes the GPU kernels run with the reference's own plans, so
+    # the GPU tests can compare against the reference directly (in
+    # reference-twiddle mode).  A second generator keeps the inputs above.
+    rng = np.random.default_rng(20261202)
+    for n in (1024, 2048):                       # radix-8 with a lead 2 / 4 pass
+        a, b = _cu(rng, (1, n)), _cu(rng, (1, n)) / n
+        bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 8))])
+        lead, nr8 = _lead_count(n, 8)
+        out = np.empty_like(a)
+        R.ref_vk_pipeline_ip(n, lead, nr8, 1, a.ctypes.data, bdr.ctypes.data, out.ctypes.data, 1)
+        save(f"r8_n{n}", kind="r8", n=n, a=a, bdr=bdr, out=out.reshape(-1))
+
+    for n in (2048, 4096):                       # radix 16 with a lead 8 pass / pure 16^3
+        a, b = _cu(rng, (1, n)), _cu(rng, (1, n)) / n
+        bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 16))])
+        lead, nrv = _lead_count(n, 16)
+        out = np.empty_like(a)
+        R.ref_vk_pipeline_v16(n, lead, nrv, 1, a.ctypes.data, bdr.ctypes.data, out.ctypes.data, 1)
+        save(f"v16_n{n}", kind="v16", n=n, a=a, bdr=bdr, out=out.reshape(-1))
+
+    n, batch = 512, 2                            # two-for-one real, radix 8
+    x = rng.uniform(-1, 1, (batch, n)).astype(np.float32)
+    y = rng.uniform(-1, 1, (batch, n)).astype(np.float32)
+    b = _cu(rng, (batch, n)) / n
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.kernel_plan(n, 8))])
+    lead, nr8 = _lead_count(n, 8)
+    u, v = np.empty_like(x), np.empty_like(y)
+    R.ref_vk_conv_r2(n, lead, nr8, 1, x.ctypes.data, y.ctypes.data, bdr.ctypes.data,
+                     u.ctypes.data, v.ctypes.data, batch)
+    save("r2_n512", kind="r2", n=n, x=x, y=y, bdr=bdr, u=u.reshape(-1), v=v.reshape(-1))
+
+    n, mid = 8192, 512                           # four-step, radix-8 middle (the GPU's plan)
+    a, b = _cu(rng, (1, n)), _cu(rng, (1, n)) / n
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.large_plan(1, mid, 8))])
+    A = a.copy()
+    R.ref_vk_conv_foursteps_cfg(A.ctypes.data, bdr.ctypes.data, n, 1, 16, mid, 0)
+    save("fourstep_n8192_mid512_r8", kind="fourstep", n=n, lout=1, mid=mid, mid_v=8, a=a, bdr=bdr,
+         out=A.reshape(-1))
+
 
 if __name__ == "__main__":
     main()

@@ -1,0 +1,194 @@
+"""GPU kernels against the reference's own CPU transcription, bit for bit.
+
+With the device table switched to the reference's base twiddles
+(fufft_set_twiddles(FUFFT_TWIDDLES_REFERENCE): cosf / sinf of the fp32 angle
+(2*pi/P)*j, as verify_kernel.cpp:31, 93-99 computes them), the fp32 kernels
+perform exactly the operations of the reference's transcription
+(verify_kernel.cpp: kernel_pipeline_v16, kernel_pipeline_ip, _fwd / _apply,
+kernel_conv_r2, conv_foursteps_cfg, kernel_conv2d), so:
+
+1. on the golden fixtures written from the compiled reference
+   (tests/golden/make_golden.py) the GPU output equals the reference's output
+   bit for bit, for every fixture whose plan a GPU kernel runs;
+2. at every supported size, mid operation and path the GPU equals the oracle
+   in libm-twiddle mode bit for bit -- the mode tests/test_oracle_pins.py pins
+   bit for bit to the compiled reference -- and stays within 2e-6 of fp64.
+
+The module switches the table back to the default source when it ends.
+"""
+import numpy as np
+import pytest
+
+from conftest import bits_equal, crandn, cuniform
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 2e-6
+
+
+def to_dev(x, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy().reshape(-1)
+
+
+@pytest.fixture(scope="module")
+def ref_tw(dev):
+    import fufft_amd as ff
+    ff.set_twiddles("reference")
+    assert ff.get_twiddles() == "reference"
+    try:
+        yield dev
+    finally:
+        ff.set_twiddles("accurate")
+        assert ff.get_twiddles() == "accurate"
+
+
+def _golden():
+    from tests.golden import golden
+    return golden.load_all()
+
+
+# fixtures whose plan a GPU kernel runs (the GPU's smallest sizes are N = 256
+# radix 16 and N = 512 radix 8; its four-step middle is radix 8 in [512, 4096])
+GPU_FIXTURES = ["v16_n512", "v16_n1024", "v16_n2048", "v16_n4096", "r8_n512", "r8_n1024",
+                "r8_n2048", "r8_n4096", "split_n512", "r2_n512", "fourstep_n8192_mid512_r8"]
+
+
+@pytest.mark.parametrize("name", GPU_FIXTURES)
+def test_gpu_equals_reference_on_golden_fixture(ref_tw, name):
+    import torch
+    import fufft_amd as ff
+    dev = ref_tw
+    case = _golden()[name]
+    kind = str(case["kind"])
+    print(f"case golden {name} kind={kind}", flush=True)
+    if kind in ("v16", "r8"):
+        n = int(case["n"])
+        a = case["a"]
+        da = to_dev(a, dev)
+        out = torch.empty_like(da)
+        ff.conv(da, to_dev(case["bdr"], dev), out, n=n, batch=a.size // n, filt_stride=n, variant=kind)
+        assert bits_equal(host(out), case["out"])
+    elif kind == "split":
+        n = int(case["n"])
+        a = case["a"]
+        batch = a.size // n
+        da = to_dev(a, dev)
+        spec, out = torch.empty_like(da), torch.empty_like(da)
+        ff.fwd(da, spec, n=n, batch=batch, variant="r8")
+        ff.apply(spec, to_dev(case["bdr"], dev), out, n=n, batch=batch, spec_stride=n, filt_stride=n,
+                 variant="r8")
+        assert bits_equal(host(spec), case["spec"])
+        assert bits_equal(host(out), case["out"])
+    elif kind == "r2":
+        n = int(case["n"])
+        x, y = case["x"], case["y"]
+        dx, dy = to_dev(x, dev), to_dev(y, dev)
+        du, dv = torch.empty_like(dx), torch.empty_like(dy)
+        ff.conv_r2(dx, dy, to_dev(case["bdr"], dev), du, dv, n=n, batch=x.size // n, filt_stride=n,
+                   variant="r8")
+        assert bits_equal(host(du), case["u"])
+        assert bits_equal(host(dv), case["v"])
+    elif kind == "fourstep":
+        n = int(case["n"])
+        lout, mid = ff.large_plan(n)
+        assert (lout, mid) == (int(case["lout"]), int(case["mid"]))
+        buf = to_dev(case["a"], dev)
+        ff.conv_large(buf, to_dev(case["bdr"], dev), n=n, batch=case["a"].size // n, filt_stride=n)
+        assert bits_equal(host(buf), case["out"])
+    else:
+        raise AssertionError(kind)
+
+
+SIZES = [("v16", n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + \
+        [("r8", n) for n in (512, 1024, 2048, 4096, 8192)]
+V = {"v16": 16, "r8": 8}
+
+
+@pytest.mark.parametrize("variant,n", SIZES)
+@pytest.mark.parametrize("mid", ["mul", "conj", "none"])
+def test_conv_equals_libm_oracle(ref_tw, variant, n, mid, rng):
+    import torch
+    import fufft_amd as ff
+    dev = ref_tw
+    batch = max(2, 16384 // n)
+    a = crandn(rng, (batch, n))
+    spec = crandn(rng, n) / n
+    plan = O.kernel_plan(n, V[variant])
+    fdr = spec[O.mixedrev(plan)]
+    print(f"case reftw conv variant={variant} n={n} mid={mid} batch={batch}", flush=True)
+    da = to_dev(a, dev)
+    out = torch.empty_like(da)
+    ff.conv(da, to_dev(fdr, dev), out, n=n, batch=batch, mid=mid, variant=variant)
+    got = host(out)
+    assert bits_equal(got, O.conv(a, fdr, n, plan, mid=mid, tw=O.TW_LIBM))
+    assert O.rel_l2(got, O.conv_spec_f64(a, spec, n, mid=mid)) <= TOL_F32
+
+
+@pytest.mark.parametrize("n", [32768, 65536])
+def test_fourstep_equals_libm_oracle(ref_tw, n, rng):
+    import fufft_amd as ff
+    dev = ref_tw
+    lout, mid = ff.large_plan(n)
+    plan = O.large_plan(lout, mid, 8)
+    a = cuniform(rng, (2, n))
+    spec = cuniform(rng, n) / n
+    fdr = spec[O.mixedrev(plan)]
+    print(f"case reftw fourstep n={n}", flush=True)
+    buf = to_dev(a, dev)
+    ff.conv_large(buf, to_dev(fdr, dev), n=n, batch=2)
+    got = host(buf)
+    assert bits_equal(got, O.conv(a, fdr, n, plan, tw=O.TW_LIBM))
+    assert O.rel_l2(got, O.conv_spec_f64(a, spec, n)) <= TOL_F32
+
+
+@pytest.mark.parametrize("h,w", [(256, 512), (512, 512)])
+def test_conv2d_equals_libm_oracle(ref_tw, h, w, rng):
+    import torch
+    import fufft_amd as ff
+    dev = ref_tw
+    vr, vc = ff.plan2d(h, w)
+    ph, pw = O.kernel_plan(h, vc), O.kernel_plan(w, vr)
+    # at these shapes the GPU's row and column plans are the reference's
+    # radix-8 plans (kernel_conv2d runs radix 8 in both dimensions)
+    assert (ph.radices, pw.radices) == (O.ref_plan(h, 8).radices, O.ref_plan(w, 8).radices)
+    a = cuniform(rng, (2, h, w))
+    filt = ff.plan_filter2d(cuniform(rng, h * w), h, w)
+    print(f"case reftw conv2d {h}x{w}", flush=True)
+    da = to_dev(a, dev)
+    out = torch.empty_like(da)
+    ff.conv2d(da, to_dev(filt, dev), out, h, w, batch=2)
+    assert bits_equal(host(out), O.conv2d(a, filt, h, w, ph, pw, tw=O.TW_LIBM))
+
+
+@pytest.mark.parametrize("n", [512, 4096])
+def test_bfp_equals_libm_oracle(ref_tw, n, rng):
+    import torch
+    import fufft_amd as ff
+    dev = ref_tw
+    batch = 16
+    x = (crandn(rng, (batch, n)) * 10.0 ** rng.uniform(-3, 3, (batch, 1))).astype(np.complex64)
+    q, e = ff.bfp_quantize(x)
+    filt = ff.plan_filter(crandn(rng, n), n, variant="auto", kind=ff.FILTER_TAPS)
+    print(f"case reftw bfp n={n}", flush=True)
+    dq, de = to_dev(q, dev), to_dev(e, dev)
+    qo, eo = torch.empty_like(dq), torch.empty_like(de)
+    ff.conv_bfp16(dq, de, to_dev(filt, dev), qo, eo, n=n, batch=batch)
+    oq, oe = O.bfp_conv(q, e, filt, n, O.kernel_plan(n, 8), tw=O.TW_LIBM)
+    assert np.array_equal(host(eo), oe)
+    assert np.array_equal(host(qo), oq)
+
+
+def test_set_twiddles_rejects_bad_source(dev):
+    import fufft_amd as ff
+    before = ff.get_twiddles()
+    with pytest.raises(ff.FufftError):
+        ff.check(ff.lib.fufft_set_twiddles(0, 5), "fufft_set_twiddles")
+    assert ff.get_twiddles() == before

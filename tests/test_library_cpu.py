@@ -108,6 +108,35 @@ def test_twiddle_table_matches_oracle_bitwise():
             assert tab[P + j, 0] == np.float32(c.value) and tab[P + j, 1] == np.float32(s.value), (P, j)
 
 
+def test_reference_twiddle_table_matches_libm_mode_both_signs():
+    """FUFFT_TWIDDLES_REFERENCE holds the fp32-angle cosf/sinf of the
+    reference's transcription (the oracle's LIBM mode, which is pinned bit for
+    bit to the compiled reference).  The kernels negate the stored sine for
+    the forward passes, so that negation must equal the forward's own
+    cosf/sinf(-angle) bit for bit too."""
+    import fufft_amd as ff
+    log_max = 20
+    tab = ff.twiddle_table_host(log_max, "reference").view(np.float32).reshape(-1, 2)
+    acc = ff.twiddle_table_host(log_max, "accurate").view(np.float32).reshape(-1, 2)
+    c, s = C.c_float(), C.c_float()
+    differs = 0
+    for p in range(1, log_max + 1):
+        P = 1 << p
+        js = range(P) if P <= 4096 else list(range(0, P, 97)) + [P - 1]
+        for j in js:
+            O.lib.or_twiddle(O.TW_LIBM, +1, P, j, C.byref(c), C.byref(s))
+            assert tab[P + j].view(np.uint32).tolist() == \
+                np.array([c.value, s.value], np.float32).view(np.uint32).tolist(), (P, j)
+            O.lib.or_twiddle(O.TW_LIBM, -1, P, j, C.byref(c), C.byref(s))
+            neg = np.array([tab[P + j, 0], -tab[P + j, 1]], np.float32)
+            assert neg.view(np.uint32).tolist() == \
+                np.array([c.value, s.value], np.float32).view(np.uint32).tolist(), (P, j, "fwd")
+            differs += int(tab[P + j, 0] != acc[P + j, 0] or tab[P + j, 1] != acc[P + j, 1])
+    assert differs > 1000          # the two sources really differ
+    with pytest.raises(ff.FufftError):
+        ff.check(ff.lib.fufft_twiddle_table_host_source(4, 7, tab.ctypes.data), "bad source")
+
+
 def test_bfp_codec_matches_oracle(rng):
     import fufft_amd as ff
     vals = [0.0, 1e-45, 1.17e-38, 1.0, 32767.0, 32767.5, 32768.0, 65534.0, 65535.0, 3.4e38]
