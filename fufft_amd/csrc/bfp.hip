@@ -222,9 +222,9 @@ static hipError_t launch_bfp_nv(int layout, const BfpParams& p, hipStream_t s)
       }
    }
    switch(p.mid) {
-      case MID_MUL:  return launch_bfp_one<N, V, LAYOUT_PAD, MID_MUL>(p, s);
-      case MID_CONJ: return launch_bfp_one<N, V, LAYOUT_PAD, MID_CONJ>(p, s);
-      default:       return launch_bfp_one<N, V, LAYOUT_PAD, MID_NONE>(p, s);
+      case MID_MUL:  return launch_bfp_one<N, V, default_lds_layout(N, V), MID_MUL>(p, s);
+      case MID_CONJ: return launch_bfp_one<N, V, default_lds_layout(N, V), MID_CONJ>(p, s);
+      default:       return launch_bfp_one<N, V, default_lds_layout(N, V), MID_NONE>(p, s);
    }
 }
 

@@ -83,13 +83,14 @@ int upload_table(int source, void** addr)
    return FUFFT_OK;
 }
 
-// LDS layout: padded by default (additive addresses); FUFFT_LDS_LAYOUT=xor
-// selects the zero-padding XOR swizzle (a tuning knob, both are bit-identical)
+// LDS layout: each plan's additive default (per-exchange layouts, or the
+// padded one; default_lds_layout) unless FUFFT_LDS_LAYOUT=xor selects the
+// zero-padding XOR swizzle (a tuning knob; all are bit-identical)
 int lds_layout()
 {
    static const int layout = [] {
       const char* e = std::getenv("FUFFT_LDS_LAYOUT");
-      return (e && std::strcmp(e, "xor") == 0) ? LAYOUT_XOR : LAYOUT_PAD;
+      return (e && std::strcmp(e, "xor") == 0) ? LAYOUT_XOR : LAYOUT_DEFAULT;
    }();
    return layout;
 }
@@ -451,7 +452,7 @@ int fufft_conv_timed_f32(const void* in, const void* filt, int64_t filt_stride, 
    if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt)) || !aligned4(timing))
       return FUFFT_ERR_ALIGN;
    // one launch only, so record g is workgroup g of the whole call
-   if(lds_layout() != LAYOUT_PAD) return FUFFT_ERR_UNSUPPORTED;
+   if(lds_layout() != LAYOUT_DEFAULT) return FUFFT_ERR_UNSUPPORTED;
    Conv1dParams p{};
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
    if((uint64_t)p.fcount * (uint64_t)n * 8 > 0xffffffffull) return FUFFT_ERR_UNSUPPORTED;

@@ -228,8 +228,8 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
       case K_C2C_INV:   return launch_one<N, V, LAYOUT, K_C2C_INV, MID_NONE>(p, s);
       case K_PLAN_TAPS: return launch_one<N, V, LAYOUT, K_PLAN_TAPS, MID_NONE>(p, s);
       case K_CONV_TIMED:
-         // the timed build exists for the default (padded) LDS layout only
-         if constexpr(LAYOUT == LAYOUT_PAD) {
+         // the timed build exists for the default LDS layout only
+         if constexpr(LAYOUT == default_lds_layout(N, V)) {
             switch(p.mid) {
                case MID_MUL:  return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_MUL>(p, s);
                case MID_CONJ: return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_CONJ>(p, s);
@@ -246,8 +246,8 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
 template<int N, int V>
 static hipError_t launch_nv(int kind, int layout, const Conv1dParams& p, hipStream_t s)
 {
-   return layout == LAYOUT_PAD ? launch_kind<N, V, LAYOUT_PAD>(kind, p, s)
-                               : launch_kind<N, V, LAYOUT_XOR>(kind, p, s);
+   return layout == LAYOUT_XOR ? launch_kind<N, V, LAYOUT_XOR>(kind, p, s)
+                               : launch_kind<N, V, default_lds_layout(N, V)>(kind, p, s);
 }
 
 bool conv1d_supported(int n, int v)

@@ -72,10 +72,52 @@ __device__ __forceinline__ void static_for(F&& f)
 //    phys(base + k*M) = phys(base) + phys(k*M),
 // so a lane computes one address per group and the taps use immediate
 // offsets.  At most 2-way conflicts remain in the consecutive-lane passes.
-enum { LAYOUT_XOR = 0, LAYOUT_PAD = 1 };
+enum { LAYOUT_XOR = 0, LAYOUT_PAD = 1, LAYOUT_XCHG = 2 };
+// run-time selection passed to the launchers: each plan's default, or XOR
+enum { LAYOUT_DEFAULT = 3 };
 
 template<int V, int LAYOUT>
 struct Lds;
+
+// Exchange E (between pass E and pass E + 1) of plan PL: one spare block of
+// Mb slots after every Ma = V*Mb positions, phys = i + Mb*(i / Ma), where Mb
+// is the stride of the first wavefront-private pass after the exchange (the
+// first pass from E + 1 on with M <= 64).
+//  - Conflicts: a private reader (M = Mb) reads runs of Mb consecutive
+//    positions Ma apart, which land Ma + Mb slots apart and tile the 64 banks;
+//    every other pass writes or reads runs of 32 consecutive positions,
+//    which no spare block splits.
+//  - Additive for both passes' taps: base + k*M never crosses an Ma block in
+//    a pass with M <= Mb and crosses k whole blocks in a pass with M >= Ma.
+//  - Races: a pass gathers from exchange E-1 and scatters into exchange E
+//    with no barrier in between.  A pass that spans wavefronts (M > 64)
+//    therefore gets the same layout on both sides (it reads and writes the
+//    same slots, as with a single layout); a private pass keeps each
+//    wavefront inside its own block of V*64 positions, and both of its
+//    layouts map block boundaries to the same slot, so wavefronts never touch
+//    each other's slots.
+// tests/test_lds_audit.py checks all of this by brute force for every plan.
+// Under the 64-bank model every exchange is conflict free, where the single
+// padded layout below leaves 2-way conflicts after the wide passes.
+template<class PL, int E>
+struct XchgLds {
+   static constexpr int reader_stride(int e)
+   {
+      int q = e + 1;
+      while(PL::stride(q) > 64) q++;
+      return PL::stride(q);
+   }
+   static constexpr int Mb = reader_stride(E), Ma = PL::V * Mb;
+   static constexpr bool additive = true;
+   __device__ __forceinline__ static int phys(int i) { return i + Mb * (i / Ma); }
+   static constexpr int cphys(int i) { return i + Mb * (i / Ma); }
+};
+
+// The default layout of a plan: per-exchange (XchgLds) wherever it keeps the
+// kernel's VGPRs; at radix 8, N = 8192 its extra exchange base addresses take
+// the kernel from 62 to 71 VGPRs, which halves the workgroups per CU, so that
+// plan keeps the single padded layout.
+constexpr int default_lds_layout(int n, int v) { return (v == 8 && n > 4096) ? LAYOUT_PAD : LAYOUT_XCHG; }
 
 template<int V>
 struct Lds<V, LAYOUT_XOR> {
@@ -88,6 +130,7 @@ struct Lds<V, LAYOUT_XOR> {
       return i ^ ((i >> LOGV) & (V - 1)) ^ (((i >> (2 * LOGV)) & ((1 << HI) - 1)) << LOGV);
    }
    static constexpr int cphys(int i) { return i; }
+   template<class PL, int E> using at = Lds;
 };
 
 template<int V>
@@ -96,6 +139,15 @@ struct Lds<V, LAYOUT_PAD> {
    static constexpr int size(int n) { return n + n / V; }
    __device__ __forceinline__ static int phys(int i) { return i + i / V; }
    static constexpr int cphys(int i) { return i + i / V; }
+   template<class PL, int E> using at = Lds;
+};
+
+// Per-exchange layouts for the pass exchanges (XchgLds, at most N + N/V
+// slots: M_{E+1} / M_E = 1/V for every E); the padded layout for any other
+// exchange through the slot (the natural-order C2C's).
+template<int V>
+struct Lds<V, LAYOUT_XCHG> : Lds<V, LAYOUT_PAD> {
+   template<class PL, int E> using at = XchgLds<PL, E>;
 };
 
 // ---- pass machinery ---------------------------------------------------------------
@@ -262,9 +314,12 @@ __device__ __forceinline__ void forward_dif(float2 (&r)[PL::V], float2* A, int L
 {
    static_for<PL::NP>([&](auto pi) {
       constexpr int p = decltype(pi)::value;
-      if constexpr(p > 0) { exchange_sync<PL, p - 1, LANES, WL>(); lds_gather<PL, p, LD>(r, A, L); }
+      if constexpr(p > 0) {
+         exchange_sync<PL, p - 1, LANES, WL>();
+         lds_gather<PL, p, typename LD::template at<PL, p - 1>>(r, A, L);
+      }
       compute_pass<PL, p, -1, false, KEEP>(r, tw, kc);
-      if constexpr(p < PL::NP - 1) lds_scatter<PL, p, LD>(r, A, L);
+      if constexpr(p < PL::NP - 1) lds_scatter<PL, p, typename LD::template at<PL, p>>(r, A, L);
    });
 }
 
@@ -284,9 +339,12 @@ __device__ __forceinline__ void inverse_dit(float2 (&r)[PL::V], float2* A, int L
 {
    static_for<PL::NP>([&](auto qi) {
       constexpr int p = PL::NP - 1 - decltype(qi)::value;
-      if constexpr(p < PL::NP - 1) lds_gather<PL, p, LD>(r, A, L);
+      if constexpr(p < PL::NP - 1) lds_gather<PL, p, typename LD::template at<PL, p>>(r, A, L);
       compute_pass<PL, p, +1, true, KEEP>(r, tw, kc);
-      if constexpr(p > 0) { lds_scatter<PL, p, LD>(r, A, L); exchange_sync<PL, p - 1, LANES, WL>(); }
+      if constexpr(p > 0) {
+         lds_scatter<PL, p, typename LD::template at<PL, p - 1>>(r, A, L);
+         exchange_sync<PL, p - 1, LANES, WL>();
+      }
    });
 }
 

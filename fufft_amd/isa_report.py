@@ -43,7 +43,7 @@ TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 KINDS = {0: "conv", 1: "conv_r2", 2: "fwd", 3: "apply", 4: "fwd_r2", 5: "apply_r2",
          6: "c2c_fwd", 7: "c2c_inv", 8: "plan_taps", 9: "conv_timed"}
 MIDS = {0: "mul", 1: "conj", 2: "none"}
-LAYOUTS = {0: "xor", 1: "pad"}
+LAYOUTS = {0: "xor", 1: "pad", 2: "xchg"}
 
 FP32_ARITH = re.compile(r"^v_(add|sub|subrev|mul|fma|fmac|fmaak|fmamk)_f32")
 # bytes moved per lane by each LDS data instruction
@@ -228,10 +228,15 @@ def occupancy(vgpr: int, agpr: int, lds_bytes: int, waves_per_wg: int) -> dict:
     return {"waves_per_simd": int(min(limits.values())), "limited_by": lim, "vgpr_alloc": regs}
 
 
+def default_layout(n: int, v: int) -> str:
+    """The LDS layout a plan runs by default (default_lds_layout in fufft_plan.hpp)."""
+    return "pad" if (v == 8 and n > 4096) else "xchg"
+
+
 def lds_bytes_conv(n: int, v: int, layout: str) -> int:
     t = n // v
     cpb = 1 if t >= 128 else 256 // t
-    return cpb * (n + (n // v if layout == "pad" else 0)) * 8
+    return cpb * (n + (n // v if layout in ("pad", "xchg") else 0)) * 8
 
 
 def conv_rows(rows=None) -> list:
@@ -259,12 +264,12 @@ def conv_rows(rows=None) -> list:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--kind", default="conv")
-    ap.add_argument("--layout", default="pad")
+    ap.add_argument("--layout", default="default", help="default (each plan's own), xchg, pad or xor")
     ap.add_argument("--mid", default="mul")
     ap.add_argument("--markdown", action="store_true")
     a = ap.parse_args()
-    rows = [r for r in conv_rows() if r["kind"] == a.kind and r["layout"] == a.layout
-            and r["mid"] == a.mid]
+    rows = [r for r in conv_rows() if r["kind"] == a.kind and r["mid"] == a.mid
+            and r["layout"] == (default_layout(r["n"], r["v"]) if a.layout == "default" else a.layout)]
     rows.sort(key=lambda r: (r["family"], r["v"], r["n"]))
     if not a.markdown:
         for r in rows:

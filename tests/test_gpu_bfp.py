@@ -98,3 +98,31 @@ def test_bfp_per_signal_filter_and_none(dev, rng):
     qo, eo = run_bfp(dev, q, e, fdr, n, batch, mid="none")
     got = O.bfp_dequantize(qo, eo)
     assert O.rel_l2(got, n * O.bfp_dequantize(q, e)) < 1e-4
+
+
+@pytest.mark.parametrize("n,variant", [(512, "auto"), (1024, "auto"), (2048, "auto"), (4096, "auto"),
+                                       (8192, "auto"), (1024, "v16"), (4096, "v16"), (16384, "v16")])
+def test_bfp_full_batch_every_size(dev, n, variant):
+    """2^27 points (full occupancy): 16 transforms spread over the batch,
+    words and exponents bit-identical to the oracle."""
+    import torch
+    import fufft_amd as ff
+    batch = (1 << 27) // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(n)
+    dq = torch.randint(-32767, 32768, (2 * batch * n,), dtype=torch.int16, device=dev, generator=gen)
+    de = torch.randint(-30, 10, (batch * n // ff.BFP_BLOCK,), dtype=torch.int8, device=dev, generator=gen)
+    rng = np.random.default_rng(n)
+    filt = ff.plan_filter(crandn(rng, n), n, variant=variant, kind=ff.FILTER_TAPS)
+    qo, eo = torch.empty_like(dq), torch.empty_like(de)
+    print(f"case bfp full-batch n={n} variant={variant} batch={batch}", flush=True)
+    ff.conv_bfp16(dq, de, to_dev(filt, dev), qo, eo, n=n, batch=batch, variant=variant)
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
+    q_s = dq.view(batch, 2 * n)[idx].cpu().numpy()
+    e_s = de.view(batch, n // ff.BFP_BLOCK)[idx].cpu().numpy()
+    v = 8 if ff.resolve_variant(n, variant) == "r8" else 16
+    oq, oe = O.bfp_conv(q_s, e_s, filt, n, O.kernel_plan(n, v))
+    torch.cuda.synchronize()
+    assert np.array_equal(eo.view(batch, n // ff.BFP_BLOCK)[idx].cpu().numpy(), oe.reshape(16, -1))
+    assert np.array_equal(qo.view(batch, 2 * n)[idx].cpu().numpy(), oq.reshape(16, -1))
+    del dq, de, qo, eo

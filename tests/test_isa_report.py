@@ -33,7 +33,8 @@ def conv(rows):
     return R.conv_rows(rows)
 
 
-def pick(conv, kind, n, v, layout="pad", mid="mul"):
+def pick(conv, kind, n, v, layout=None, mid="mul"):
+    layout = layout or R.default_layout(n, v)
     got = [r for r in conv if r["family"] == "conv1d" and r["kind"] == kind and r["n"] == n and r["v"] == v
            and r["layout"] == layout and r["mid"] == mid]
     assert len(got) == 1, (kind, n, v)
@@ -44,10 +45,10 @@ SIZES = [(n, 16) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + [(n, 8) f
 
 
 def test_no_kernel_spills_or_uses_scratch(rows):
-    """Every kernel of the default (padded) LDS layout is spill-free.  The
-    opt-in XOR layout (FUFFT_LDS_LAYOUT=xor) keeps one address register per
-    tap; at N = 16384 (1024 threads, so at most 128 VGPRs) it spills, which is
-    one more reason the padded layout is the default."""
+    """Every kernel of the default LDS layouts is spill-free.  The opt-in XOR
+    layout (FUFFT_LDS_LAYOUT=xor) keeps one address register per tap; at
+    N = 16384 (1024 threads, so at most 128 VGPRs) it spills, which is one
+    more reason the additive layouts are the default."""
     assert len(rows) > 100
     bad, xor16k = [], []
     for r in rows:
@@ -81,7 +82,7 @@ def test_occupancy_radix8_vs_radix16(conv):
 
 def test_counters_agree_with_model_and_isa(conv):
     """profiles/conv_f32_n4096.md: SQ_INSTS_VALU, SQ_INSTS_LDS and SQ_INSTS_VMEM
-    per wavefront of conv1d_kernel<4096, 8, pad, conv, mul>."""
+    per wavefront of the headline kernel, conv1d_kernel<4096, 8, xchg, conv, mul>."""
     text = (ROOT / "profiles" / "conv_f32_n4096.md").read_text()
 
     def per_wave(counter):

@@ -13,7 +13,9 @@ modulo 32):
   - the conflict degree stays within the bound documented for the layout
     (XOR: conflict free everywhere; PAD: at most 2-way);
   - the reference's own swizzle, derived for 32 banks / 16-lane phases, is not
-    conflict free under this model (why the layout was re-derived).
+    conflict free under this model (why the layout was re-derived);
+  - the per-exchange layouts the kernels use by default are bijections within
+    the slot, additive, conflict free, and free of cross-wavefront races.
 """
 import itertools
 
@@ -217,3 +219,90 @@ def test_unscramble_targets_and_conflicts(v, n):
         worst = max(worst, degree([phys_pad(p, v) for p in pos]))
     # measured bound of the scattered side; the natural side is pass 0's pattern
     assert worst <= (2 if n <= 4096 and (v, n) != (8, 1024) else 4), worst
+
+
+# ---- per-exchange layouts (XchgLds, fufft_plan.hpp) -------------------------------------
+# Exchange e uses phys = i + Mb * (i // (V * Mb)), Mb = the stride of the first
+# wavefront-private pass (M <= 64) after the exchange.  A pass gathers from
+# exchange e - 1 and scatters into exchange e with no barrier in between, so
+# beyond conflicts and additivity the audit checks by brute force that no
+# wavefront's writes land on slots another wavefront still has to read, and
+# that exchanges synchronised by a wavefront fence are read only by their
+# writers.
+def xchg_params(pl, e, v, wl=64):
+    q = e + 1
+    while pl[q][1] > wl:
+        q += 1
+    return v * pl[q][1], pl[q][1]
+
+
+def xchg_phys(i, ma, mb):
+    return i + mb * (i // ma)
+
+
+def xchg_naive(pl, e, v, wl=64):
+    """(M_e, M_{e+1}): conflict free too, but races after a pass spanning wavefronts"""
+    return pl[e][1], pl[e + 1][1]
+
+
+def xchg_problems(n, v, rule, wl=64):
+    pl = plan(n, v)
+    T, NP = n // v, len(pl)
+    lay = [rule(pl, e, v) for e in range(NP - 1)]
+    waves = max(1, T // wl)
+    out = []
+
+    def slots(p, e, w):
+        R, M = pl[p]
+        lanes = range(w * wl, min(T, (w + 1) * wl)) if T > wl else range(T)
+        return {xchg_phys(tap_pos(L, g, k, R, M, T), *lay[e])
+                for L in lanes for g in range(v // R) for k in range(R)}
+
+    for e in range(NP - 1):
+        ph = [xchg_phys(i, *lay[e]) for i in range(n)]
+        if len(set(ph)) != n or max(ph) >= n + n // v:
+            out.append(("bijection / slot size", e))
+        for p in (e, e + 1):
+            R, M = pl[p]
+            for g, k in itertools.product(range(v // R), range(R)):
+                lanes = []
+                for wl_i in range(64):
+                    t, L = divmod(wl_i, T) if T < 64 else (0, wl_i)
+                    lanes.append(t * (n + n // v) + xchg_phys(tap_pos(L, g, k, R, M, T), *lay[e]))
+                if degree(lanes) > 1:
+                    out.append(("conflict", e, p, g, k))
+                for L in range(T):
+                    base = tap_pos(L, g, 0, R, M, T)
+                    if xchg_phys(base + k * M, *lay[e]) != xchg_phys(base, *lay[e]) + xchg_phys(k * M, *lay[e]):
+                        out.append(("not additive", e, p, g, k))
+                        break
+    for p in range(1, NP - 1):                    # gather (e = p - 1) -> scatter (e = p), no barrier
+        for w in range(waves):
+            written = slots(p, p, w)
+            for w2 in range(waves):
+                if w2 != w and written & slots(p, p - 1, w2):
+                    out.append(("clobbers another wavefront's input", p, w, w2))
+    for e in range(NP - 1):
+        if T > wl and exchange_in_wave(n, v, e, wl):
+            for w in range(waves):
+                if not slots(e + 1, e, w) <= slots(e, e, w):
+                    out.append(("fence-only exchange read across wavefronts", e, w))
+    return out
+
+
+XCHG_PLANS = [(16, n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + \
+             [(8, n) for n in (512, 1024, 2048, 4096, 8192)]
+
+
+@pytest.mark.parametrize("v,n", XCHG_PLANS)
+def test_exchange_layouts(v, n):
+    assert xchg_problems(n, v, xchg_params) == []
+
+
+@pytest.mark.parametrize("v,n", [(8, 8192), (16, 8192), (16, 16384)])
+def test_exchange_layouts_audit_catches_the_race(v, n):
+    """Switching layouts inside a pass that spans wavefronts races: the
+    per-exchange (M_e, M_{e+1}) rule fails the audit exactly where it gave
+    wrong results on the GPU at full batch (radix 8, N = 8192)."""
+    kinds = {x[0] for x in xchg_problems(n, v, xchg_naive)}
+    assert kinds == {"clobbers another wavefront's input"}
