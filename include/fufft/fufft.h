@@ -151,8 +151,9 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
  *   [4], [5] start time (s_memtime), low and high word,
  *   [6 .. 10] phase << 24 | cycles since start (saturated at 2^24 - 1) for
  *   phases 1 load, 2 forward DIF, 3 mid operation, 4 inverse DIT, 5 store.
- * Padded LDS layout only (the default); a call that would need more than one
- * launch (per-signal filters beyond 4 GiB) returns FUFFT_ERR_UNSUPPORTED. */
+ * Default LDS layouts only (not FUFFT_LDS_LAYOUT=xor); a call that would need
+ * more than one launch (per-signal filters beyond 4 GiB) returns
+ * FUFFT_ERR_UNSUPPORTED. */
 #define FUFFT_TIMER_STRIDE 12
 int fufft_transforms_per_workgroup(int64_t n, int variant);
 int fufft_conv_timed_f32(const void* in, const void* filt, int64_t filt_stride,
