@@ -78,6 +78,7 @@ def _load() -> C.CDLL:
         "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
         "fufft_conv_large_f32": ([vp, vp, i64, i64, i64, i32, vp], i32),
         "fufft_plan2d": ([i64, i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
+        "fufft_plan2d_column_order": ([i64, i64, C.POINTER(C.c_int32)], i32),
         "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, vp, vp], i32),
         "fufft_conv2d_f32": ([vp, vp, i64, vp, i64, i64, i64, i32, vp], i32),
         "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp], i32),
@@ -335,9 +336,18 @@ def plan2d(h: int, w: int) -> tuple[int, int]:
     return vr.value, vc.value
 
 
+def column_order2d(h: int, w: int) -> np.ndarray:
+    """slot[c]: the row plan's digit-order slot held by column c of 2D filters and spectra."""
+    out = np.empty(w, dtype=np.int32)
+    check(lib.fufft_plan2d_column_order(h, w, out.ctypes.data_as(C.POINTER(C.c_int32))),
+          "fufft_plan2d_column_order")
+    return out
+
+
 def plan_filter2d(x: np.ndarray, h: int, w: int, kind: int = FILTER_SPECTRUM,
                   fold_inv_n: bool = True) -> np.ndarray:
-    """2D filter as the column kernels read it: slot (r, c) = bin (rev_h(r), rev_w(c))."""
+    """2D filter as the column kernels read it: entry (r, c) = bin (rev_h(r), rev_w(slot(c))),
+    slot = column_order2d(h, w)."""
     src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
     assert src.size == h * w
     out = np.empty(h * w, dtype=np.complex64)

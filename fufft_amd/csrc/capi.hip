@@ -842,14 +842,26 @@ int check_2d(int64_t h, int64_t w, int64_t batch, Plan2d* p)
 }
 
 // the three launches of a 2D pass share this row-launch helper: n = w points
-// per row, h * batch rows
+// per row, h * batch rows.  Row spectra are lane-major (position L + k*T of a
+// row holds digit-order slot L*V + k): the row forward then stores and the
+// row inverse loads whole contiguous runs per wavefront.  The column kernels
+// do not care which slot a column holds, so 2D filters and spectra carry
+// their columns in the same order (fufft_plan2d_column_order).
 Conv1dParams rows_params(const float2* tw, int64_t h, int64_t batch)
 {
    Conv1dParams p{};
    p.tw = tw;
    p.ntrans = (uint32_t)(h * batch);
    p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR;
+   p.sl = FUFFT_LAYOUT_LANE;
    return p;
+}
+
+// digit-order slot held by column c of a 2D row spectrum (lane-major rows)
+int64_t column_slot(int64_t c, int64_t w, int vr)
+{
+   const int64_t T = w / vr;
+   return (c % T) * vr + c / T;
 }
 
 ColParams col_params(const float2* tw, int64_t w, int64_t batch)
@@ -863,6 +875,16 @@ ColParams col_params(const float2* tw, int64_t w, int64_t batch)
 }  // namespace
 
 extern "C" {
+
+int fufft_plan2d_column_order(int64_t h, int64_t w, int32_t* slot)
+{
+   Plan2d pl;
+   const int st = plan2d(h, w, &pl);
+   if(st != FUFFT_OK) return st;
+   if(!slot) return FUFFT_ERR_INVALID;
+   for(int64_t c = 0; c < w; c++) slot[c] = (int32_t)column_slot(c, w, pl.vr);
+   return FUFFT_OK;
+}
 
 int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind, int fold_inv_n,
                             const float* in, float* out)
@@ -893,7 +915,7 @@ int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind, int fold_inv_
    for(int64_t r = 0; r < h; r++) {
       const int64_t br = group_reverse((int32_t)r, pl.rc, pl.nc);
       for(int64_t c = 0; c < w; c++) {
-         const int64_t bc = group_reverse((int32_t)c, pl.rr, pl.nr);
+         const int64_t bc = group_reverse((int32_t)column_slot(c, w, pl.vr), pl.rr, pl.nr);
          out[2 * (r * w + c)]     = (float)(s[2 * (br * w + bc)] * scale);
          out[2 * (r * w + c) + 1] = (float)(s[2 * (br * w + bc) + 1] * scale);
       }
@@ -922,12 +944,13 @@ int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t
       g.scale = scale;
       g.dh = digits_of(pl.rc, pl.nc);
       g.dw = digits_of(pl.rr, pl.nr);
+      g.lane_v = pl.vr;
       return status_of(launch_gather(g, s));
    }
    // taps: rows DIF (scaled) into out, then columns DIF in place -- the
    // forward half of fufft_conv2d_f32
    Conv1dParams r = rows_params(tw, h, count);
-   r.in0 = in; r.out0 = out; r.scale = scale;
+   r.in0 = in; r.out0 = out; r.scale = scale; r.fl = FUFFT_LAYOUT_LANE;
    if((st = run_conv1d(K_PLAN_TAPS, (int)w, pl.vr, r, stream)) != FUFFT_OK) return st;
    ColParams c = col_params(tw, w, count);
    c.in = out; c.out = out;

@@ -48,7 +48,7 @@ enum { TIMER_STRIDE = 12, TIMER_MARKS = 5 };
 struct Conv1dParams {
    const void*   in0;      // complex input, or real x (K_CONV_R2)
    const void*   in1;      // real y (K_CONV_R2)
-   const void*   spec;     // digit-order spectrum (K_APPLY)
+   const void*   spec;     // spectrum (K_APPLY), laid out as sl says
    const void*   filt;     // filter, digit order or lane-major
    void*         out0;     // complex output / spectrum (K_FWD) / real u
    void*         out1;     // real v (K_CONV_R2)
@@ -58,6 +58,7 @@ struct Conv1dParams {
    uint32_t      scount;   // transform t uses spectrum (t % scount)
    int32_t       mid;      // MID_MUL / MID_CONJ / MID_NONE
    int32_t       fl;       // FLT_DR / FLT_LANE (filter read; K_PLAN_TAPS: layout written)
+   int32_t       sl;       // FLT_DR / FLT_LANE: spectrum K_FWD writes, K_APPLY reads
    float         scale;    // K_PLAN_TAPS: factor applied to the spectrum
    uint32_t*     timing;   // K_CONV_TIMED: TIMER_STRIDE words per workgroup
    uint32_t      timing_groups;   // workgroups that write a record
@@ -76,7 +77,7 @@ struct GatherParams {
    const float2* in;       // natural-order spectra
    float2*       out;      // planned filters (must not alias in)
    uint64_t      total;    // points over all items
-   int32_t       lane_v;   // 1D lane-major output: values per lane; 0 = digit order
+   int32_t       lane_v;   // lane-major columns: values per lane of the row plan; 0 = digit order
    float         scale;
    GatherDigits  dh, dw;   // rows (dh.np = 0 in 1D) and row digits
 };

@@ -5,8 +5,9 @@
 // order (bench_fufft.cu:410-428) and the 2D order (verify_kernel.cpp:738-748).
 // This kernel does the permutation for spectra already in device memory:
 // output position (r, c) of an h x w item (h = 1 in 1D) receives bin
-// (rev_h(r), rev_w(c)) times scale, each rev a bit-group reversal over the
-// plan's radix widths in pass order.  One thread per output point, so the
+// (rev_h(r), rev_w(c')) times scale, each rev a bit-group reversal over the
+// plan's radix widths in pass order, c' = c or, lane-major, the digit-order
+// slot that position c holds.  One thread per output point, so the
 // writes are coalesced and the reads gather; planning runs once per filter,
 // not on the conv's hot path.  (Taps are planned by the conv kernels' own
 // forward half, K_PLAN_TAPS.)
@@ -37,13 +38,14 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherParams p)
    const uint32_t per = 1u << lb;
    const uint64_t item = i >> lb;
    const uint32_t o = (uint32_t)(i & (per - 1u));
-   uint32_t slot = o;
+   const uint32_t r = o >> p.dw.bits;
+   uint32_t c = o & ((1u << p.dw.bits) - 1u);
    if(p.lane_v) {
-      // lane-major (1D): output position L + k*T holds slot L*V + k
-      const uint32_t T = per / (uint32_t)p.lane_v;
-      slot = (o % T) * (uint32_t)p.lane_v + o / T;
+      // lane-major along the row (1D filters, 2D columns): position L + k*T
+      // holds digit-order slot L*V + k
+      const uint32_t T = (1u << p.dw.bits) / (uint32_t)p.lane_v;
+      c = (c % T) * (uint32_t)p.lane_v + c / T;
    }
-   const uint32_t r = slot >> p.dw.bits, c = slot & ((1u << p.dw.bits) - 1u);
    const uint32_t src = (group_reverse_dev(r, p.dh) << p.dw.bits) | group_reverse_dev(c, p.dw);
    const float2 v = p.in[item * per + src];
    p.out[i] = make_float2(v.x * p.scale, v.y * p.scale);

@@ -257,16 +257,25 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
 
 /* ---- 2D ---------------------------------------------------------------------------
  * h x w images, row-major, h and w single-launch sizes.  Rows DIF, columns
- * DIF, mid, columns DIT, rows DIT (fufft_conv2d, fufft.cuh:1209-1258); the
- * filter slot (r, c) holds spectrum bin (mixedrev_h(r), mixedrev_w(c)).
+ * DIF, mid, columns DIT, rows DIT (fufft_conv2d, fufft.cuh:1209-1258).
  * Runs as three launches in place on out: row forward, fused column conv,
- * row inverse (7 HBM passes for an image too large for one workgroup). */
+ * row inverse (7 HBM passes for an image too large for one workgroup).
+ * 2D filters and spectra: entry (r, c) holds spectrum bin
+ * (mixedrev_h(r), mixedrev_w(slot(c))), where slot(c) is the row plan's
+ * digit-order slot that column c holds (fufft_plan2d_column_order).  The
+ * reference's own order (verify_kernel.cpp:738-748) has slot(c) = c; here the
+ * rows are lane-major, slot(c) = (c % T)*V + c / T with V the row plan's
+ * values per lane and T = w / V, so the row kernels store and load whole
+ * contiguous runs.  fufft_plan_filter2d_f32 / _device_f32 produce this order. */
 /* Values per lane of the row plan (the 1D kernel at FUFFT_AUTO for length w)
  * and of the column plan (8 up to h = 512, 16 for h = 1024, 2048); the
  * per-dimension digit orders are those of fufft_digit_order with that many
  * values per lane.  No reference counterpart (the reference fixes both
  * dimensions at compile time, fufft.cuh:1209-1214). */
 int fufft_plan2d(int64_t h, int64_t w, int* v_rows, int* v_cols);
+/* slot[c] (w entries) = the row plan's digit-order slot held by column c of
+ * 2D filters and spectra.  No reference counterpart (a layout of this build). */
+int fufft_plan2d_column_order(int64_t h, int64_t w, int32_t* slot);
 int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind,
                             int fold_inv_n, const float* in, float* out);
 int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride,
@@ -277,7 +286,7 @@ int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride,
 int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt,
                         int64_t filt_stride, float* u, float* v, void* work,
                         int64_t h, int64_t w, int64_t batch, void* stream);
-/* split 2D path: fwd = rows DIF then columns DIF into spec (2D digit order);
+/* split 2D path: fwd = rows DIF then columns DIF into spec (the 2D order above);
  * apply = spec mid filt, columns DIT, rows DIT into out.  spec_stride 0 shares
  * one spectrum across the batch. */
 int fufft_fwd2d_f32(const void* in, void* spec, int64_t h, int64_t w,

@@ -50,3 +50,15 @@ def bits_equal(a, b) -> bool:
     a = np.ascontiguousarray(a)
     b = np.ascontiguousarray(b)
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def cols_to_dr(x, h, w):
+    """A 2D filter or spectrum in the library's column order (lane-major rows,
+    fufft_plan2d_column_order) re-ordered to the reference's digit order,
+    slot (r, c) = bin (mixedrev_h(r), mixedrev_w(c)), which the oracle uses."""
+    import fufft_amd as ff
+    slot = ff.column_order2d(h, w)
+    a = np.asarray(x).reshape(-1, h, w)
+    out = np.empty_like(a)
+    out[:, :, slot] = a
+    return out.reshape(np.shape(x))

@@ -8,7 +8,7 @@ convolution.  The split path equals the fused one bit for bit.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, crandn, cuniform
+from conftest import bits_equal, cols_to_dr, crandn, cuniform
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -58,7 +58,7 @@ def test_conv2d_matches_oracle(dev, h, w, mid, rng):
     ph, pw = plans(h, w)
     print(f"case conv2d {h}x{w} mid={mid} plans {ph.radices} x {pw.radices}", flush=True)
     got = run_conv2d(dev, a, filt, h, w, mid=mid)
-    assert bits_equal(got, O.conv2d(a, filt, h, w, ph, pw, mid=mid))
+    assert bits_equal(got, O.conv2d(a, cols_to_dr(filt, h, w), h, w, ph, pw, mid=mid))
     assert O.rel_l2(got, fp64_conv2d(a, taps, h, w, mid)) <= TOL_F32
 
 
@@ -73,7 +73,7 @@ def test_conv2d_per_image_filter_in_place(dev, rng):
     print("case conv2d per-image filters, in place", flush=True)
     ff.conv2d(buf, to_dev(filt, dev), buf, h, w, batch=batch, filt_stride=h * w)
     torch.cuda.synchronize()
-    assert bits_equal(buf.cpu().numpy(), O.conv2d(a, filt, h, w, ph, pw, filt_stride=h * w))
+    assert bits_equal(buf.cpu().numpy(), O.conv2d(a, cols_to_dr(filt, h, w), h, w, ph, pw, filt_stride=h * w))
 
 
 @pytest.mark.parametrize("h,w", [(512, 512), (256, 1024)])
@@ -95,7 +95,7 @@ def test_conv2d_two_real_images(dev, h, w, rng):
     torch.cuda.synchronize()
     z = (x + 1j * y).astype(np.complex64)
     ph, pw = plans(h, w)
-    want = O.conv2d(z, filt, h, w, ph, pw)
+    want = O.conv2d(z, cols_to_dr(filt, h, w), h, w, ph, pw)
     assert bits_equal(u.cpu().numpy(), np.ascontiguousarray(want.real))
     assert bits_equal(v.cpu().numpy(), np.ascontiguousarray(want.imag))
     s = np.fft.fft2(taps.reshape(h, w).astype(np.float64))
@@ -123,9 +123,10 @@ def test_split_2d_equals_fused(dev, h, w, rng):
     ff.apply2d(spec, df, out, h, w, batch=nf, spec_stride=0, filt_stride=h * w)
     torch.cuda.synchronize()
     got_spec = spec.cpu().numpy()
-    assert bits_equal(got_spec, O.fwd2d(a, h, w, ph, pw))
+    assert bits_equal(cols_to_dr(got_spec, h, w), O.fwd2d(a, h, w, ph, pw))
     got = out.cpu().numpy()
-    assert bits_equal(got, O.apply2d(got_spec, filters, h, w, nf, ph, pw, spec_stride=0, filt_stride=h * w))
+    assert bits_equal(got, O.apply2d(cols_to_dr(got_spec, h, w), cols_to_dr(filters, h, w), h, w, nf, ph, pw,
+                                     spec_stride=0, filt_stride=h * w))
     fused = run_conv2d(dev, np.tile(a, nf), filters, h, w, filt_stride=h * w)
     assert bits_equal(got, fused)
 
@@ -153,7 +154,7 @@ def test_split_2d_baseline_config(dev, rng):
     fa = np.fft.fft2(a.reshape(h, w).astype(np.complex128))
     for i in (0, 77, 255):
         f_i = filters[i * h * w:(i + 1) * h * w]
-        assert bits_equal(got[i], O.apply2d(sp, f_i, h, w, 1, ph, pw))
+        assert bits_equal(got[i], O.apply2d(cols_to_dr(sp, h, w), cols_to_dr(f_i, h, w), h, w, 1, ph, pw))
         want = np.fft.ifft2(fa * spec_nat[i].reshape(h, w).astype(np.complex128)).reshape(-1)
         assert O.rel_l2(got[i], want) <= TOL_F32
 

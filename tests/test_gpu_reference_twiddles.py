@@ -19,7 +19,7 @@ The module switches the table back to the default source when it ends.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, crandn, cuniform
+from conftest import bits_equal, cols_to_dr, crandn, cuniform
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -165,7 +165,7 @@ def test_conv2d_equals_libm_oracle(ref_tw, h, w, rng):
     da = to_dev(a, dev)
     out = torch.empty_like(da)
     ff.conv2d(da, to_dev(filt, dev), out, h, w, batch=2)
-    assert bits_equal(host(out), O.conv2d(a, filt, h, w, ph, pw, tw=O.TW_LIBM))
+    assert bits_equal(host(out), O.conv2d(a, cols_to_dr(filt, h, w), h, w, ph, pw, tw=O.TW_LIBM))
 
 
 @pytest.mark.parametrize("n", [512, 4096])

@@ -91,7 +91,12 @@ def test_filter_planning_large_and_2d(rng):
     S = np.fft.fft2(taps2.reshape(h, w).astype(np.complex128)) / (h * w)
     rh, rw = O.mixedrev(O.kernel_plan(h, vc)), O.mixedrev(O.kernel_plan(w, vr))
     got2 = ff.plan_filter2d(taps2, h, w, kind=ff.FILTER_TAPS)
-    want2 = S[np.ix_(rh, rw)].reshape(-1)
+    # columns in the library's order: column c holds row slot (c % T) * vr + c // T
+    slot = ff.column_order2d(h, w)
+    T = w // vr
+    assert np.array_equal(slot, [(c % T) * vr + c // T for c in range(w)])
+    assert sorted(slot) == list(range(w))
+    want2 = S[np.ix_(rh, rw[slot])].reshape(-1)
     assert np.max(np.abs(got2 - want2)) <= 2e-7 * np.max(np.abs(want2))
 
 
