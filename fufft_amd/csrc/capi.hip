@@ -176,14 +176,20 @@ bool pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
-// FUFFT_AUTO resolves to the faster lane layout measured on MI355X: radix 8
-// (eight values per lane: twice the wavefronts per CU for the same LDS) from
-// N = 512 to 8192, radix 16 elsewhere.
+// FUFFT_AUTO resolves to the faster lane layout measured on MI355X, one rule
+// for the fp32 and the BFP conv (a filter planned at FUFFT_AUTO must match
+// both): radix 8 at N = 512 and 4096, radix 16 elsewhere.  Same box, 2^27
+// points, Gpt/s radix 8 / radix 16: fp32 N = 512 371 / 345, 1024 330 / 337,
+// 2048 323 / 328, 4096 317 / 306, 8192 257 / 255; BFP N = 1024 406 / 424,
+// 2048 384 / 386, 4096 365 / 368, 8192 215 / 298.
 int resolve_variant(int64_t n, int variant)
 {
    if(variant != FUFFT_AUTO) return variant;
-   return (n >= 512 && n <= 8192) ? FUFFT_R8 : FUFFT_V16;
+   return (n == 512 || n == 4096) ? FUFFT_R8 : FUFFT_V16;
 }
+
+// The four-step middle always runs radix 8 (N = 512 .. 4096 per chunk).
+constexpr int kLargeMiddleV = 8;
 
 int values_per_lane(int variant)
 {
@@ -685,7 +691,7 @@ static int large_radices(int64_t n, int* lout, int* mid, int* r)
    if(st != FUFFT_OK) return st;
    int np = 0;
    for(int i = 0; i < *lout; i++) r[np++] = 16;
-   np += factor(*mid, values_per_lane(resolve_variant(*mid, FUFFT_AUTO)), r + np);
+   np += factor(*mid, kLargeMiddleV, r + np);
    return np;
 }
 
@@ -751,7 +757,7 @@ int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int
    p.tw = tw; p.in0 = out; p.out0 = out;
    p.ntrans = (uint32_t)(count * (n / mn));
    p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR; p.scale = scale;
-   return run_conv1d(K_PLAN_TAPS, mn, values_per_lane(resolve_variant(mn, FUFFT_AUTO)), p, stream);
+   return run_conv1d(K_PLAN_TAPS, mn, kLargeMiddleV, p, stream);
 }
 
 int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64_t n,
@@ -765,7 +771,7 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
    if(!buf || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
    if(!aligned16(buf) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
    if(filt_stride != 0 && filt_stride != n) return FUFFT_ERR_INVALID;
-   const int v = values_per_lane(resolve_variant(mn, FUFFT_AUTO));
+   const int v = kLargeMiddleV;
    if(!conv1d_supported(mn, v)) return FUFFT_ERR_UNSUPPORTED;
    Conv1dParams p{};
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;

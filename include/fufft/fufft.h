@@ -49,9 +49,10 @@ extern "C" {
 /* lane layout / radix family */
 #define FUFFT_V16  0   /* 16 values per lane, radix 16 (fufft_pipeline_v16)  */
 #define FUFFT_R8   1   /* 8 values per lane, radix 8 (fufft_pipeline_ip)     */
-#define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X:
-                          FUFFT_R8 for 512 <= N <= 8192, else FUFFT_V16.
-                          The filter must be planned with the same variant. */
+#define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X, one
+                          rule for the fp32 and the BFP conv: FUFFT_R8 at
+                          N = 512 and 4096, FUFFT_V16 elsewhere.  The filter
+                          must be planned with the same variant. */
 
 /* filter layouts */
 #define FUFFT_LAYOUT_DR    0  /* slot i holds bin mixedrev(i) (MidMultiply, fufft.cuh:635) */
@@ -247,7 +248,7 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
  * levels (run_large / MidLaunch, bench_fufft.cu:357-492;
  * fufft_outer_pass_r, fufft.cuh:1113-1140).  buf is transformed in place.
  * filt is in the chained digit order (fufft_large_digit_order).
- * 4*lout + 3 HBM passes. */
+ * 4*lout + 3 HBM passes.  The middle runs radix 8 (FUFFT_R8) at every mid. */
 int fufft_large_plan(int64_t n, int* lout, int* mid);
 int fufft_large_digit_order(int64_t n, int32_t* perm);
 int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n,

@@ -88,7 +88,7 @@ def test_bfp_per_signal_filter_and_none(dev, rng):
     x = config3_signals(rng, batch, n)
     q, e = ff.bfp_quantize(x)
     spec = (crandn(rng, (batch, n)) / n).astype(np.complex64)
-    plan = O.kernel_plan(n, 8)
+    plan = O.kernel_plan(n, 8 if ff.resolve_variant(n, "auto") == "r8" else 16)
     fdr = np.ascontiguousarray(spec[:, O.mixedrev(plan)]).reshape(-1)
     print("case bfp per-signal filter", flush=True)
     qo, eo = run_bfp(dev, q, e, fdr, n, batch, filt_stride=n)

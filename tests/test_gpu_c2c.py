@@ -170,7 +170,7 @@ def test_plan_device_large(dev, n, rng):
     host_s = np.stack([ff.plan_filter_large(spec[i], n, kind=ff.FILTER_SPECTRUM) for i in range(count)])
     assert bits_equal(got_s, host_s)
     lout, mid = ff.large_plan(n)
-    want_t = O.fwd(taps, n, O.large_plan(lout, mid, mid_v=V[ff.resolve_variant(mid, "auto")]))
+    want_t = O.fwd(taps, n, O.large_plan(lout, mid, mid_v=8))          # the middle runs radix 8
     assert bits_equal(got_t.reshape(-1), scaled(want_t, 1.0 / n))
     host_t = np.stack([ff.plan_filter_large(taps[i], n, kind=ff.FILTER_TAPS) for i in range(count)])
     assert O.rel_l2(got_t, host_t) <= 1e-6

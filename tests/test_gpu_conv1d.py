@@ -224,7 +224,7 @@ def test_config1_every_signal_against_fp64(dev):
     filt = ff.plan_filter(taps, n, "auto", kind=ff.FILTER_TAPS)
     print("case config1 n=1024 batch=8192", flush=True)
     got = run_conv(dev, a, filt, n, 0, "mul", "auto", "dr")
-    assert bits_equal(got, O.conv(a, filt, n, O.kernel_plan(n, 8)))
+    assert bits_equal(got, O.conv(a, filt, n, O.kernel_plan(n, V[ff.resolve_variant(n, "auto")])))
     want = np.fft.ifft(np.fft.fft(a.astype(np.complex128), axis=1)
                        * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
     per = np.linalg.norm(got.reshape(batch, n) - want, axis=1) / np.linalg.norm(want, axis=1)
