@@ -146,7 +146,7 @@ bfp_kernel(const BfpParams p)
    forward_dif<PL, LD, (T < 64 ? 64 : T), 64, KEEP_STORE>(r, A, L, tw, kc);
    {
       const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
-      const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
+      const uint32_t fo = (modulo_count(t, p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
       mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
    }
    inverse_dit<PL, LD, (T < 64 ? 64 : T), 64, KEEP_USE>(r, A, L, tw, kc);
@@ -203,6 +203,7 @@ static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
    constexpr int T = N / V, CPB = bfp_cpb(T);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
    const void* k = reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID>);
+   if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
    static std::atomic<uint64_t> lds_ok{0};
    if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);

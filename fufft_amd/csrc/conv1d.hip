@@ -86,12 +86,12 @@ conv1d_kernel(const Conv1dParams p)
       const Buf sb(p.spec, p.scount * (uint32_t)N * 8u);
       if(p.sl == FLT_LANE) {
          // lane-major: slot L*V + k at position L + k*T, one coalesced load per k
-         const uint32_t so = ((t % p.scount) * N + L) * 8u;
+         const uint32_t so = (modulo_count(t, p.scount) * N + L) * 8u;
 #pragma unroll
          for(int k = 0; k < V; k++) r[k] = sb.ld2(so, k * T * 8);
       } else {
          // digit order: slots L*V .. L*V+V-1, two complex per 16-byte load
-         const uint32_t so = ((t % p.scount) * N + L * V) * 8u;
+         const uint32_t so = (modulo_count(t, p.scount) * N + L * V) * 8u;
 #pragma unroll
          for(int m = 0; m < V / 2; m++) {
             const float4 q = sb.ld4(so, m * 16);
@@ -157,7 +157,7 @@ conv1d_kernel(const Conv1dParams p)
    } else {
       if constexpr(!C2C_INV) {
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
-         const uint32_t fo = ((t % p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
+         const uint32_t fo = (modulo_count(t, p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
          mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
       }
       stamp(3);
@@ -207,6 +207,7 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
    constexpr int T = N / V, CPB = cpb_for(T);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
    const void* k = reinterpret_cast<const void*>(&conv1d_kernel<N, V, LAYOUT, KIND, MID>);
+   if(!modulo_count_ok(p.fcount, p.ntrans) || !modulo_count_ok(p.scount, p.ntrans)) return hipErrorInvalidValue;
    static std::atomic<uint64_t> lds_ok{0};
    if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);

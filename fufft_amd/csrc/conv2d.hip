@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
    float2 r[V];
 
    if constexpr(KIND == COL_APPLY) {
-      const Buf sb(static_cast<const char*>(p.spec) + (size_t)(img % p.scount) * ibytes, ibytes);
+      const Buf sb(static_cast<const char*>(p.spec) + (size_t)modulo_count(img, p.scount) * ibytes, ibytes);
 #pragma unroll
       for(int k = 0; k < V; k++) r[k] = sb.ld2(dro, k * W8);
    } else {
@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
       for(int k = 0; k < V; k++) ob.st2(r[k], dro, k * W8);
    } else {
       {
-         const Buf fb(static_cast<const char*>(p.filt) + (size_t)(img % p.fcount) * ibytes, ibytes);
+         const Buf fb(static_cast<const char*>(p.filt) + (size_t)modulo_count(img, p.fcount) * ibytes, ibytes);
          mid_op<PL, MID>(r, fb, dro, W8);
       }
       inverse_dit<PL, LD, C * T, 64 / C, KEEP_I>(r, A, L, tw, kc);
@@ -88,7 +88,8 @@ static hipError_t launch_col_one(const ColParams& p, hipStream_t s)
    const void* k = reinterpret_cast<const void*>(&col_kernel<H, V, LAYOUT_PAD, KIND, MID, C>);
    static std::atomic<uint64_t> lds_ok{0};
    if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
-   if(p.w % C || p.fcount == 0 || p.scount == 0) return hipErrorInvalidValue;
+   if(p.w % C || !modulo_count_ok(p.fcount, p.nimg) || !modulo_count_ok(p.scount, p.nimg))
+      return hipErrorInvalidValue;
    const uint64_t blocks = (uint64_t)p.nimg * (p.w / C);
    if(blocks > 0x7fffffffu) return hipErrorInvalidValue;
    const dim3 grid((unsigned)blocks), block(C * T);

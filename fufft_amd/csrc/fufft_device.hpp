@@ -295,6 +295,21 @@ struct Buf {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// t % count for the filter and spectrum counts the entry points produce: one
+// shared array (1), one per transform (count >= the launch's transforms, so
+// t < count), or one per chunk of a four-step transform (a power of two).
+// Three VALU operations instead of a runtime integer division (about a dozen);
+// the launchers reject any other count (modulo_count_ok).
+__device__ __forceinline__ uint32_t modulo_count(uint32_t t, uint32_t count)
+{
+   return t < count ? t : t & (count - 1u);
+}
+
+__host__ __device__ constexpr bool modulo_count_ok(uint32_t count, uint32_t ntrans)
+{
+   return count != 0 && (count >= ntrans || (count & (count - 1u)) == 0);
+}
+
 // ---- synchronisation between passes -------------------------------------------
 // A transform held by one wavefront needs no s_barrier: LDS operations of a
 // wave execute in order, so a wavefront-scope fence (which stops the compiler
