@@ -19,6 +19,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libfufft_amd.so"
+PROBE_LIB = PKG / "libfufft_lds_probe.so"
 ORACLE = ROOT / "oracle"
 REFERENCE = Path(os.environ.get("FUFFT_REFERENCE", "/root/reference"))
 
@@ -64,6 +65,13 @@ def build_library(jobs: int = 8) -> Path:
     return LIB
 
 
+def build_probe() -> Path:
+    """The LDS bank probe (a diagnostic, python -m fufft_amd.lds_probe)."""
+    src = CSRC / "probe" / "lds_probe.hip"
+    _run([HIPCC, *HIPFLAGS, "-shared", "-o", str(PROBE_LIB), str(src)])
+    return PROBE_LIB
+
+
 def build_oracle() -> None:
     _run(["make", "-s", "-C", str(ORACLE)])
     if (REFERENCE / "verify_kernel.cpp").exists() and shutil.which("g++"):
@@ -73,6 +81,7 @@ def build_oracle() -> None:
 def build(jobs: int = 8) -> None:
     build_oracle()
     build_library(jobs)
+    build_probe()
 
 
 if __name__ == "__main__":

@@ -12,10 +12,13 @@
 // Mapping: thread = (lane L of the column transform, column col) with the
 // column fastest, so every tap load or store of a wavefront covers 64/C rows
 // of C consecutive points -- full 128-byte runs for C = 16.  Each column keeps
-// its own LDS slot; slots are skewed by 32/C float2 so that the C columns of a
-// half-wavefront start on distinct bank pairs, which makes every exchange of
-// the padded layout conflict-free under the 64-bank model (audited on the
-// CPU in tests/test_lds_audit.py).
+// its own LDS slot.  The exchanges are ds_read2_b64 / ds_write2_b64, and
+// gfx950 services each of their 8-byte accesses 16 lanes at a time: lanes of
+// one quarter-wavefront conflict when their float2 slots agree modulo 16
+// (measured with SQ_LDS_BANK_CONFLICT; tests/test_lds_audit.py).  A quarter
+// holds 16/C lanes L of C columns, so slots are skewed by 16/C float2 (the
+// padded slot size is a multiple of 16): the columns then fall on distinct
+// residues, and every exchange is conflict-free.
 #include "fufft_device.hpp"
 #include "fufft_plan.hpp"
 #include "fufft_internal.hpp"
@@ -32,7 +35,7 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
    using PL = Plan<H, V>;
    using LD = Lds<V, LAYOUT>;
    constexpr int T     = PL::T;
-   constexpr int SLOTC = LD::size(H) + 32 / C;
+   constexpr int SLOTC = LD::size(H) + 16 / C;
 
    extern __shared__ float2 lds[];
    const int col = threadIdx.x % C;
@@ -83,7 +86,7 @@ template<int H, int KIND, int MID>
 static hipError_t launch_col_one(const ColParams& p, hipStream_t s)
 {
    constexpr int V = col_v(H), T = H / V, C = col_c(H);
-   constexpr int SLOTC = Lds<V, LAYOUT_PAD>::size(H) + 32 / C;
+   constexpr int SLOTC = Lds<V, LAYOUT_PAD>::size(H) + 16 / C;
    const size_t shm = (size_t)C * SLOTC * sizeof(float2);
    const void* k = reinterpret_cast<const void*>(&col_kernel<H, V, LAYOUT_PAD, KIND, MID, C>);
    static std::atomic<uint64_t> lds_ok{0};

@@ -17,6 +17,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 #include <utility>
 
 #include "fufft_device.hpp"
@@ -379,6 +380,60 @@ __device__ __forceinline__ int lane_bin(int L)
    return f;
 }
 
+// Layout of the digit <-> natural exchange.  Its paired LDS accesses conflict
+// when lanes of a quarter-wavefront (16 lanes, lane bits 0-3) hit slots that
+// agree modulo 16.  The natural side touches L + q*T: those 16 lanes differ in
+// bits 0-3.  The digit side touches lane_bin(L) + k*T: they differ in the bin
+// bits where lane bits 0-3 land, most of them high.  phys = i ^ (each such
+// high bin bit copied onto one of the bits 0-3 the bin does not already
+// vary), so both sides cover 16 residues.  Bits from log2(T) up pass through,
+// so offsets k*T and q*T stay additive (cphys(off) = off); the map is a
+// bijection on [0, N) because bits 0-3 only receive bits above them.
+template<class PL>
+struct UnscrambleLds {
+   // bit of lane_bin(L) that lane bit b becomes
+   static constexpr int bin_bit(int b)
+   {
+      int w = 0;
+      for(int p = 0; p < PL::NP - 1; p++) {
+         const int d = ilog2c(PL::stride(p) / PL::V), r = ilog2c(PL::radix(p));
+         if(b >= d && b < d + r) return w + b - d;
+         w += r;
+      }
+      return -1;
+   }
+   struct Moves { int n = 0; int src[4] = {}; int dst[4] = {}; };
+   static constexpr Moves moves()
+   {
+      Moves m;
+      bool low[4] = {};
+      for(int b = 0; b < 4; b++)
+         if(bin_bit(b) >= 0 && bin_bit(b) < 4) low[bin_bit(b)] = true;
+      int next = 0;
+      for(int b = 0; b < 4; b++) {
+         const int s = bin_bit(b);
+         if(s < 4) continue;
+         while(low[next]) next++;
+         m.src[m.n] = s;
+         m.dst[m.n] = next++;
+         m.n++;
+      }
+      return m;
+   }
+   static constexpr Moves MV = moves();
+   static constexpr bool additive = true;
+   static_assert(PL::T >= 16, "a quarter-wavefront within one transform");
+
+   __device__ __forceinline__ static int phys(int i)
+   {
+      int x = 0;
+#pragma unroll
+      for(int j = 0; j < MV.n; j++) x |= ((i >> MV.src[j]) & 1) << MV.dst[j];
+      return i ^ x;
+   }
+   static constexpr int cphys(int off) { return off; }     // off is a multiple of T
+};
+
 // LDS slot of logical position base + off, where off is a multiple of V (so
 // the padded layout stays additive)
 template<class LD>
@@ -391,18 +446,21 @@ __device__ __forceinline__ float2* lds_slot(float2* A, int base_phys, int base, 
 // r[k] = slot L*V + k (forward DIF output)  ->  r[q] = bin L + q*T, so the
 // store that follows is the coalesced natural-order store of the conv kernels.
 // The first barrier orders the last DIF pass's gather before these writes.
+// The exchange has its own layout (UnscrambleLds); the XOR layout, chosen at
+// run time for comparison, keeps its own map.
 template<class PL, class LD, int LANES>
 __device__ __forceinline__ void digit_to_natural(float2 (&r)[PL::V], float2* A, int L)
 {
+   using UL = std::conditional_t<LD::additive, UnscrambleLds<PL>, LD>;
    constexpr int V = PL::V, T = PL::T;
    const int f = lane_bin<PL>(L);
-   const int fp = LD::phys(f), lp = LD::phys(L);
+   const int fp = UL::phys(f), lp = UL::phys(L);
    pass_barrier<LANES>();
 #pragma unroll
-   for(int k = 0; k < V; k++) *lds_slot<LD>(A, fp, f, k * T) = r[k];
+   for(int k = 0; k < V; k++) *lds_slot<UL>(A, fp, f, k * T) = r[k];
    pass_barrier<LANES>();
 #pragma unroll
-   for(int q = 0; q < V; q++) r[q] = *lds_slot<LD>(A, lp, L, q * T);
+   for(int q = 0; q < V; q++) r[q] = *lds_slot<UL>(A, lp, L, q * T);
 }
 
 // r[q] = bin L + q*T (natural-order load)  ->  r[k] = slot L*V + k, what the
@@ -411,14 +469,15 @@ __device__ __forceinline__ void digit_to_natural(float2 (&r)[PL::V], float2* A, 
 template<class PL, class LD, int LANES, bool WAR>
 __device__ __forceinline__ void natural_to_digit(float2 (&r)[PL::V], float2* A, int L)
 {
+   using UL = std::conditional_t<LD::additive, UnscrambleLds<PL>, LD>;
    constexpr int V = PL::V, T = PL::T;
    const int f = lane_bin<PL>(L);
-   const int fp = LD::phys(f), lp = LD::phys(L);
+   const int fp = UL::phys(f), lp = UL::phys(L);
 #pragma unroll
-   for(int q = 0; q < V; q++) *lds_slot<LD>(A, lp, L, q * T) = r[q];
+   for(int q = 0; q < V; q++) *lds_slot<UL>(A, lp, L, q * T) = r[q];
    pass_barrier<LANES>();
 #pragma unroll
-   for(int k = 0; k < V; k++) r[k] = *lds_slot<LD>(A, fp, f, k * T);
+   for(int k = 0; k < V; k++) r[k] = *lds_slot<UL>(A, fp, f, k * T);
    if constexpr(WAR) pass_barrier<LANES>();
 }
 

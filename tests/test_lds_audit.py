@@ -1,10 +1,14 @@
 """CPU audit of the LDS layouts used by the fused kernels (fufft_plan.hpp).
 
 For every plan (V, N) and every pass, it enumerates the slot each lane touches
-for each tap and checks, under the gfx950 bank model measured with
-SQ_LDS_BANK_CONFLICT (64 banks x 4 B; an 8-byte access is serviced 32 lanes
-at a time, so lanes of an aligned half-wave conflict when their slots agree
-modulo 32):
+for each tap and checks it under the gfx950 bank model measured with
+SQ_LDS_BANK_CONFLICT (fufft_amd/lds_probe.py, profiles/lds_bank_model.md):
+ds_read_b64 is serviced 32 lanes at a time, so lanes of an aligned
+half-wavefront conflict when their slots agree modulo 32; each 8-byte access
+of ds_write_b64 and of the paired forms the exchanges use (ds_read2_b64,
+ds_write2_b64, ds_read2st64_b64) is serviced 16 lanes at a time, so lanes of
+an aligned quarter-wavefront conflict when their slots agree modulo 16.
+Checked:
 
   - the layout is a bijection onto [0, size(N));
   - the padded layout is additive for every pass, phys(base + k*M) =
@@ -15,11 +19,19 @@ modulo 32):
   - the reference's own swizzle, derived for 32 banks / 16-lane phases, is not
     conflict free under this model (why the layout was re-derived);
   - the per-exchange layouts the kernels use by default are bijections within
-    the slot, additive, conflict free, and free of cross-wavefront races.
+    the slot, additive, conflict free, and free of cross-wavefront races;
+  - the model reproduces every probe measurement and the kernel counters on
+    record.
 """
 import itertools
+import re
+from pathlib import Path
 
 import pytest
+
+from fufft_amd.lds_probe import PATTERNS, FORMS, conflict_cycles
+
+ROOT = Path(__file__).resolve().parent.parent
 
 
 def ilog2(x):
@@ -62,14 +74,20 @@ def lane_sets(n, v):
             yield (R, M, g, k), [tap_pos(L, g, k, R, M, T) for L in range(T)]
 
 
-def degree(slots, lanes=32):
+def degree(slots, lanes=32, mod=32):
+    """worst number of distinct slots sharing a residue within a lane group:
+    lanes=32, mod=32 for ds_read_b64; lanes=16, mod=16 for the paired forms"""
     worst = 1
     for h in range(0, len(slots), lanes):
         banks = {}
         for s in slots[h:h + lanes]:
-            banks.setdefault(s % 32, set()).add(s)
+            banks.setdefault(s % mod, set()).add(s)
         worst = max(worst, max(len(x) for x in banks.values()))
     return worst
+
+
+def quarter(slots):
+    return degree(slots, 16, 16)
 
 
 PLANS = [(16, n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + [(8, n) for n in (512, 1024, 2048, 4096)]
@@ -101,6 +119,8 @@ def test_conflict_degree(v, n):
             pos = [p + r * stride for r in range(reps) for p in pos]
         assert degree([phys_xor(p, v) for p in pos]) == 1, ("xor", key)
         assert degree([phys_pad(p, v) for p in pos]) <= 2, ("pad", key)
+        assert quarter([phys_xor(p, v) for p in pos]) == 1, ("xor", key)
+        assert quarter([phys_pad(p, v) for p in pos]) <= 2, ("pad", key)
 
 
 def test_reference_swizzle_conflicts_on_gfx950():
@@ -114,24 +134,49 @@ def test_reference_swizzle_conflicts_on_gfx950():
 
 
 # column kernels (conv2d.hip): C columns side by side, thread = (L, col) with
-# the column fastest, per-column slot skewed by 32 / C float2
+# the column fastest, per-column slot skewed by 16 / C float2.  Their
+# exchanges are paired ds_read2_b64 / ds_write2_b64, so the quarter-wavefront
+# rule applies.
 COLS = [(256, 8, 16), (512, 8, 16), (1024, 16, 16), (2048, 16, 8)]
 
 
-@pytest.mark.parametrize("h,v,c", COLS)
-def test_column_tiles_conflict_free(h, v, c):
+def column_cost(h, v, c, slotc):
+    """conflict cycles per wavefront of one pass over every tap, paired forms"""
     T = h // v
-    slotc = h + h // v + 32 // c
+    total = 0
     for (R, M) in plan(h, v):
         for g, k in itertools.product(range(v // R), range(R)):
             addrs = [(tid % c) * slotc + phys_pad(tap_pos(tid // c, g, k, R, M, T), v)
                      for tid in range(c * T)]
             for w0 in range(0, len(addrs), 64):
-                assert degree(addrs[w0:w0 + 64]) == 1, (h, v, c, R, M, g, k)
-    # without the skew the C columns of a half-wavefront share banks
-    addrs = [(tid % c) * (h + h // v) + phys_pad(tap_pos(tid // c, 0, 0, *plan(h, v)[0], T), v)
-             for tid in range(64)]
-    assert degree(addrs) > 1
+                total += conflict_cycles(addrs[w0:w0 + 64], "write_b64")
+    return total / (c * T // 64)
+
+
+@pytest.mark.parametrize("h,v,c", COLS)
+def test_column_tiles_conflict_free(h, v, c):
+    T = h // v
+    slotc = h + h // v + 16 // c
+    for (R, M) in plan(h, v):
+        for g, k in itertools.product(range(v // R), range(R)):
+            addrs = [(tid % c) * slotc + phys_pad(tap_pos(tid // c, g, k, R, M, T), v)
+                     for tid in range(c * T)]
+            for w0 in range(0, len(addrs), 64):
+                assert quarter(addrs[w0:w0 + 64]) == 1, (h, v, c, R, M, g, k)
+    # the earlier skew of 32 / C is conflict-free only for ds_read_b64
+    assert column_cost(h, v, c, h + h // v + 32 // c) > 0
+
+
+def test_column_kernel_counter_matches_the_model():
+    """rocprofv3 measured 256 conflict cycles per wavefront in the 512-row
+    column conv (and 128 in the column apply, which runs half the passes)
+    with the 32 / C skew, and 0 with 16 / C (profiles/lds_bank_model.md).
+    The conv kernel scatters and gathers every pass's taps in both
+    directions: 4 tap sets per direction for 3 passes."""
+    h, v, c = 512, 8, 16
+    per_pass_set = column_cost(h, v, c, h + h // v + 32 // c) / len(plan(h, v))
+    assert per_pass_set * 8 == 256
+    assert column_cost(h, v, c, h + h // v + 16 // c) == 0
 
 
 # exchange_in_wave (fufft_plan.hpp): the exchange between pass p and p + 1 may
@@ -203,22 +248,52 @@ def mixedrev(s, n, v):
 UNSCRAMBLE = PLANS + [(8, 8192)]
 
 
+def unscramble_moves(n, v):
+    """UnscrambleLds (fufft_plan.hpp): (source bit, target bit) pairs.  Lane
+    bit b lands on bin bit bin_bit(b); the high ones are copied onto the bits
+    0-3 the bin does not already vary, in order."""
+    pl = plan(n, v)
+
+    def bin_bit(b):
+        w = 0
+        for (R, M) in pl[:-1]:
+            d, r = ilog2(M // v), ilog2(R)
+            if d <= b < d + r:
+                return w + b - d
+            w += r
+        return -1
+    bits = [bin_bit(b) for b in range(4)]
+    free = [t for t in range(4) if t not in bits]
+    return [(s, free.pop(0)) for s in bits if s >= 4]
+
+
+def phys_unscramble(i, moves):
+    x = 0
+    for s, d in moves:
+        x |= ((i >> s) & 1) << d
+    return i ^ x
+
+
 @pytest.mark.parametrize("v,n", UNSCRAMBLE)
 def test_unscramble_targets_and_conflicts(v, n):
     T = n // v
+    mv = unscramble_moves(n, v)
+    ph = [phys_unscramble(i, mv) for i in range(n)]
+    assert sorted(ph) == list(range(n))                       # bijection within the slot
     for L in range(T):
         f = lane_bin(L, n, v)
         for k in range(v):
             assert f + k * T == mixedrev(L * v + k, n, v)
-            assert phys_pad(f + k * T, v) == phys_pad(f, v) + phys_pad(k * T, v)
-    worst = 1
+            assert phys_unscramble(f + k * T, mv) == phys_unscramble(f, mv) + k * T
+            assert phys_unscramble(L + k * T, mv) == phys_unscramble(L, mv) + k * T
+    # both sides conflict-free for the paired forms (quarter-wavefront rule),
+    # where the padded layout was not (128 cycles per wavefront measured for
+    # the radix-8 N = 4096 C2C, test_model_reproduces_kernel_counters)
+    reps = max(1, 64 // T)
     for k in range(v):
-        pos = [lane_bin(L, n, v) + k * T for L in range(T)]
-        if len(pos) < 32:
-            pos = [p + r * n for r in range(32 // len(pos)) for p in pos]
-        worst = max(worst, degree([phys_pad(p, v) for p in pos]))
-    # measured bound of the scattered side; the natural side is pass 0's pattern
-    assert worst <= (2 if n <= 4096 and (v, n) != (8, 1024) else 4), worst
+        for side in ([lane_bin(L, n, v) + k * T for L in range(T)], [L + k * T for L in range(T)]):
+            pos = [t * (n + n // v) + phys_unscramble(p, mv) for t in range(reps) for p in side]
+            assert quarter(pos) == 1, (k, side[:4])
 
 
 # ---- per-exchange layouts (XchgLds, fufft_plan.hpp) -------------------------------------
@@ -269,7 +344,7 @@ def xchg_problems(n, v, rule, wl=64):
                 for wl_i in range(64):
                     t, L = divmod(wl_i, T) if T < 64 else (0, wl_i)
                     lanes.append(t * (n + n // v) + xchg_phys(tap_pos(L, g, k, R, M, T), *lay[e]))
-                if degree(lanes) > 1:
+                if degree(lanes) > 1 or quarter(lanes) > 1:
                     out.append(("conflict", e, p, g, k))
                 for L in range(T):
                     base = tap_pos(L, g, 0, R, M, T)
@@ -306,3 +381,48 @@ def test_exchange_layouts_audit_catches_the_race(v, n):
     wrong results on the GPU at full batch (radix 8, N = 8192)."""
     kinds = {x[0] for x in xchg_problems(n, v, xchg_naive)}
     assert kinds == {"clobbers another wavefront's input"}
+
+
+# ---- the model against its measurements --------------------------------------------------
+def test_bank_model_reproduces_the_probe():
+    """Every row of the committed probe summary: measured == model."""
+    text = (ROOT / "profiles" / "lds_bank_model.md").read_text()
+    rows = 0
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) != 1 + len(FORMS) or cells[0] not in PATTERNS:
+            continue
+        rows += 1
+        for form, cell in zip(FORMS, cells[1:]):
+            measured, model = (float(x) for x in cell.split("/"))
+            assert model == conflict_cycles(PATTERNS[cells[0]], form), (cells[0], form)
+            assert measured == model, (cells[0], form, measured, model)
+    assert rows == len(PATTERNS)
+
+
+def test_model_reproduces_kernel_counters():
+    """Counters on record: radix-8 N = 4096 conv with the single padded
+    layout, 192 cycles per wavefront; natural-order C2C forward at N = 4096
+    (per-exchange layouts for the DIF, padded digit-to-natural exchange), 128.
+    Every exchange instruction of both kernels is a paired form."""
+    n, v = 4096, 8
+    T, pl = n // v, plan(n, v)
+
+    def tapset(R, M, g, k, phys):
+        return [phys(tap_pos(L, g, k, R, M, T)) for L in range(T)]
+
+    def cost(slots):
+        return sum(conflict_cycles(slots[w:w + 64], "write_b64") for w in range(0, len(slots), 64)) / (T // 64)
+
+    pad = lambda i: phys_pad(i, v)
+    conv = 0
+    for e in range(len(pl) - 1):
+        for p in (e, e + 1):
+            R, M = pl[p]
+            conv += sum(cost(tapset(R, M, g, k, pad)) for g in range(v // R) for k in range(R))
+    assert 2 * conv == 192                    # forward and inverse
+    # C2C: the DIF exchanges cost nothing (per-exchange layouts); the unscramble
+    # scatters slot L*V + k to bin lane_bin(L) + k*T and gathers bins L + q*T
+    scat = sum(cost([pad(lane_bin(L, n, v) + k * T) for L in range(T)]) for k in range(v))
+    gath = sum(cost([pad(L + q * T) for L in range(T)]) for q in range(v))
+    assert scat + gath == 128
