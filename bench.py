@@ -19,7 +19,8 @@ bytes per point for fp32 (bench_fufft.cu:314-317), over the average launch
 duration; with a shared filter one of those passes is served from cache, so
 the physical minimum is 16 B/pt and `physical` reports that figure too.  For
 int16-BFP the model is 3 x 4 = 12 B/pt (physical 8 B/pt + 2 B per 64-point
-block of exponents).  roofline.traffic is the HBM bytes per launch measured by
+block of exponents); at the headline N, "bfp" also reports the same conv with
+one exponent per signal (block = N, the reference's per-transform scale).  roofline.traffic is the HBM bytes per launch measured by
 rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE) for this same command, read from the
 committed summary profiles/conv_f32_n4096.md when present.
 
@@ -305,9 +306,10 @@ def bench_2d(torch, ff, dev, pts, steps, warmup, stream, seed):
     }
 
 
-def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed):
+def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64):
     """int16-BFP fused conv: Gaussian x 10^u per signal (u ~ U[-3, 3]), quantised on
-    the host by the library codec, one shared fp32 filter spectrum."""
+    the host by the library codec (one exponent per `block` points), one shared
+    fp32 filter spectrum."""
     batch = pts // n
     rng = np.random.default_rng(seed)
     x = np.empty((batch, n), dtype=np.complex64)
@@ -319,21 +321,21 @@ def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed):
         s = (10.0 ** rng.uniform(-3, 3, (b1 - b0, 1))).astype(np.float32)
         x[b0:b1].real = re * s
         x[b0:b1].imag = im * s
-    q, e = ff.bfp_quantize(x)
+    q, e = ff.bfp_quantize(x, block=block)
     taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
     filt = torch.from_numpy(ff.plan_filter(taps, n, variant="auto", kind=ff.FILTER_TAPS)).to(dev)
     dq, de = torch.from_numpy(q).to(dev), torch.from_numpy(e).to(dev)
     qo, eo = torch.empty_like(dq), torch.empty_like(de)
 
     def step():
-        ff.conv_bfp16(dq, de, filt, qo, eo, n=n, batch=batch, stream=stream)
+        ff.conv_bfp16(dq, de, filt, qo, eo, n=n, batch=batch, stream=stream, block=block)
 
     step()
     torch.cuda.synchronize()
     idx = np.linspace(0, batch - 1, 16).astype(np.int64)
     qs = qo.view(batch, 2 * n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
-    es = eo.view(batch, n // ff.BFP_BLOCK)[torch.from_numpy(idx).to(dev)].cpu().numpy()
-    got = ff.bfp_dequantize(qs, es).reshape(16, n)
+    es = eo.view(batch, n // block)[torch.from_numpy(idx).to(dev)].cpu().numpy()
+    got = ff.bfp_dequantize(qs, es, block=block).reshape(16, n)
     want = np.fft.ifft(np.fft.fft(x[idx].astype(np.complex128), axis=1)
                        * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
     per_sig = np.linalg.norm(got - want, axis=1) / np.linalg.norm(want, axis=1)
@@ -482,6 +484,13 @@ def main():
                            "variant": ff.resolve_variant(s, "auto")}
             if s == n:
                 bfp[str(s)]["speedup_vs_fp32"] = round(g / gpts, 3)
+                # one exponent per signal: the reference's per-transform scale
+                a, r, worst = bench_bfp(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 99 + s, block=s)
+                if not r <= 1e-4:
+                    print(json.dumps({"error": f"BFP (block = N) accuracy check failed at N={s}: rel L2 {r:.3e}"}))
+                    sys.exit(1)
+                bfp[str(s)]["block_n"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                                          "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst}
         line["bfp"] = bfp
 
     large = {}

@@ -70,9 +70,9 @@ def _load() -> C.CDLL:
         "fufft_apply_f32": ([vp, i64, vp, i64, vp, i64, i64, i32, i32, i32, vp], i32),
         "fufft_conv_r2_f32": ([vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, vp], i32),
         "fufft_bfp_exponent": ([C.c_float], i32),
-        "fufft_bfp_quantize": ([vp, i64, vp, vp], i32),
-        "fufft_bfp_dequantize": ([vp, vp, i64, vp], i32),
-        "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, i32, vp], i32),
+        "fufft_bfp_quantize": ([vp, i64, i64, vp, vp], i32),
+        "fufft_bfp_dequantize": ([vp, vp, i64, i64, vp], i32),
+        "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, i32, i32, vp], i32),
         "fufft_large_plan": ([i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
         "fufft_large_digit_order": ([i64, C.POINTER(C.c_int32)], i32),
         "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
@@ -259,10 +259,12 @@ def conv_r2(x, y, filt, u, v, n: int, batch: int, filt_stride: int = 0, variant:
 
 
 def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int = 0,
-               mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None) -> None:
+               mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None,
+               block: int = BFP_BLOCK) -> None:
+    """int16-BFP fused conv; one exponent per `block` points (64 .. n, a power of two)."""
     check(lib.fufft_conv_bfp16(_ptr(qin), _ptr(ein), _ptr(filt), filt_stride, _ptr(qout),
-                               _ptr(eout), n, batch, MID[mid], VARIANT[variant], LAYOUT[layout],
-                               _stream(stream)), "fufft_conv_bfp16")
+                               _ptr(eout), n, batch, block, MID[mid], VARIANT[variant],
+                               LAYOUT[layout], _stream(stream)), "fufft_conv_bfp16")
 
 
 def c2c(inp, out, n: int, batch: int, direction: int = FORWARD, variant: str = "auto",
@@ -382,19 +384,19 @@ def bfp_exponent(absmax: float) -> int:
     return lib.fufft_bfp_exponent(absmax)
 
 
-def bfp_quantize(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+def bfp_quantize(x: np.ndarray, block: int = BFP_BLOCK) -> tuple[np.ndarray, np.ndarray]:
     src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
     q = np.empty(2 * src.size, dtype=np.int16)
-    e = np.empty(src.size // BFP_BLOCK, dtype=np.int8)
-    check(lib.fufft_bfp_quantize(src.ctypes.data, src.size, q.ctypes.data, e.ctypes.data),
+    e = np.empty(max(src.size // block, 1), dtype=np.int8)
+    check(lib.fufft_bfp_quantize(src.ctypes.data, src.size, block, q.ctypes.data, e.ctypes.data),
           "fufft_bfp_quantize")
-    return q, e
+    return q, e[: src.size // block]
 
 
-def bfp_dequantize(q: np.ndarray, e: np.ndarray) -> np.ndarray:
+def bfp_dequantize(q: np.ndarray, e: np.ndarray, block: int = BFP_BLOCK) -> np.ndarray:
     npts = q.size // 2
     x = np.empty(npts, dtype=np.complex64)
     check(lib.fufft_bfp_dequantize(np.ascontiguousarray(q).ctypes.data,
-                                   np.ascontiguousarray(e).ctypes.data, npts, x.ctypes.data),
+                                   np.ascontiguousarray(e).ctypes.data, npts, block, x.ctypes.data),
           "fufft_bfp_dequantize")
     return x

@@ -8,14 +8,19 @@
 // fp32 and the exponent rule is
 //    e = -128 for an all-zero (or subnormal) block, else the smallest integer
 //        with absmax <= 32767 * 2^e, clamped at -128;   q = rint(x * 2^-e).
+// A block is B consecutive points of a signal, B a power of two from 64 to N
+// (B = N: one exponent per signal, the reference's per-transform scale).
 //
 // Mapping: a transform has T = N/V >= 64 lanes, and register q of a wavefront
 // holds the 64 consecutive points 64*w + q*T .. (w = wavefront index within
-// the transform), i.e. exactly one block.  So input exponents are uniform per
-// (wavefront, register), and the V output blocks' abs-maxima come from one
-// transposed cross-lane reduction of the wavefront's V registers -- no LDS pass
-// and no workgroup barrier for the scale, unlike the reference's shared-memory
-// atomicMax rendezvous (fufft.cuh:1674-1692).
+// the transform), all inside one block.  So input exponents are uniform per
+// (wavefront, register), and the V abs-maxima of a wavefront's registers come
+// from one transposed cross-lane reduction.  With B = 64 each of them is a
+// block's maximum: no LDS pass and no workgroup barrier for the scale, unlike
+// the reference's shared-memory atomicMax rendezvous (fufft.cuh:1674-1692).
+// With B > 64 a block spans several (wavefront, register) pairs, and their
+// maxima meet in one LDS atomic max per pair (the reference's rendezvous,
+// on V values per wavefront instead of every element).
 #include "fufft_device.hpp"
 #include "fufft_plan.hpp"
 #include "fufft_internal.hpp"
@@ -100,7 +105,10 @@ __device__ __forceinline__ uint32_t block_maxima(uint32_t (&m)[V], uint32_t lane
    return swap_max32(swap_max16(x));
 }
 
-template<int N, int V, int LAYOUT, int MID>
+// bmax words per transform for blocks of 128 points or more
+constexpr int bfp_bmax_words(int n) { return n / 128; }
+
+template<int N, int V, int LAYOUT, int MID, bool BIG>
 __global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V))
 bfp_kernel(const BfpParams p)
 {
@@ -109,8 +117,7 @@ bfp_kernel(const BfpParams p)
    constexpr int T     = PL::T;
    constexpr int CPB   = bfp_cpb(T);
    constexpr int SLOT  = LD::size(N);
-   constexpr int NB    = N / 64;                  // exponent blocks per transform
-   static_assert(T >= 64, "a wavefront register must cover one 64-point block");
+   static_assert(T >= 64, "a wavefront register must lie inside one block");
 
    extern __shared__ float2 lds[];
    const int slot = threadIdx.x / T;
@@ -120,24 +127,49 @@ bfp_kernel(const BfpParams p)
    if(t >= p.ntrans) return;
    const uint32_t tu = (uint32_t)uniform((int)t);
    const int w = uniform(L >> 6);                 // wavefront within the transform
+   const int lb = BIG ? p.log_block : 6;          // log2 of the block length
+   const int nbk = N >> lb;                       // exponent blocks per transform
+   // block of (wavefront w, register q): its first point is 64*w + q*T
+   auto block_of = [&](int q) { return BIG ? (64 * w + q * T) >> lb : w + q * (T / 64); };
 
    float2* A = lds + slot * SLOT;
+   // per-block abs-max bits (B > 64 only), after the exchange slots; zeroed
+   // here, ordered before the atomics by the exchanges' barriers (or, for a
+   // transform inside one wavefront, by program order)
+   uint32_t* bmax = reinterpret_cast<uint32_t*>(lds + CPB * SLOT) + slot * bfp_bmax_words(N);
+   if constexpr(BIG) {
+      if(L < nbk) bmax[L] = 0u;
+   }
    Twiddles<PL> tw;
    tw.load(p.tw, L);
 
-   // this wavefront's V input exponents, blocks w + q*T/64 of transform t: the
-   // address is uniform and nothing in the kernel has stored yet, so these are
-   // scalar loads (dwords of the transform's NB exponent bytes, 4-byte aligned
-   // by the entry point's contract) and the bytes are picked apart in SALU
-   const uint32_t* ew = reinterpret_cast<const uint32_t*>(p.ein) + (size_t)tu * (NB / 4);
+   // this wavefront's V input exponents.  B = 64: the address is uniform and
+   // nothing in the kernel has stored yet, so these are scalar loads (aligned
+   // dwords of the transform's N/64 exponent bytes, a multiple of 4; the array
+   // is 4-byte aligned by the entry point's contract) and the bytes are picked
+   // apart in SALU.  B > 64: a transform's exponents need not fill whole
+   // dwords, so lane l reads register l % V's byte through a bounds-checked
+   // buffer load and the registers take it by readlane.
+   const size_t ebase = (size_t)tu * nbk;
+   const uint32_t* ew = reinterpret_cast<const uint32_t*>(p.ein + (BIG ? 0 : ebase));
+   int ein_lane = 0;
+   if constexpr(BIG) {
+      const Buf eb(p.ein + ebase, (uint32_t)nbk);
+      ein_lane = eb.ldi8((uint32_t)block_of(lane % V), 0);
+   }
 
    const Buf qb(static_cast<const char*>(p.qin) + (size_t)tu * N * 4, N * 4);
    float2 r[V];
 #pragma unroll
    for(int q = 0; q < V; q++) {
       const uint32_t word = qb.ldu((uint32_t)L * 4u, q * T * 4);
-      const int byte = w + q * (T / 64);
-      const int e = (int)(int8_t)(ew[byte >> 2] >> (8 * (byte & 3)));
+      int e;
+      if constexpr(BIG) {
+         e = __builtin_amdgcn_readlane(ein_lane, q);
+      } else {
+         const int byte = block_of(q);
+         e = (int)(int8_t)(ew[byte >> 2] >> (8 * (byte & 3)));
+      }
       r[q] = make_float2(__builtin_amdgcn_ldexpf((float)(int)(int16_t)(word & 0xffffu), e),
                          __builtin_amdgcn_ldexpf((float)((int)word >> 16), e));
    }
@@ -156,7 +188,17 @@ bfp_kernel(const BfpParams p)
 #pragma unroll
    for(int q = 0; q < V; q++)
       m[q] = __builtin_bit_cast(uint32_t, __builtin_fmaxf(__builtin_fabsf(r[q].x), __builtin_fabsf(r[q].y)));
-   const int e_lane = bfp_exponent_bits(block_maxima<V>(m, (uint32_t)lane));   // block lane % V
+   // lane l: the abs-max of register l % V over the wavefront
+   const uint32_t wmax = block_maxima<V>(m, (uint32_t)lane);
+   int e_lane;                                    // exponent of register lane % V's block
+   if constexpr(BIG) {
+      if(lane < V) atomicMax(&bmax[block_of(lane)], wmax);
+      if constexpr(T > 64) __syncthreads();       // CPB == 1: every wavefront is this transform's
+      else                 pass_barrier<64>();
+      e_lane = bfp_exponent_bits(bmax[block_of(lane % V)]);
+   } else {
+      e_lane = bfp_exponent_bits(wmax);
+   }
    const Buf ob(static_cast<char*>(p.qout) + (size_t)tu * N * 4, N * 4);
    int eq[V];
    int emin = 127;
@@ -191,9 +233,10 @@ bfp_kernel(const BfpParams p)
          store(q, __builtin_amdgcn_ldexpf(r[q].x, -eq[q]) + 12582912.0f,
                __builtin_amdgcn_ldexpf(r[q].y, -eq[q]) + 12582912.0f);
    }
-   if(lane < V) {
-      const Buf xb(p.eout + (size_t)tu * NB, NB);
-      __builtin_amdgcn_raw_buffer_store_b8((unsigned char)e_lane, xb.r, (uint32_t)(w + lane * (T / 64)), 0, 0);
+   // one store per block, by the lane of its first (wavefront, register) pair
+   if(lane < V && (!BIG || ((64 * w + lane * T) & ((1 << lb) - 1)) == 0)) {
+      const Buf xb(p.eout + ebase, nbk);
+      __builtin_amdgcn_raw_buffer_store_b8((unsigned char)e_lane, xb.r, (uint32_t)block_of(lane), 0, 0);
    }
 }
 
@@ -201,11 +244,15 @@ template<int N, int V, int LAYOUT, int MID>
 static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
 {
    constexpr int T = N / V, CPB = bfp_cpb(T);
-   const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
-   const void* k = reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID>);
+   const bool big = p.log_block > 6;
+   if(p.log_block < 6 || (1 << p.log_block) > N) return hipErrorInvalidValue;
+   const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2)
+                    + (big ? (size_t)CPB * bfp_bmax_words(N) * 4 : 0);
+   const void* k = big ? reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID, true>)
+                       : reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID, false>);
    if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
-   static std::atomic<uint64_t> lds_ok{0};
-   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
+   static std::atomic<uint64_t> lds_ok[2]{};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok[big]); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
    BfpParams arg = p;
    void* argv[] = { &arg };

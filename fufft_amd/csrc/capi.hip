@@ -590,7 +590,8 @@ int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t c
 
 int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
                      int64_t filt_stride, void* qout, int8_t* eout, int64_t n,
-                     int64_t batch, int mid, int variant, int layout, void* stream)
+                     int64_t batch, int64_t block, int mid, int variant, int layout,
+                     void* stream)
 {
    const int vv = resolve_variant(n, variant);
    const int v = values_per_lane(vv);
@@ -598,6 +599,7 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
    if(layout != FUFFT_LAYOUT_DR && layout != FUFFT_LAYOUT_LANE) return FUFFT_ERR_INVALID;
    if(batch < 0 || batch > 0xffffffffll) return FUFFT_ERR_INVALID;
    if(!pow2(n) || n > 16384 || !bfp_supported((int)n, v)) return FUFFT_ERR_UNSUPPORTED;
+   if(!pow2(block) || block < FUFFT_BFP_BLOCK || block > n) return FUFFT_ERR_INVALID;
    if(!qin || !ein || !qout || !eout || (mid != FUFFT_MID_NONE && !filt)) return FUFFT_ERR_INVALID;
    // exponents are read as aligned dwords through the scalar cache
    if(!aligned4(qin) || !aligned4(qout) || !aligned4(ein) || !aligned4(eout) || (filt && !aligned16(filt)))
@@ -609,6 +611,8 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
    if(batch == 0) return FUFFT_OK;
    p.qin = qin; p.ein = ein; p.filt = filt; p.qout = qout; p.eout = eout;
    p.ntrans = (uint32_t)batch; p.mid = mid; p.fl = layout;
+   p.log_block = 0;
+   while(((int64_t)1 << p.log_block) < block) p.log_block++;
    hipStream_t s = static_cast<hipStream_t>(stream);
    // per-signal filters beyond 4 GiB: chunks keep the 32-bit filter offsets in range
    const uint64_t fbytes = (uint64_t)n * 8;
@@ -620,8 +624,8 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
       q.fcount = q.ntrans;
       q.qin  = static_cast<const char*>(p.qin) + (size_t)t0 * n * 4;
       q.qout = static_cast<char*>(p.qout) + (size_t)t0 * n * 4;
-      q.ein  = p.ein + (size_t)t0 * (n / FUFFT_BFP_BLOCK);
-      q.eout = p.eout + (size_t)t0 * (n / FUFFT_BFP_BLOCK);
+      q.ein  = p.ein + (size_t)t0 * (n / block);
+      q.eout = p.eout + (size_t)t0 * (n / block);
       q.filt = static_cast<const char*>(p.filt) + (size_t)t0 * fbytes;
       const hipError_t e = launch_bfp((int)n, v, lds_layout(), q, s);
       if(e != hipSuccess) return status_of(e);
@@ -644,27 +648,27 @@ int fufft_bfp_exponent(float absmax)
    return e < -128 ? -128 : e;
 }
 
-int fufft_bfp_quantize(const float* x, int64_t npts, int16_t* q, int8_t* e)
+int fufft_bfp_quantize(const float* x, int64_t npts, int64_t block, int16_t* q, int8_t* e)
 {
-   if(!x || !q || !e || npts < 0 || npts % FUFFT_BFP_BLOCK) return FUFFT_ERR_INVALID;
-   for(int64_t b = 0; b < npts / FUFFT_BFP_BLOCK; b++) {
-      const float* xb = x + 2 * b * FUFFT_BFP_BLOCK;
+   if(!x || !q || !e || npts < 0 || block < 1 || npts % block) return FUFFT_ERR_INVALID;
+   for(int64_t b = 0; b < npts / block; b++) {
+      const float* xb = x + 2 * b * block;
       float m = 0.0f;
-      for(int i = 0; i < 2 * FUFFT_BFP_BLOCK; i++) m = std::fmax(m, std::fabs(xb[i]));
+      for(int64_t i = 0; i < 2 * block; i++) m = std::fmax(m, std::fabs(xb[i]));
       const int ex = fufft_bfp_exponent(m);
       e[b] = (int8_t)ex;
-      for(int i = 0; i < 2 * FUFFT_BFP_BLOCK; i++)
-         q[2 * b * FUFFT_BFP_BLOCK + i] = (int16_t)std::rint(std::ldexp(xb[i], -ex));
+      for(int64_t i = 0; i < 2 * block; i++)
+         q[2 * b * block + i] = (int16_t)std::rint(std::ldexp(xb[i], -ex));
    }
    return FUFFT_OK;
 }
 
-int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float* x)
+int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, int64_t block, float* x)
 {
-   if(!x || !q || !e || npts < 0 || npts % FUFFT_BFP_BLOCK) return FUFFT_ERR_INVALID;
-   for(int64_t b = 0; b < npts / FUFFT_BFP_BLOCK; b++)
-      for(int i = 0; i < 2 * FUFFT_BFP_BLOCK; i++)
-         x[2 * b * FUFFT_BFP_BLOCK + i] = std::ldexp((float)q[2 * b * FUFFT_BFP_BLOCK + i], e[b]);
+   if(!x || !q || !e || npts < 0 || block < 1 || npts % block) return FUFFT_ERR_INVALID;
+   for(int64_t b = 0; b < npts / block; b++)
+      for(int64_t i = 0; i < 2 * block; i++)
+         x[2 * b * block + i] = std::ldexp((float)q[2 * b * block + i], e[b]);
    return FUFFT_OK;
 }
 

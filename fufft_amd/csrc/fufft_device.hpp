@@ -273,6 +273,10 @@ struct Buf {
    {
       return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
    }
+   __device__ __forceinline__ int ldi8(uint32_t voff, uint32_t soff) const
+   {
+      return (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
+   }
    __device__ __forceinline__ void st1(float v, uint32_t voff, uint32_t soff) const
    {
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);

@@ -86,7 +86,7 @@ hipError_t launch_gather(const GatherParams& p, hipStream_t s);
 // ---- int16 block floating point (bfp.hip) ---------------------------------------------
 struct BfpParams {
    const void*   qin;      // int16 pairs
-   const int8_t* ein;      // one exponent per block
+   const int8_t* ein;      // one exponent per block of 2^log_block points
    const void*   filt;     // fp32 filter
    void*         qout;
    int8_t*       eout;
@@ -95,6 +95,7 @@ struct BfpParams {
    uint32_t      fcount;
    int32_t       mid;
    int32_t       fl;
+   int32_t       log_block;   // 6 .. log2(n)
 };
 
 bool       bfp_supported(int n, int v);

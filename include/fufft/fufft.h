@@ -221,26 +221,32 @@ int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t
 
 /* ---- int16 block floating point ----------------------------------------------
  * A point is two int16 (re in the low halfword, im in the high halfword);
- * every block of FUFFT_BFP_BLOCK consecutive points of a signal shares one
- * int8 exponent e, value = q * 2^e.  Exponent rule: e = -128 for an all-zero
+ * every block of `block` consecutive points of a signal shares one int8
+ * exponent e, value = q * 2^e.  Exponent rule: e = -128 for an all-zero
  * (or subnormal) block, else the smallest e with absmax <= 32767 * 2^e,
  * clamped at -128; q = rint(x * 2^-e), so |q| <= 32767.
  * Replaces fufft_pipeline_v16_bfp (fufft.cuh:1614-1701), whose format is one
- * fp32 scale per transform and an int16 filter; here the filter is fp32. */
+ * fp32 scale per transform and an int16 filter; here the filter is fp32, and
+ * block = n gives one exponent per transform like the reference's scale.
+ * FUFFT_BFP_BLOCK is the smallest block (and the bench's). */
 #define FUFFT_BFP_BLOCK 64
 int fufft_bfp_exponent(float absmax);
-/* host reference codec (bfp_quant_host, bench_fufft.cu:105-117) */
-int fufft_bfp_quantize(const float* x, int64_t npts, int16_t* q, int8_t* e);
-int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, float* x);
+/* host reference codec (bfp_quant_host, bench_fufft.cu:105-117); npts a
+ * multiple of block */
+int fufft_bfp_quantize(const float* x, int64_t npts, int64_t block, int16_t* q, int8_t* e);
+int fufft_bfp_dequantize(const int16_t* q, const int8_t* e, int64_t npts, int64_t block,
+                         float* x);
 /* Fused conv on BFP data: dequantise on load, the fp32 pipeline of
  * fufft_conv_f32 (bit for bit), quantise on store with the rule above.
- * qin / qout: n*batch points (4 bytes each); ein / eout: n*batch/64 exponents;
+ * qin / qout: n*batch points (4 bytes each); ein / eout: n*batch/block
+ * exponents; block: a power of two, FUFFT_BFP_BLOCK <= block <= n;
  * filt: fp32 filter planned for the same variant.  Needs n/V >= 64 lanes:
  * FUFFT_R8 512..8192, FUFFT_V16 1024..16384.  qin == qout and ein == eout are
  * allowed.  qin, qout, ein and eout must be 4-byte aligned (FUFFT_ERR_ALIGN). */
 int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
                      int64_t filt_stride, void* qout, int8_t* eout, int64_t n,
-                     int64_t batch, int mid, int variant, int layout, void* stream);
+                     int64_t batch, int64_t block, int mid, int variant, int layout,
+                     void* stream);
 
 /* ---- four-step large N -------------------------------------------------------------
  * N = 16^lout * mid with mid a single-launch size: lout radix-16 DIF levels

@@ -82,14 +82,16 @@ inline int conv_r2(const float* x, const float* y, const void* filt, float* u, f
    return fufft_conv_r2_f32(x, y, filt, filt_stride, u, v, n, batch, (int)var, layout, stream);
 }
 
-// fufft_pipeline_v16_bfp<Mid> (fufft.cuh:1614-1701), int8 exponent per 64-point block
+// fufft_pipeline_v16_bfp<Mid> (fufft.cuh:1614-1701), int8 exponent per block of
+// `block` points (64 by default; block = n: one exponent per transform)
 template<class Mid = MidMultiply>
 inline int pipeline_bfp(const void* qin, const int8_t* ein, const void* filt, void* qout, int8_t* eout,
                         int64_t n, int64_t batch, void* stream = nullptr, int64_t filt_stride = 0,
-                        Variant v = Variant::Auto, int layout = FUFFT_LAYOUT_DR)
+                        Variant v = Variant::Auto, int layout = FUFFT_LAYOUT_DR,
+                        int64_t block = FUFFT_BFP_BLOCK)
 {
-   return fufft_conv_bfp16(qin, ein, filt, filt_stride, qout, eout, n, batch, Mid::id, (int)v, layout,
-                           stream);
+   return fufft_conv_bfp16(qin, ein, filt, filt_stride, qout, eout, n, batch, block, Mid::id, (int)v,
+                           layout, stream);
 }
 
 // fufft_c2c<N, LOG8N, CPB> (fufft.cuh:879-904): natural-order batched C2C; the

@@ -1,7 +1,7 @@
 """GPU parity of the int16 block-floating-point fused conv (fufft_conv_bfp16).
 
 Bar: int16 words and int8 exponents bit-identical to the oracle's BFP conv
-(same plan, same exponent rule), and rel L2 <= 1e-4 against the fp64
+(same plan, same exponent rule, same block length), and rel L2 <= 1e-4 against the fp64
 convolution of the UNquantised input (input quantisation included), on the
 BASELINE config-3 style input: per-signal N(0,1) scaled by 10^u, u ~ U[-3, 3].
 """
@@ -26,14 +26,15 @@ def config3_signals(rng, batch, n):
     return (crandn(rng, (batch, n)) * scale).astype(np.complex64)
 
 
-def run_bfp(dev, q, e, filt, n, batch, filt_stride=0, mid="mul", variant="auto", inplace=False):
+def run_bfp(dev, q, e, filt, n, batch, filt_stride=0, mid="mul", variant="auto", inplace=False,
+            block=64):
     import torch
     import fufft_amd as ff
     dq, de, df = to_dev(q, dev), to_dev(e, dev), to_dev(filt, dev)
     qo = dq if inplace else torch.empty_like(dq)
     eo = de if inplace else torch.empty_like(de)
     ff.conv_bfp16(dq, de, df, qo, eo, n=n, batch=batch, filt_stride=filt_stride, mid=mid,
-                  variant=variant)
+                  variant=variant, block=block)
     torch.cuda.synchronize()
     return qo.cpu().numpy(), eo.cpu().numpy()
 
@@ -64,6 +65,55 @@ def test_bfp_conv_matches_oracle_and_fp64(dev, n, variant, mid, rng):
     per_signal = np.sqrt(np.sum(np.abs(got - want) ** 2, axis=1) / np.sum(np.abs(want) ** 2, axis=1))
     print(f"   rel L2 {rel:.3e}, worst signal {per_signal.max():.3e}", flush=True)
     assert rel <= TOL_BFP
+
+
+# blocks longer than 64 points: one LDS atomic max per (wavefront, register)
+# pair; T = 64 plans (one wavefront per transform, 4 per workgroup) sync by a
+# wavefront fence, wider ones by the workgroup barrier.  block = n is one
+# exponent per signal, the reference's per-transform scale.
+BLOCKS = [(512, "auto", 128), (512, "auto", 512), (1024, "v16", 1024), (1024, "auto", 256),
+          (2048, "auto", 256), (4096, "auto", 128), (4096, "auto", 1024), (4096, "auto", 4096),
+          (4096, "v16", 2048), (8192, "auto", 8192), (16384, "v16", 16384)]
+
+
+@pytest.mark.parametrize("n,variant,block", BLOCKS)
+def test_bfp_block_lengths(dev, n, variant, block, rng):
+    import fufft_amd as ff
+    batch = max(5, 20480 // n) | 1                # odd: a partly filled last workgroup at T = 64
+    x = config3_signals(rng, batch, n)
+    x[1] = 0                                      # a zero signal: every block e = -128
+    x[2, : min(block, n // 2)] = 0                # a zero block (or part of one)
+    q, e = ff.bfp_quantize(x, block=block)
+    oq0, oe0 = O.bfp_quantize(x, block=block)
+    assert np.array_equal(q, oq0) and np.array_equal(e, oe0)
+    assert e.size == batch * n // block
+    taps = crandn(rng, n)
+    v = 8 if ff.resolve_variant(n, variant) == "r8" else 16
+    filt = ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS)
+    print(f"case bfp block={block} n={n} variant={variant} batch={batch}", flush=True)
+    qo, eo = run_bfp(dev, q, e, filt, n, batch, variant=variant, block=block, inplace=(block == n))
+    oq, oe = O.bfp_conv(q, e, filt, n, O.kernel_plan(n, v), block=block)
+    assert np.array_equal(eo, oe)
+    assert np.array_equal(qo, oq)
+    assert np.all(eo.reshape(batch, -1)[1] == -128) and np.all(qo.reshape(batch, -1)[1] == 0)
+    spec = np.fft.fft(taps.astype(np.complex128))
+    want = np.fft.ifft(np.fft.fft(x.astype(np.complex128), axis=1) * spec[None, :], axis=1)
+    got = O.bfp_dequantize(qo, eo, block=block).reshape(batch, n)
+    rel = np.sqrt(np.sum(np.abs(got - want) ** 2) / np.sum(np.abs(want) ** 2))
+    print(f"   rel L2 {rel:.3e}", flush=True)
+    assert rel <= TOL_BFP
+
+
+def test_bfp_block_rejects_bad_lengths(dev):
+    import fufft_amd as ff
+    import torch
+    n = 4096
+    d = torch.zeros(2 * n, dtype=torch.int16, device=dev)
+    de = torch.zeros(n // 64, dtype=torch.int8, device=dev)
+    f = torch.zeros(n, dtype=torch.complex64, device=dev)
+    for block in (32, 96, 2 * n):
+        with pytest.raises(RuntimeError):
+            ff.conv_bfp16(d, de, f, d, de, n=n, batch=1, block=block)
 
 
 def test_bfp_zero_blocks_and_in_place(dev, rng):
@@ -100,29 +150,32 @@ def test_bfp_per_signal_filter_and_none(dev, rng):
     assert O.rel_l2(got, n * O.bfp_dequantize(q, e)) < 1e-4
 
 
-@pytest.mark.parametrize("n,variant", [(512, "auto"), (1024, "auto"), (2048, "auto"), (4096, "auto"),
-                                       (8192, "auto"), (1024, "v16"), (4096, "v16"), (16384, "v16")])
-def test_bfp_full_batch_every_size(dev, n, variant):
+@pytest.mark.parametrize("n,variant,block", [(512, "auto", 64), (1024, "auto", 64), (2048, "auto", 64),
+                                             (4096, "auto", 64), (8192, "auto", 64), (1024, "v16", 64),
+                                             (4096, "v16", 64), (16384, "v16", 64), (512, "auto", 512),
+                                             (4096, "auto", 4096), (16384, "v16", 1024)])
+def test_bfp_full_batch_every_size(dev, n, variant, block):
     """2^27 points (full occupancy): 16 transforms spread over the batch,
     words and exponents bit-identical to the oracle."""
     import torch
     import fufft_amd as ff
     batch = (1 << 27) // n
+    nb = n // block
     gen = torch.Generator(device=dev)
-    gen.manual_seed(n)
+    gen.manual_seed(n + block)
     dq = torch.randint(-32767, 32768, (2 * batch * n,), dtype=torch.int16, device=dev, generator=gen)
-    de = torch.randint(-30, 10, (batch * n // ff.BFP_BLOCK,), dtype=torch.int8, device=dev, generator=gen)
+    de = torch.randint(-30, 10, (batch * nb,), dtype=torch.int8, device=dev, generator=gen)
     rng = np.random.default_rng(n)
     filt = ff.plan_filter(crandn(rng, n), n, variant=variant, kind=ff.FILTER_TAPS)
     qo, eo = torch.empty_like(dq), torch.empty_like(de)
-    print(f"case bfp full-batch n={n} variant={variant} batch={batch}", flush=True)
-    ff.conv_bfp16(dq, de, to_dev(filt, dev), qo, eo, n=n, batch=batch, variant=variant)
+    print(f"case bfp full-batch n={n} variant={variant} block={block} batch={batch}", flush=True)
+    ff.conv_bfp16(dq, de, to_dev(filt, dev), qo, eo, n=n, batch=batch, variant=variant, block=block)
     idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
     q_s = dq.view(batch, 2 * n)[idx].cpu().numpy()
-    e_s = de.view(batch, n // ff.BFP_BLOCK)[idx].cpu().numpy()
+    e_s = de.view(batch, nb)[idx].cpu().numpy()
     v = 8 if ff.resolve_variant(n, variant) == "r8" else 16
-    oq, oe = O.bfp_conv(q_s, e_s, filt, n, O.kernel_plan(n, v))
+    oq, oe = O.bfp_conv(q_s, e_s, filt, n, O.kernel_plan(n, v), block=block)
     torch.cuda.synchronize()
-    assert np.array_equal(eo.view(batch, n // ff.BFP_BLOCK)[idx].cpu().numpy(), oe.reshape(16, -1))
+    assert np.array_equal(eo.view(batch, nb)[idx].cpu().numpy(), oe.reshape(16, -1))
     assert np.array_equal(qo.view(batch, 2 * n)[idx].cpu().numpy(), oq.reshape(16, -1))
     del dq, de, qo, eo

@@ -150,10 +150,12 @@ def test_bfp_codec_matches_oracle(rng):
         assert ff.bfp_exponent(x) == O.bfp_exponent(x), x
     x = (crandn(rng, 64 * 40) * 10.0 ** rng.uniform(-3, 3)).astype(np.complex64)
     x[:64] = 0
-    q, e = ff.bfp_quantize(x)
-    oq, oe = O.bfp_quantize(x)
-    assert np.array_equal(q, oq) and np.array_equal(e, oe)
-    assert np.array_equal(ff.bfp_dequantize(q, e), O.bfp_dequantize(oq, oe))
+    for block in (64, 128, 640, 64 * 40):
+        q, e = ff.bfp_quantize(x, block=block)
+        oq, oe = O.bfp_quantize(x, block=block)
+        assert e.size == x.size // block
+        assert np.array_equal(q, oq) and np.array_equal(e, oe)
+        assert np.array_equal(ff.bfp_dequantize(q, e, block=block), O.bfp_dequantize(oq, oe, block=block))
 
 
 def test_status_codes_without_gpu_calls():
@@ -168,15 +170,18 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_conv_f32(fake, fake, 17, fake, 4096, 1, 0, 2, 0, None) == ff.ERR_INVALID
     assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, -1, 0, 2, 0, None) == ff.ERR_INVALID
     assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, 1, 0, 9, 0, None) == ff.ERR_INVALID
-    assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 256, 1, 0, 1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 256, 1, 64, 0, 1, 0, None) == ff.ERR_UNSUPPORTED
+    for block in (32, 96, 8192):                # below 64, not a power of two, longer than n
+        assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 4096, 1, block, 0, 1, 0, None) == ff.ERR_INVALID
     assert L.fufft_conv_large_f32(fake, fake, 0, 4096, 1, 0, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_conv_large_f32(fake, fake, 3, 32768, 1, 0, None) == ff.ERR_INVALID
     assert L.fufft_conv2d_f32(fake, fake, 0, fake, 128, 512, 1, 0, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 100, 1, 0, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_conv2d_f32(fake, fake, 5, fake, 512, 512, 1, 0, None) == ff.ERR_INVALID
     assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake, 512, 512, 2, 0, None) == ff.ERR_INVALID
-    assert L.fufft_bfp_quantize(None, 64, None, None) == ff.ERR_INVALID
-    assert L.fufft_bfp_quantize(fake, 65, fake, fake) == ff.ERR_INVALID
+    assert L.fufft_bfp_quantize(None, 64, 64, None, None) == ff.ERR_INVALID
+    assert L.fufft_bfp_quantize(fake, 65, 64, fake, fake) == ff.ERR_INVALID
+    assert L.fufft_bfp_quantize(fake, 64, 0, fake, fake) == ff.ERR_INVALID
     assert L.fufft_c2c_f32(fake, fake, 4096, 1, 0, 2, None) == ff.ERR_INVALID
     assert L.fufft_c2c_f32(fake, fake, 4097, 1, -1, 2, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_c2c_f32(fake + 8, fake, 4096, 1, -1, 2, None) == ff.ERR_ALIGN
