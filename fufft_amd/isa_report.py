@@ -141,10 +141,12 @@ def decode_name(name: str) -> dict | None:
         n, v, lay, kind, mid = map(int, m.groups())
         return {"family": "conv1d", "n": n, "v": v, "layout": LAYOUTS[lay], "kind": KINDS[kind],
                 "mid": MIDS[mid]}
-    m = re.search(r"bfp_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)E", name)
+    m = re.search(r"bfp_kernelILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb([01])E", name)
     if m:
-        n, v, lay, mid = map(int, m.groups())
-        return {"family": "bfp", "n": n, "v": v, "layout": LAYOUTS[lay], "kind": "conv", "mid": MIDS[mid]}
+        n, v, lay, mid, big = map(int, m.groups())
+        # big: blocks of more than 64 points (LDS rendezvous of the block maxima)
+        return {"family": "bfp", "n": n, "v": v, "layout": LAYOUTS[lay],
+                "kind": "conv_blocks" if big else "conv", "mid": MIDS[mid]}
     return None
 
 
