@@ -292,7 +292,7 @@ const char* fufft_status_string(int status)
       case FUFFT_ERR_INVALID:     return "invalid argument";
       case FUFFT_ERR_UNSUPPORTED: return "unsupported size or variant";
       case FUFFT_ERR_HIP:         return "HIP runtime error";
-      case FUFFT_ERR_ALIGN:       return "pointer not 16-byte aligned";
+      case FUFFT_ERR_ALIGN:       return "misaligned pointer (16 bytes for fp32 data, 4 for BFP data)";
       default:                    return "unknown status";
    }
 }

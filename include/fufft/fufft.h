@@ -38,7 +38,7 @@ extern "C" {
 #define FUFFT_ERR_INVALID      -1   /* null pointer, bad count, stride or enum */
 #define FUFFT_ERR_UNSUPPORTED  -2   /* size / variant combination not built    */
 #define FUFFT_ERR_HIP          -3   /* HIP runtime error (init, launch)        */
-#define FUFFT_ERR_ALIGN        -4   /* pointer not 16-byte aligned             */
+#define FUFFT_ERR_ALIGN        -4   /* misaligned pointer (16 B fp32, 4 B BFP)  */
 
 /* ---- enums ----------------------------------------------------------------- */
 /* mid operation between forward and inverse (Mid policies, fufft.cuh:616-650) */
