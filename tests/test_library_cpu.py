@@ -189,7 +189,7 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_plan_filter_device_f32(fake, fake + 16, 4096, 1, 2, 0, 5, 1, None) == ff.ERR_INVALID
     assert L.fufft_plan_filter_large_device_f32(fake, fake, 4096, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_plan_filter2d_device_f32(fake, fake, 512, 100, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
-    assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("pointer")
+    assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("misaligned pointer")
 
 
 def test_cpp_mirror_header_builds_and_runs(tmp_path):
