@@ -108,8 +108,15 @@ __device__ __forceinline__ uint32_t block_maxima(uint32_t (&m)[V], uint32_t lane
 // bmax words per transform for blocks of 128 points or more
 constexpr int bfp_bmax_words(int n) { return n / 128; }
 
+// Radix-8 lanes run 8 wavefronts per SIMD within 64 VGPRs.  Without the hint
+// the long-block epilogue (N = 4096) and the radix-8 N = 8192 plan allocate
+// 71, i.e. 7 wavefronts per SIMD (for N = 8192 one 1024-lane workgroup per CU
+// instead of two); with it they fit 64 without spilling.  The XOR layout
+// (the comparison option) keeps the compiler's choice: at 64 it spills.
+constexpr int bfp_min_waves(int v, int layout) { return (v == 8 && layout != LAYOUT_XOR) ? 8 : 1; }
+
 template<int N, int V, int LAYOUT, int MID, bool BIG>
-__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V))
+__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
 bfp_kernel(const BfpParams p)
 {
    using PL = Plan<N, V>;
