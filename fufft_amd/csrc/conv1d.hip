@@ -58,7 +58,7 @@ conv1d_kernel(const Conv1dParams p)
    // the wavefront's first transform (uniform) and this lane's offset from it
    const uint32_t t0 = (T >= 64) ? (uint32_t)uniform((int)t)
                                  : blockIdx.x * CPB + (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
-   const uint32_t lane_pos = (t - t0) * N + L;
+   const uint32_t lane_pos = (T >= 64) ? (uint32_t)L : (t - t0) * N + L;
 
    float2* A = lds + slot * SLOT;
    // phase timer: every memory operation retired and every wavefront of the
@@ -157,8 +157,10 @@ conv1d_kernel(const Conv1dParams p)
    } else {
       if constexpr(!C2C_INV) {
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
-         const uint32_t fo = (modulo_count(t, p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
-         mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
+         const uint32_t fb0 = modulo_count(t, p.fcount) * N;
+         // a uniform branch on the filter layout: each side computes only its own offset
+         if(p.fl == FLT_DR) mid_op<PL, MID>(r, fb, (fb0 + L * V) * 8u, 8u);
+         else               mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
       }
       stamp(3);
       inverse_dit<PL, LD, LANES, 64, KEEP_I>(r, A, L, tw, kc);
