@@ -72,6 +72,22 @@ def build_probe() -> Path:
     return PROBE_LIB
 
 
+def build_cpp_checks() -> Path:
+    """The C++ caller test (tests/cpp/abi_gpu_check.cpp): host code only,
+    linked against this library and the HIP runtime; run on a GPU by
+    tests/test_gpu_cpp_caller.py."""
+    src = ROOT / "tests" / "cpp" / "abi_gpu_check.cpp"
+    out_dir = ROOT / "tests" / "cpp" / "_build"
+    out_dir.mkdir(exist_ok=True)
+    exe = out_dir / "abi_gpu_check"
+    rocm = Path(HIPCC).resolve().parent.parent
+    _run(["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+          f"-I{ROOT / 'include'}", f"-I{rocm / 'include'}", str(src),
+          f"-L{PKG}", "-lfufft_amd", f"-L{rocm / 'lib'}", "-lamdhip64",
+          "-Wl,-rpath,$ORIGIN/../../../fufft_amd", f"-Wl,-rpath,{rocm / 'lib'}", "-o", str(exe)])
+    return exe
+
+
 def build_oracle() -> None:
     _run(["make", "-s", "-C", str(ORACLE)])
     if (REFERENCE / "verify_kernel.cpp").exists() and shutil.which("g++"):
@@ -82,6 +98,8 @@ def build(jobs: int = 8) -> None:
     build_oracle()
     build_library(jobs)
     build_probe()
+    if shutil.which("g++"):
+        build_cpp_checks()
 
 
 if __name__ == "__main__":
