@@ -354,3 +354,42 @@ def test_bfp_quantize_round_trip_and_saturation(rng):
         assert m <= 32767 * step
     # the block max lands within one binade below full scale
     assert np.abs(q.astype(np.int32)).reshape(-1, 128)[1:].max(axis=1).min() >= 16383
+
+
+@pytest.mark.parametrize("block", [64, 128, 512, 4096])
+def test_bfp_quantize_any_block_closed_form(block, rng):
+    """Blocks of any length: q = rint(x * 2^-e) with e from the block's abs-max
+    (the exponent rule is pinned above), restated in numpy."""
+    nb = 6
+    x = crandn(rng, block * nb) * np.repeat(10.0 ** rng.uniform(-3, 3, nb), block).astype(np.float32)
+    x[:block] = 0                                               # a zero block
+    q, e = O.bfp_quantize(x, block=block)
+    assert e.size == nb
+    for b in range(nb):
+        blk = x[block * b:block * (b + 1)]
+        m = np.float32(max(np.abs(blk.real).max(), np.abs(blk.imag).max()))
+        eb = O.bfp_exponent(float(m))
+        assert e[b] == eb
+        want = np.empty(2 * block, dtype=np.int16)
+        want[0::2] = np.rint(np.ldexp(blk.real.astype(np.float64), -eb))
+        want[1::2] = np.rint(np.ldexp(blk.imag.astype(np.float64), -eb))
+        assert np.array_equal(q[2 * block * b:2 * block * (b + 1)], want)
+    assert np.array_equal(O.bfp_dequantize(q, e, block=block).view(np.uint32),
+                          np.concatenate([np.ldexp(q[0::2].astype(np.float32), np.repeat(e, block))
+                                          + 1j * np.ldexp(q[1::2].astype(np.float32), np.repeat(e, block))
+                                          ]).astype(np.complex64).view(np.uint32))
+
+
+@pytest.mark.parametrize("n,block", [(512, 512), (1024, 256), (4096, 64), (4096, 4096)])
+def test_bfp_conv_is_dequantise_conv_quantise(n, block, rng):
+    """The BFP conv is the fp32 conv of the dequantised input, quantised with
+    the same block length: a composition of pinned pieces."""
+    batch = 3
+    x = crandn(rng, batch * n) * np.repeat(10.0 ** rng.uniform(-3, 3, batch), n).astype(np.float32)
+    q, e = O.bfp_quantize(x, block=block)
+    filt = crandn(rng, n, scale=1.0 / n)
+    plan = O.kernel_plan(n, 8)
+    oq, oe = O.bfp_conv(q, e, filt, n, plan, block=block)
+    y = O.conv(O.bfp_dequantize(q, e, block=block), filt, n, plan)
+    wq, we = O.bfp_quantize(y, block=block)
+    assert np.array_equal(oe, we) and np.array_equal(oq, wq)
