@@ -2,6 +2,8 @@
 
 - Two conv calls issued on two different streams at once compute exactly what
   they compute one after the other (the calls are stateless).
+- Four host threads on four streams call four entry points concurrently, with
+  the same results.
 - fufft_conv_f32, the four-step chain and the 2D conv captured in a graph
   (torch.cuda.CUDAGraph drives hipStreamBeginCapture) replay bit-identically
   to the eager call, replay after replay, with eager work in between.  None
@@ -93,3 +95,79 @@ def test_graph_capture_fourstep_and_2d(dev, rng):
     f2 = torch.from_numpy(ff.plan_filter2d(crandn(rng, (h, w)), h, w, kind=ff.FILTER_TAPS)).to(dev)
     out2 = torch.empty_like(img)
     _graph_matches_eager(lambda s: ff.conv2d(img, f2, out2, h, w, batch=2, stream=s), out2)
+
+
+def test_host_threads_call_concurrently(dev, rng):
+    """Four host threads, each on its own stream, call different entry points
+    at the same time (ctypes releases the GIL, so the library is entered
+    concurrently, including first-use paths such as the dynamic-LDS
+    attribute); every result equals the one computed alone beforehand."""
+    import threading
+    import torch
+    import fufft_amd as ff
+    n1, b1 = 8192, 512                                  # fp32 conv, radix 16
+    x1 = torch.from_numpy(crandn(rng, (b1, n1))).to(dev)
+    f1 = torch.from_numpy(ff.plan_filter(crandn(rng, n1), n1, "auto", kind=ff.FILTER_TAPS)).to(dev)
+    nq, bq = 2048, 512                                  # BFP, 256-point blocks
+    q, e = ff.bfp_quantize(crandn(rng, bq * nq), block=256)
+    dq, de = torch.from_numpy(q).to(dev), torch.from_numpy(e).to(dev)
+    fq = torch.from_numpy(ff.plan_filter(crandn(rng, nq), nq, "auto", kind=ff.FILTER_TAPS)).to(dev)
+    nl, bl = 65536, 8                                   # four-step
+    xl = torch.from_numpy(crandn(rng, bl * nl)).to(dev)
+    fl = torch.from_numpy(ff.plan_filter_large(crandn(rng, nl), nl, kind=ff.FILTER_TAPS)).to(dev)
+    h = w = 256                                         # 2D
+    x2 = torch.from_numpy(crandn(rng, 6 * h * w)).to(dev)
+    f2 = torch.from_numpy(ff.plan_filter2d(crandn(rng, h * w), h, w, kind=ff.FILTER_TAPS)).to(dev)
+
+    def job_conv(out, s):
+        ff.conv(x1, f1, out, n=n1, batch=b1, variant="auto", stream=s)
+
+    def job_bfp(out, s):
+        ff.conv_bfp16(dq, de, fq, out[0], out[1], n=nq, batch=bq, block=256, stream=s)
+
+    def job_large(out, s):
+        out.copy_(xl)                                   # conv_large works in place
+        ff.conv_large(out, fl, n=nl, batch=bl, stream=s)
+
+    def job_2d(out, s):
+        ff.conv2d(x2, f2, out, h, w, batch=6, stream=s)
+
+    jobs = [(job_conv, lambda: torch.empty_like(x1)),
+            (job_bfp, lambda: (torch.empty_like(dq), torch.empty_like(de))),
+            (job_large, lambda: torch.empty_like(xl)),
+            (job_2d, lambda: torch.empty_like(x2))]
+    ref = []
+    for job, make in jobs:
+        out = make()
+        job(out, None)
+        ref.append(out)
+    torch.cuda.synchronize()
+    print("case four host threads", flush=True)
+    errors, outs = [], [make() for _, make in jobs]
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                if jobs[i][0] is job_large:
+                    jobs[i][0](outs[i], s)              # the copy rides on s as well
+                else:
+                    for _ in range(4):
+                        jobs[i][0](outs[i], s)
+            s.synchronize()
+        except Exception as ex:                         # reported by the main thread
+            errors.append(repr(ex))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(jobs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for i, (r, o) in enumerate(zip(ref, outs)):
+        if isinstance(r, tuple):
+            assert torch.equal(r[0], o[0]) and torch.equal(r[1], o[1]), i
+        else:
+            assert torch.equal(r.view(torch.int64), o.view(torch.int64)), i
