@@ -505,7 +505,9 @@ def main():
                          "plan": f"{lout} outer radix-16 level(s) + fused middle N={mid}",
                          "model_bytes_per_point": model,
                          "frac_model": round(model * pts / a / 1e9 / HBM_PEAK_GBS, 4),
-                         "physical_bytes_per_point": model - 8,
+                         # three passes of 16 B (the two outer levels of a two-level plan
+                         # run as one pass); the filter is cache-resident
+                         "physical_bytes_per_point": 48,
                          "rel_l2": r}
     if large:
         line["large"] = large

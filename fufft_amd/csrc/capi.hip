@@ -726,6 +726,20 @@ int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n, cons
    return FUFFT_OK;
 }
 
+// the forward (DIF, largest stride first) or inverse (DIT, smallest first)
+// outer levels of a four-step plan; two levels run as one fused pass
+static hipError_t outer_levels(float2* a, int64_t n, int64_t batch, int lout, bool dit, const float2* tw,
+                               hipStream_t s)
+{
+   if(lout == 2) return launch_outer2_pass(a, n, batch, dit, tw, s);
+   hipError_t e = hipSuccess;
+   for(int i = 0; i < lout && e == hipSuccess; i++) {
+      const int l = dit ? lout - 1 - i : i;
+      e = launch_outer_pass(a, n, batch, n >> (4 * (l + 1)), dit, tw, s);
+   }
+   return e;
+}
+
 int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int64_t count,
                                        int filter_kind, int fold_inv_n, void* stream)
 {
@@ -753,10 +767,8 @@ int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int
    // taps: the forward half of the four-step chain, in place on out
    if(in != out && hipMemcpyAsync(out, in, (size_t)count * n * 8, hipMemcpyDeviceToDevice, s) != hipSuccess)
       return FUFFT_ERR_HIP;
-   for(int l = 0; l < lout; l++) {
-      const hipError_t e = launch_outer_pass(static_cast<float2*>(out), n, count, n >> (4 * (l + 1)), false, tw, s);
-      if(e != hipSuccess) return status_of(e);
-   }
+   if(const hipError_t e = outer_levels(static_cast<float2*>(out), n, count, lout, false, tw, s); e != hipSuccess)
+      return status_of(e);
    Conv1dParams p{};
    p.tw = tw; p.in0 = out; p.out0 = out;
    p.ntrans = (uint32_t)(count * (n / mn));
@@ -787,10 +799,8 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
    for(int64_t t0 = 0; t0 < batch; t0 += sub) {
       const int64_t nb = batch - t0 < sub ? batch - t0 : sub;
       float2* a = static_cast<float2*>(buf) + t0 * n;
-      hipError_t e = hipSuccess;
       // forward outer levels, largest stride first
-      for(int l = 0; l < lout && e == hipSuccess; l++)
-         e = launch_outer_pass(a, n, nb, n >> (4 * (l + 1)), false, p.tw, s);
+      hipError_t e = outer_levels(a, n, nb, lout, false, p.tw, s);
       if(e != hipSuccess) return status_of(e);
       // the middle: every mn-point chunk is one fused conv, in place; chunk c
       // of a transform uses filter slots [c*mn, (c+1)*mn) of the chained order
@@ -803,8 +813,7 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
       q.scount = 1; q.mid = mid; q.fl = FUFFT_LAYOUT_DR;
       if((st = run_conv1d(K_CONV, mn, v, q, stream)) != FUFFT_OK) return st;
       // inverse outer levels, smallest stride first
-      for(int l = lout - 1; l >= 0 && e == hipSuccess; l--)
-         e = launch_outer_pass(a, n, nb, n >> (4 * (l + 1)), true, p.tw, s);
+      e = outer_levels(a, n, nb, lout, true, p.tw, s);
       if(e != hipSuccess) return status_of(e);
    }
    return FUFFT_OK;

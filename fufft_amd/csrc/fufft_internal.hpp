@@ -104,6 +104,10 @@ hipError_t launch_bfp(int n, int v, int layout, const BfpParams& p, hipStream_t 
 // ---- four-step outer levels (large.hip) -------------------------------------------
 // one radix-16 level (stride M) over a batch of n-point transforms, in place;
 // dit = false: forward DIF level, dit = true: inverse DIT level
+// both outer levels of a two-level plan (n = 16 * 16 * mid, n >= 2^17) in one
+// pass through LDS; bit-identical to the two single-level launches
+hipError_t launch_outer2_pass(float2* buf, int64_t n, int64_t batch, bool dit, const float2* tw,
+                              hipStream_t s);
 hipError_t launch_outer_pass(float2* buf, int64_t n, int64_t batch, int64_t M, bool dit,
                              const float2* tw, hipStream_t s);
 

@@ -254,7 +254,10 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
  * levels (run_large / MidLaunch, bench_fufft.cu:357-492;
  * fufft_outer_pass_r, fufft.cuh:1113-1140).  buf is transformed in place.
  * filt is in the chained digit order (fufft_large_digit_order).
- * 4*lout + 3 HBM passes.  The middle runs radix 8 (FUFFT_R8) at every mid. */
+ * The reference makes 4*lout + 3 HBM passes; here the two outer levels of a
+ * two-level plan (n >= 2^17) run as one pass through LDS, bit-identical, so
+ * every plan reads and writes the data three times.  The middle runs radix 8
+ * (FUFFT_R8) at every mid. */
 int fufft_large_plan(int64_t n, int* lout, int* mid);
 int fufft_large_digit_order(int64_t n, int32_t* perm);
 int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n,
