@@ -426,3 +426,30 @@ def test_model_reproduces_kernel_counters():
     scat = sum(cost([pad(lane_bin(L, n, v) + k * T) for L in range(T)]) for k in range(v))
     gath = sum(cost([pad(L + q * T) for L in range(T)]) for q in range(v))
     assert scat + gath == 128
+
+
+# ---- two outer levels in one pass (large.hip: outer2_kernel) -------------------------------
+# 256 threads, tid = jj + 16 * hi; slot(k1, k2, jj) = k1 * 272 + k2 * 16 + jj.
+# Forward: threads (jj, k2 = hi) write slot(k1, hi, jj) for every k1, then
+# threads (jj, k1 = hi) read slot(hi, k2, jj) for every k2; the inverse swaps
+# the roles.  Both sides must be conflict-free under both bank rules.
+def outer2_slot(k1, k2, jj):
+    return k1 * 272 + k2 * 16 + jj
+
+
+def test_outer2_exchange_conflict_free():
+    sides = {
+        "k2 fixed per thread, loop k1": lambda tid, q: outer2_slot(q, tid >> 4, tid & 15),
+        "k1 fixed per thread, loop k2": lambda tid, q: outer2_slot(tid >> 4, q, tid & 15),
+    }
+    for name, slot in sides.items():
+        for q in range(16):
+            addrs = [slot(tid, q) for tid in range(256)]
+            assert len(set(addrs)) == 256
+            for w0 in range(0, 256, 64):
+                wave = addrs[w0:w0 + 64]
+                assert conflict_cycles(wave, "read_b64") == 0, (name, q)
+                assert conflict_cycles(wave, "write_b64") == 0, (name, q)
+    # without the 16-slot skew per k1 block the half-wavefront rule fails
+    flat = [(tid >> 4) * 256 + q * 16 + (tid & 15) for q in (0,) for tid in range(64)]
+    assert conflict_cycles(flat, "read_b64") > 0
