@@ -127,8 +127,22 @@ def rel_l2(got, want):
     return float(np.linalg.norm(got - want) / np.linalg.norm(want))
 
 
-def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, settle_s=0.0):
-    """fp32 fused conv at size n over pts points: (seconds per launch, rel L2 of a sample)."""
+def per_launch_us(torch, fn, count, stream):
+    """Durations of `count` launches timed one by one (an event pair around
+    each), in microseconds -- after the timed region, so that region's own
+    timing is untouched."""
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(count)]
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in ev]
+
+
+def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, settle_s=0.0, per_launch=0):
+    """fp32 fused conv at size n over pts points: (seconds per launch, rel L2 of
+    a sample), plus the one-by-one launch durations in us when per_launch > 0."""
     batch = pts // n
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -150,7 +164,10 @@ def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, set
     want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
     rel = rel_l2(ys, want)
     secs = time_launches(torch, step, steps, warmup, stream, settle_s)
+    each = per_launch_us(torch, step, per_launch, stream) if per_launch else []
     del x, out
+    if per_launch:
+        return secs / steps, rel, each
     return secs / steps, rel
 
 
@@ -414,7 +431,8 @@ def main():
         return
     copy_gbs, _ = copy_ceiling(torch, dev, pts, 20, 3, stream)
 
-    avg, rel = bench_fp32(torch, ff, dev, n, pts, args.variant, args.steps, args.warmup, stream, 1234)
+    avg, rel, each = bench_fp32(torch, ff, dev, n, pts, args.variant, args.steps, args.warmup, stream, 1234,
+                                per_launch=50)
     if not rel <= 2e-6:
         print(json.dumps({"error": f"fp32 accuracy check failed at N={n}: rel L2 {rel:.3e}"}))
         sys.exit(1)
@@ -431,6 +449,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(avg * 1e3, 5),
+        # median / min / max of 50 further launches timed one by one (event pair
+        # around each), after the timed region
+        "launch_us": {"median": round(float(np.median(each)), 2), "min": round(min(each), 2),
+                      "max": round(max(each), 2), "count": len(each)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
