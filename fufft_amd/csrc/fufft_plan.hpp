@@ -60,11 +60,14 @@ __device__ __forceinline__ void static_for(F&& f)
 
 // ---- LDS layouts ------------------------------------------------------------------
 // phys(i) maps logical position i of a transform to its float2 slot.  gfx950
-// LDS has 64 banks of 4 bytes; a ds_read_b64 / ds_write_b64 is serviced 32
-// lanes at a time, so lanes of an aligned half-wave conflict when their slots
-// are equal modulo 32 (measured with SQ_LDS_BANK_CONFLICT; each extra way costs
-// one cycle per instruction).  tests/test_lds_audit.py checks every access
-// pattern of every plan against this model.
+// LDS bank model, measured with SQ_LDS_BANK_CONFLICT (fufft_amd/lds_probe.py):
+// ds_read_b64 is serviced 32 lanes at a time, so lanes of an aligned
+// half-wavefront conflict when their slots agree modulo 32; ds_write_b64 and
+// each 8-byte access of the paired forms the exchanges compile to
+// (ds_read2_b64, ds_write2_b64, ds_read2st64_b64) are serviced 16 lanes at a
+// time, so lanes of an aligned quarter-wavefront conflict when their slots
+// agree modulo 16.  Each extra way costs one cycle.  tests/test_lds_audit.py
+// checks every access pattern of every plan against both rules.
 //
 // Xor: bits [0, v) ^= bits [v, 2v), bits [v, 5) ^= bits [2v, v+5).  Conflict
 // free for every pass pattern, but the XOR keeps one address register per tap.
@@ -98,8 +101,8 @@ struct Lds;
 //    layouts map block boundaries to the same slot, so wavefronts never touch
 //    each other's slots.
 // tests/test_lds_audit.py checks all of this by brute force for every plan.
-// Under the 64-bank model every exchange is conflict free, where the single
-// padded layout below leaves 2-way conflicts after the wide passes.
+// Under both rules every exchange is conflict free, where the single padded
+// layout below leaves 2-way conflicts after the wide passes.
 template<class PL, int E>
 struct XchgLds {
    static constexpr int reader_stride(int e)
