@@ -37,7 +37,7 @@ def resolve_variant(n: int, variant: str) -> str:
     """The lane layout FUFFT_AUTO picks for n (mirrors the library's rule)."""
     if variant != "auto":
         return variant
-    return "r8" if n in (512, 4096) else "v16"
+    return "r8" if n in (512, 4096, 8192) else "v16"
 
 
 class FufftError(RuntimeError):

@@ -115,6 +115,11 @@ constexpr int bfp_bmax_words(int n) { return n / 128; }
 // (the comparison option) keeps the compiler's choice: at 64 it spills.
 constexpr int bfp_min_waves(int v, int layout) { return (v == 8 && layout != LAYOUT_XOR) ? 8 : 1; }
 
+// The BFP kernels take the per-exchange layouts at every plan: under the
+// 64-VGPR bound above the radix-8 N = 8192 plan fits them without spilling
+// (the fp32 kernel of that plan does not, so it keeps the padded layout).
+constexpr int bfp_lds_layout(int n, int v) { return (void)n, (void)v, LAYOUT_XCHG; }
+
 template<int N, int V, int LAYOUT, int MID, bool BIG>
 __global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
 bfp_kernel(const BfpParams p)
@@ -277,9 +282,9 @@ static hipError_t launch_bfp_nv(int layout, const BfpParams& p, hipStream_t s)
       }
    }
    switch(p.mid) {
-      case MID_MUL:  return launch_bfp_one<N, V, default_lds_layout(N, V), MID_MUL>(p, s);
-      case MID_CONJ: return launch_bfp_one<N, V, default_lds_layout(N, V), MID_CONJ>(p, s);
-      default:       return launch_bfp_one<N, V, default_lds_layout(N, V), MID_NONE>(p, s);
+      case MID_MUL:  return launch_bfp_one<N, V, bfp_lds_layout(N, V), MID_MUL>(p, s);
+      case MID_CONJ: return launch_bfp_one<N, V, bfp_lds_layout(N, V), MID_CONJ>(p, s);
+      default:       return launch_bfp_one<N, V, bfp_lds_layout(N, V), MID_NONE>(p, s);
    }
 }
 

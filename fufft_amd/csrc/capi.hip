@@ -178,14 +178,14 @@ bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0
 
 // FUFFT_AUTO resolves to the faster lane layout measured on MI355X, one rule
 // for the fp32 and the BFP conv (a filter planned at FUFFT_AUTO must match
-// both): radix 8 at N = 512 and 4096, radix 16 elsewhere.  Same box, 2^27
-// points, Gpt/s radix 8 / radix 16: fp32 N = 512 371 / 345, 1024 330 / 337,
-// 2048 323 / 328, 4096 317 / 306, 8192 257 / 255; BFP N = 1024 406 / 424,
-// 2048 384 / 386, 4096 365 / 368, 8192 215 / 298.
+// both): radix 8 at N = 512, 4096 and 8192, radix 16 elsewhere.  Same box,
+// 2^27 points, Gpt/s radix 8 / radix 16: fp32 N = 512 371 /345, 1024
+// 330 / 337, 2048 323 / 328, 4096 317 / 306, 8192 251-257 / 251-255; BFP
+// N = 1024 406 / 424, 2048 384 / 386, 4096 365 / 368, 8192 303 / 287.
 int resolve_variant(int64_t n, int variant)
 {
    if(variant != FUFFT_AUTO) return variant;
-   return (n == 512 || n == 4096) ? FUFFT_R8 : FUFFT_V16;
+   return (n == 512 || n == 4096 || n == 8192) ? FUFFT_R8 : FUFFT_V16;
 }
 
 // The four-step middle always runs radix 8 (N = 512 .. 4096 per chunk).

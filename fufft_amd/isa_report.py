@@ -234,8 +234,12 @@ def occupancy(vgpr: int, agpr: int, lds_bytes: int, waves_per_wg: int) -> dict:
     return {"waves_per_simd": int(min(limits.values())), "limited_by": lim, "vgpr_alloc": regs}
 
 
-def default_layout(n: int, v: int) -> str:
-    """The LDS layout a plan runs by default (default_lds_layout in fufft_plan.hpp)."""
+def default_layout(n: int, v: int, family: str = "conv1d") -> str:
+    """The LDS layout a plan runs by default: default_lds_layout in fufft_plan.hpp
+    for the fp32 kernels; the BFP kernels take the per-exchange layouts at every
+    plan (bfp_lds_layout in bfp.hip)."""
+    if family == "bfp":
+        return "xchg"
     return "pad" if (v == 8 and n > 4096) else "xchg"
 
 
@@ -275,7 +279,7 @@ def main() -> None:
     ap.add_argument("--markdown", action="store_true")
     a = ap.parse_args()
     rows = [r for r in conv_rows() if r["kind"] == a.kind and r["mid"] == a.mid
-            and r["layout"] == (default_layout(r["n"], r["v"]) if a.layout == "default" else a.layout)]
+            and r["layout"] == (default_layout(r["n"], r["v"], r["family"]) if a.layout == "default" else a.layout)]
     rows.sort(key=lambda r: (r["family"], r["v"], r["n"]))
     if not a.markdown:
         for r in rows:

@@ -51,7 +51,7 @@ extern "C" {
 #define FUFFT_R8   1   /* 8 values per lane, radix 8 (fufft_pipeline_ip)     */
 #define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X, one
                           rule for the fp32 and the BFP conv: FUFFT_R8 at
-                          N = 512 and 4096, FUFFT_V16 elsewhere.  The filter
+                          N = 512, 4096 and 8192, FUFFT_V16 elsewhere.  The filter
                           must be planned with the same variant. */
 
 /* filter layouts */
