@@ -19,7 +19,6 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libfufft_amd.so"
-PROBE_LIB = PKG / "libfufft_lds_probe.so"
 ORACLE = ROOT / "oracle"
 REFERENCE = Path(os.environ.get("FUFFT_REFERENCE", "/root/reference"))
 
@@ -65,13 +64,6 @@ def build_library(jobs: int = 8) -> Path:
     return LIB
 
 
-def build_probe() -> Path:
-    """The LDS bank probe (a diagnostic, python -m fufft_amd.lds_probe)."""
-    src = CSRC / "probe" / "lds_probe.hip"
-    _run([HIPCC, *HIPFLAGS, "-shared", "-o", str(PROBE_LIB), str(src)])
-    return PROBE_LIB
-
-
 def build_cpp_checks() -> Path:
     """The C++ caller test (tests/cpp/abi_gpu_check.cpp): host code only,
     linked against this library and the HIP runtime; run on a GPU by
@@ -97,7 +89,6 @@ def build_oracle() -> None:
 def build(jobs: int = 8) -> None:
     build_oracle()
     build_library(jobs)
-    build_probe()
     if shutil.which("g++"):
         build_cpp_checks()
 

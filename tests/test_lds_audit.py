@@ -2,7 +2,7 @@
 
 For every plan (V, N) and every pass, it enumerates the slot each lane touches
 for each tap and checks it under the gfx950 bank model measured with
-SQ_LDS_BANK_CONFLICT (fufft_amd/lds_probe.py, profiles/lds_bank_model.md):
+SQ_LDS_BANK_CONFLICT (tests/lds_bank_model.py, profiles/lds_bank_model.md):
 ds_read_b64 is serviced 32 lanes at a time, so lanes of an aligned
 half-wavefront conflict when their slots agree modulo 32; each 8-byte access
 of ds_write_b64 and of the paired forms the exchanges use (ds_read2_b64,
@@ -29,7 +29,7 @@ from pathlib import Path
 
 import pytest
 
-from fufft_amd.lds_probe import PATTERNS, FORMS, conflict_cycles
+from tests.lds_bank_model import PATTERNS, FORMS, conflict_cycles
 
 ROOT = Path(__file__).resolve().parent.parent
 
