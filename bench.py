@@ -10,24 +10,29 @@ configs[1] sizes under "sweep".  Prints ONE JSON line.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 
-Timing: W untimed launches, then exactly K launches bracketed by
+Timing, the same for the headline and every other leg: a correctness check
+against fp64 first, then --settle seconds of untimed launches (after an idle
+gap the part runs 8-13% slow for the first tens of milliseconds while its
+clocks ramp), then W untimed launches, then exactly K launches bracketed by
 torch.cuda.synchronize(), measured with HIP events recorded on the stream the
 kernels are launched on.  Inputs are resident in HBM before the timed region.
 
 roofline.achieved uses the reference's bandwidth model, 3 passes x 8 B = 24
 bytes per point for fp32 (bench_fufft.cu:314-317), over the average launch
 duration; with a shared filter one of those passes is served from cache, so
-the physical minimum is 16 B/pt and `physical` reports that figure too.  For
-int16-BFP the model is 3 x 4 = 12 B/pt (physical 8 B/pt + 2 B per 64-point
-block of exponents); at the headline N, "bfp" also reports the same conv with
-one exponent per signal (block = N, the reference's per-transform scale).  roofline.traffic is the HBM bytes per launch measured by
-rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE) for this same command, read from the
-committed summary profiles/conv_f32_n4096.md when present.
+the physical minimum is 16 B/pt and `physical` reports that figure too, also
+as a fraction of the measured stream ceiling (fufft_stream_f32, plain and
+non-temporal, over the same bytes).  For int16-BFP the model is 3 x 4 = 12
+B/pt (physical 8 B/pt + 2 B per 64-point block of exponents); at the headline
+N, "bfp" also reports the same conv with one exponent per signal (block = N,
+the reference's per-transform scale).  roofline.traffic is the HBM bytes per
+launch measured by rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE) for this same
+command, read from the committed summary profiles/conv_f32_n4096.md.
 
-The cpu_baseline leg times the reference's own fp64 CPU conv path
-(cpu_mixed.cpp, built into oracle/_ref) -- or, where that was not built, this
-build's restatement of it -- on a bounded sample of the same workload, one
-thread per host core.
+The cpu_baseline leg times the reference's own CPU conv paths (cpu_mixed.cpp
+fp64, and verify_kernel.cpp's fp32 and int16-BFP transcriptions of the device
+dataflow, built into oracle/_ref) per N, on bounded samples of the same
+workloads, one thread per usable host core.
 """
 from __future__ import annotations
 
@@ -67,20 +72,26 @@ def parse():
     p.add_argument("--no-c2c", action="store_true", help="skip the natural-order C2C line")
     p.add_argument("--no-vendor", action="store_true", help="skip the rocFFT chain comparison")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=15.0)
+    p.add_argument("--cpu-seconds", type=float, default=20.0,
+                   help="wall seconds for all CPU-baseline rows together")
     p.add_argument("--settle", type=float, default=0.1,
                    help="seconds of untimed launches before each secondary figure (0 under PMC runs)")
     p.add_argument("--copy-only", action="store_true",
-                   help="time only a device copy of the workload's bytes (HBM ceiling and the "
-                        "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+                   help="time only the stream copy of the workload's bytes (HBM ceiling, and the copy "
+                        "of known size that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return p.parse_args()
 
 
-def copy_ceiling(torch, dev, pts, steps, warmup, stream):
-    """GB/s (read + write) of torch's device copy over pts complex64 points."""
+def stream_ceiling(torch, ff, dev, pts, steps, warmup, stream, nontemporal):
+    """GB/s (read + write) of the library's buffer-instruction stream copy
+    (fufft_stream_f32) over pts complex64 points, and seconds per copy."""
     x = torch.empty(pts, dtype=torch.complex64, device=dev).fill_(1.0)
     y = torch.empty_like(x)
-    secs = time_launches(torch, lambda: y.copy_(x), steps, warmup, stream, SETTLE_S)
+    secs = time_launches(torch, lambda: ff.stream_copy(x, y, pts * 8, nontemporal, stream=stream),
+                         steps, warmup, stream, SETTLE_S)
+    torch.cuda.synchronize()
+    if not torch.equal(x, y):
+        raise RuntimeError("stream copy produced a wrong result")
     del x, y
     return 2.0 * pts * 8 * steps / secs / 1e9, secs / steps
 
@@ -281,10 +292,10 @@ def bench_2d(torch, ff, dev, pts, steps, warmup, stream, seed):
     u, v = torch.empty_like(x), torch.empty_like(y)
     work = torch.empty(nimg * np_img, dtype=torch.complex64, device=dev)
     taps = rng.uniform(0, 1, np_img).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter2d(taps, h, w, kind=ff.FILTER_TAPS)).to(dev)
+    filt = torch.from_numpy(ff.plan_filter2d(taps, h, w, kind=ff.FILTER_TAPS, layout="lane")).to(dev)
 
     def r2():
-        ff.conv2d_r2(x, y, filt, u, v, work, h, w, nimg, stream=stream)
+        ff.conv2d_r2(x, y, filt, u, v, work, h, w, nimg, layout="lane", stream=stream)
 
     r2()
     torch.cuda.synchronize()
@@ -298,12 +309,13 @@ def bench_2d(torch, ff, dev, pts, steps, warmup, stream, seed):
     a = torch.rand(2 * np_img, device=dev, generator=gen).view(torch.complex64)
     spec = torch.empty_like(a)
     spec_nat = (rng.standard_normal((nf, np_img)) + 1j * rng.standard_normal((nf, np_img))).astype(np.complex64)
-    filters = torch.from_numpy(np.concatenate([ff.plan_filter2d(spec_nat[i], h, w) for i in range(nf)])).to(dev)
+    filters = torch.from_numpy(np.concatenate([ff.plan_filter2d(spec_nat[i], h, w, layout="lane")
+                                               for i in range(nf)])).to(dev)
     out = torch.empty(nf * np_img, dtype=torch.complex64, device=dev)
     ff.fwd2d(a, spec, h, w, 1, stream=stream)
 
     def apply():
-        ff.apply2d(spec, filters, out, h, w, nf, spec_stride=0, filt_stride=np_img, stream=stream)
+        ff.apply2d(spec, filters, out, h, w, nf, spec_stride=0, filt_stride=np_img, layout="lane", stream=stream)
 
     apply()
     torch.cuda.synchronize()
@@ -362,46 +374,149 @@ def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64):
     return secs / steps, rel_l2(got, want), float(per_sig.max())
 
 
-def cpu_baseline(n, seconds, threads):
-    """Reference CPU conv path on a bounded sample, `threads` host threads."""
-    sys.path.insert(0, str(ROOT))
-    from oracle import oracle as O                     # the checker library, CPU leg only
-    ref = O.load_ref()
-    rng = np.random.default_rng(3)
-    per_thread = 64
-    a = (rng.standard_normal((threads, per_thread, n)) + 1j * rng.standard_normal((threads, per_thread, n)))
-    s = (rng.standard_normal(n) + 1j * rng.standard_normal(n)) / n
-    s_full = np.ascontiguousarray(np.broadcast_to(s, (per_thread, n)))
-    out = np.empty_like(a)
+def usable_cores():
+    """(cores, affinity, quota): host cores this process may run on -- its CPU
+    affinity (os.sched_getaffinity), capped by a cgroup CPU quota where one is
+    set (cgroup v2 cpu.max, else v1 cfs_quota_us / cfs_period_us)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = int(q) / int(per)
+    except (OSError, ValueError):
+        try:
+            q = int(Path("/sys/fs/cgroup/cpu/cpu.cfs_quota_us").read_text())
+            per = int(Path("/sys/fs/cgroup/cpu/cpu.cfs_period_us").read_text())
+            if q > 0:
+                quota = q / per
+        except (OSError, ValueError):
+            pass
+    cores = affinity if quota is None else max(1, min(affinity, int(quota)))
+    return cores, affinity, quota
+
+
+def _timed_threads(threads, seconds, per_call, call):
+    """Run call(t) on `threads` host threads until `seconds` have passed; each
+    call processes per_call signals.  Returns (signals done, elapsed seconds)."""
     counts = [0] * threads
-    deadline = [0.0]
+    deadline = time.perf_counter() + seconds
 
     def work(t):
-        at = np.ascontiguousarray(a[t])
-        ot = out[t]
-        while time.perf_counter() < deadline[0]:
-            if ref is not None:
-                ref.ref_mixed_conv_f64(n, 16, at.ctypes.data, s_full.ctypes.data, n, ot.ctypes.data, per_thread)
-            else:
-                O.mixed_conv_f64(at, s_full, n, 16)
-            counts[t] += per_thread
+        while time.perf_counter() < deadline:
+            call(t)
+            counts[t] += per_call
 
-    deadline[0] = time.perf_counter() + seconds
     t0 = time.perf_counter()
     ths = [threading.Thread(target=work, args=(t,)) for t in range(threads)]
     for th in ths:
         th.start()
     for th in ths:
         th.join()
-    el = time.perf_counter() - t0
-    pts = sum(counts) * n
+    return sum(counts), time.perf_counter() - t0
+
+
+def cpu_baseline(sizes, bfp_sizes, head_n, seconds, threads):
+    """The reference's CPU conv paths on the GPU box's host cores, on bounded
+    samples of the bench workloads (Re/Im N(0,1) signals, one shared filter),
+    one thread per usable core, each thread looping over its own batch:
+
+    - fp64: cpu_mixed.cpp's V=16 fp64 DIF -> multiply -> DIT with per-twiddle
+      cos/sin (cpu_mixed.cpp:121-174, 260-266), per N in `sizes`; the headline
+      `value` is this row at head_n;
+    - fp32 transcription: verify_kernel.cpp's CPU transcription of the device
+      dataflow at the plan the GPU runs (kernel_pipeline_ip for radix 8,
+      kernel_pipeline_v16 for radix 16; verify_kernel.cpp:211-244, 1051-1082);
+    - BFP transcription: verify_kernel.cpp's kernel_v16_bfp (1111-1135), the
+      int16-BFP dataflow with one fp32 scale per transform, per N in bfp_sizes.
+
+    The reference's sources are built into oracle/_ref; where that library is
+    missing, this build's restatement (oracle/) stands in ("port")."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O                     # the checker library, CPU leg only
+    ref = O.load_ref()
+    kind = "reference" if ref is not None else "port"
+    per_row = seconds / (2 * len(sizes) + len(bfp_sizes))
+    rng = np.random.default_rng(3)
+    rows = {"fp64_cpu_mixed": {}, "fp32_transcription": {}, "bfp16_transcription": {}}
+
+    def gpts(done, el, n):
+        return round(done * n / el / 1e9, 6)
+
+    for n in sizes:
+        per = max(1, 16384 // n)                       # signals per call and thread
+        a = rng.standard_normal((threads, per, n)) + 1j * rng.standard_normal((threads, per, n))
+        spec = (rng.standard_normal(n) + 1j * rng.standard_normal(n)) / n
+        s_full = np.ascontiguousarray(np.broadcast_to(spec, (per, n)))
+        out = np.empty_like(a)
+
+        def f64(t):
+            if ref is not None:
+                ref.ref_mixed_conv_f64(n, 16, a[t].ctypes.data, s_full.ctypes.data, n, out[t].ctypes.data, per)
+            else:
+                O.mixed_conv_f64(a[t], s_full, n, 16)
+        done, el = _timed_threads(threads, per_row, per, f64)
+        rows["fp64_cpu_mixed"][str(n)] = {"gpoints_s": gpts(done, el, n), "signals": done, "seconds": round(el, 2)}
+
+        v = 8 if n in (512, 4096, 8192) else 16        # the plan FUFFT_AUTO runs on the GPU
+        plan = O.ref_plan(n, v)
+        lead = plan.radices[0] if plan.radices[0] != v else 1
+        nv = sum(1 for r in plan.radices if r == v)
+        a32 = a.astype(np.complex64)
+        f32 = np.ascontiguousarray(np.broadcast_to(spec[O.mixedrev(plan)].astype(np.complex64), (per, n)))
+        o32 = np.empty_like(a32)
+
+        def tr32(t):
+            if ref is not None:
+                fn = ref.ref_vk_pipeline_ip if v == 8 else ref.ref_vk_pipeline_v16
+                fn(n, lead, nv, 1, a32[t].ctypes.data, f32.ctypes.data, o32[t].ctypes.data, per)
+            else:
+                O.conv(a32[t], f32[0], n, plan, tw=O.TW_LIBM)
+        done, el = _timed_threads(threads, per_row, per, tr32)
+        rows["fp32_transcription"][str(n)] = {"gpoints_s": gpts(done, el, n), "plan": plan.radices,
+                                              "signals": done, "seconds": round(el, 2)}
+
+    for n in bfp_sizes:
+        plan = O.ref_plan(n, 16)                       # kernel_v16_bfp runs the radix-16 plan
+        lead = plan.radices[0] if plan.radices[0] != 16 else 1
+        nrv = sum(1 for r in plan.radices if r == 16)
+        per = max(1, 16384 // n)
+        x = (rng.standard_normal((threads, per, n)) + 1j * rng.standard_normal((threads, per, n))).astype(np.complex64)
+        spec = ((rng.standard_normal(n) + 1j * rng.standard_normal(n)) / n).astype(np.complex64)
+        qb = np.empty(2 * n, np.int16)
+        qa = np.empty((threads, per, 2 * n), np.int16)
+        sa = np.empty((threads, per), np.float32)
+        qo = np.empty_like(qa)
+        so = np.empty_like(sa)
+        if ref is not None:
+            sb = ref.ref_vk_bfp_quantize(np.ascontiguousarray(spec[O.mixedrev(plan)]).ctypes.data, n, qb.ctypes.data)
+            for t in range(threads):
+                for i in range(per):
+                    sa[t, i] = ref.ref_vk_bfp_quantize(x[t, i].ctypes.data, n, qa[t, i].ctypes.data)
+        qe, ee = O.bfp_quantize(x.reshape(-1), block=n)
+
+        def bfp(t):
+            if ref is not None:
+                ref.ref_vk_v16_bfp(n, lead, nrv, qa[t].ctypes.data, sa[t].ctypes.data, qb.ctypes.data, sb,
+                                   qo[t].ctypes.data, so[t].ctypes.data, per)
+            else:
+                O.bfp_conv(qe[2 * n * per * t:2 * n * per * (t + 1)], ee[per * t:per * (t + 1)],
+                           spec[O.mixedrev(plan)], n, plan, block=n)
+        done, el = _timed_threads(threads, per_row, per, bfp)
+        rows["bfp16_transcription"][str(n)] = {"gpoints_s": gpts(done, el, n), "plan": plan.radices,
+                                               "signals": done, "seconds": round(el, 2)}
+
+    head = rows["fp64_cpu_mixed"][str(head_n)]
+    total = sum(r["seconds"] for g in rows.values() for r in g.values())
     return {
-        "value": round(pts / el / 1e9, 6),
+        "value": head["gpoints_s"],
         "unit": "Gpoints/s",
         "cores": threads,
-        "kind": "reference" if ref is not None else "port",
-        "sample": (f"{sum(counts)} signals of N={n} (fp64 mixed-radix DIF -> multiply -> DIT with "
-                   f"per-twiddle cos/sin, cpu_mixed.cpp) in {el:.1f} s on {threads} threads"),
+        "kind": kind,
+        "sample": (f"N={head_n}: {head['signals']} signals of the fp64 cpu_mixed conv (mixed-radix DIF -> "
+                   f"multiply -> DIT, per-twiddle cos/sin) in {head['seconds']} s on {threads} threads, one per "
+                   f"usable host core; all rows below together {total:.0f} s of wall time"),
+        "rows": rows,
     }
 
 
@@ -426,13 +541,16 @@ def main():
     stream = torch.cuda.current_stream()
 
     if args.copy_only:
-        gbs, t = copy_ceiling(torch, dev, pts, args.steps, args.warmup, stream)
+        gbs, t = stream_ceiling(torch, ff, dev, pts, args.steps, args.warmup, stream, False)
         print(json.dumps({"copy_bytes": 2 * pts * 8, "ms": round(t * 1e3, 5), "gb_s": round(gbs, 1)}))
         return
-    copy_gbs, _ = copy_ceiling(torch, dev, pts, 20, 3, stream)
+    plain_gbs, _ = stream_ceiling(torch, ff, dev, pts, 20, 3, stream, False)
+    nt_gbs, _ = stream_ceiling(torch, ff, dev, pts, 20, 3, stream, True)
 
+    # the headline is timed like every other leg: correctness check first, then
+    # SETTLE_S of untimed launches, then exactly --warmup and --steps launches
     avg, rel, each = bench_fp32(torch, ff, dev, n, pts, args.variant, args.steps, args.warmup, stream, 1234,
-                                per_launch=50)
+                                SETTLE_S, per_launch=50)
     if not rel <= 2e-6:
         print(json.dumps({"error": f"fp32 accuracy check failed at N={n}: rel L2 {rel:.3e}"}))
         sys.exit(1)
@@ -449,6 +567,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(avg * 1e3, 5),
+        "settle_s": SETTLE_S,
         # median / min / max of 50 further launches timed one by one (event pair
         # around each), after the timed region
         "launch_us": {"median": round(float(np.median(each)), 2), "min": round(min(each), 2),
@@ -465,8 +584,11 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "model_bytes_per_point": 24,
                      "physical": {"bytes_per_point": 16, "achieved": round(physical, 1),
-                                  "frac": round(physical / HBM_PEAK_GBS, 4)},
-                     "copy_ceiling_gbs": round(copy_gbs, 1)},
+                                  "frac": round(physical / HBM_PEAK_GBS, 4),
+                                  "frac_of_stream": round(physical / max(plain_gbs, nt_gbs), 4)},
+                     # fufft_stream_f32 over the same 2^27 points: the measured HBM ceiling
+                     # of buffer-instruction streaming, plain and non-temporal
+                     "stream_ceiling_gbs": {"plain": round(plain_gbs, 1), "nt": round(nt_gbs, 1)}},
         "accuracy": {"rel_l2_vs_fp64_sample": rel},
     }
 
@@ -505,6 +627,7 @@ def main():
                            "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst,
                            "variant": ff.resolve_variant(s, "auto")}
             if s == n:
+                # both legs timed the same way: check, SETTLE_S, --warmup, --steps
                 bfp[str(s)]["speedup_vs_fp32"] = round(g / gpts, 3)
                 # one exponent per signal: the reference's per-transform scale
                 a, r, worst = bench_bfp(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 99 + s, block=s)
@@ -550,8 +673,12 @@ def main():
         line["conv2d"] = d2
 
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        line["cpu_baseline"] = cpu_baseline(n, args.cpu_seconds, threads)
+        cores, affinity, quota = usable_cores()
+        sizes = sorted({512, 1024, 2048, 4096, n})
+        cb = cpu_baseline(sizes, [int(v) for v in args.bfp_sizes.split(",") if v.strip()], n,
+                          args.cpu_seconds, cores)
+        cb["host"] = {"affinity_cpus": affinity, "cgroup_cpu_quota": quota, "threads": cores}
+        line["cpu_baseline"] = cb
     print(json.dumps(line))
 
 

@@ -2,8 +2,9 @@
 
 The compute path is the in-tree HIP library ``libfufft_amd.so`` (built by
 ``fufft_amd.build``).  There is no fallback: if the library is missing, import
-fails loudly.  Device memory is whatever the caller passes -- torch tensors on
-``cuda`` (ROCm) or raw device pointers.
+fails loudly.  Device buffers are torch tensors on ``cuda`` (ROCm); every
+launch wrapper checks their dtype, contiguity, size and device before the
+call (``_dev``), and launches on torch's current stream unless given one.
 
 torch is imported before the library is loaded so that both share torch's HIP
 runtime (torch bundles its own ``libamdhip64.so.7``; the loader then resolves
@@ -79,17 +80,18 @@ def _load() -> C.CDLL:
         "fufft_conv_large_f32": ([vp, vp, i64, i64, i64, i32, vp], i32),
         "fufft_plan2d": ([i64, i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
         "fufft_plan2d_column_order": ([i64, i64, C.POINTER(C.c_int32)], i32),
-        "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, vp, vp], i32),
-        "fufft_conv2d_f32": ([vp, vp, i64, vp, i64, i64, i64, i32, vp], i32),
-        "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, vp], i32),
+        "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, i32, vp, vp], i32),
+        "fufft_conv2d_f32": ([vp, vp, i64, vp, i64, i64, i64, i32, i32, vp], i32),
+        "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, i32, vp], i32),
         "fufft_fwd2d_f32": ([vp, vp, i64, i64, i64, vp], i32),
-        "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, i32, vp], i32),
         "fufft_c2c_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_stream_f32": ([vp, vp, i64, i32, vp], i32),
         "fufft_transforms_per_workgroup": ([i64, i32], i32),
         "fufft_conv_timed_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp, i64, vp], i32),
         "fufft_plan_filter_device_f32": ([vp, vp, i64, i64, i32, i32, i32, i32, vp], i32),
         "fufft_plan_filter_large_device_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
-        "fufft_plan_filter2d_device_f32": ([vp, vp, i64, i64, i64, i32, i32, vp], i32),
+        "fufft_plan_filter2d_device_f32": ([vp, vp, i64, i64, i64, i32, i32, i32, vp], i32),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name, None)
@@ -107,36 +109,88 @@ def check(status: int, where: str) -> None:
         raise FufftError(status, where)
 
 
-def _ptr(x) -> int | None:
-    """Device (or host) address of a tensor / numpy array / int / None."""
-    if x is None:
-        return None
-    if isinstance(x, int):
-        return x
-    if isinstance(x, np.ndarray):
-        return x.ctypes.data
-    return x.data_ptr()
+# Element types accepted for each kind of buffer (checked before any launch).
+_DT = {}
+if torch is not None:
+    _DT = {
+        "complex": (torch.complex64, torch.float32),          # interleaved (re, im) fp32
+        "real": (torch.float32,),
+        "bfp": (torch.int16, torch.int32),                    # int16 pairs, 4 bytes per point
+        "exp": (torch.int8, torch.uint8),
+        "words": (torch.int32,),
+    }
 
 
-def _stream(stream) -> int | None:
+def _check_shape(x, name: str, nbytes: int, kind: str) -> None:
+    if torch is None or not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch tensor in GPU memory, got {type(x).__name__}")
+    if x.dtype not in _DT[kind]:
+        allowed = ", ".join(str(d) for d in _DT[kind])
+        raise ValueError(f"{name}: dtype {x.dtype} is not one of {allowed}")
+    if not x.is_contiguous():
+        raise ValueError(f"{name}: tensor is not contiguous")
+    have = x.numel() * x.element_size()
+    if have < nbytes:
+        raise ValueError(f"{name}: holds {have} bytes, the call reads or writes {nbytes}")
+
+
+def _check_device(x, name: str) -> None:
+    if not x.is_cuda:
+        raise ValueError(f"{name}: tensor is on {x.device}, not in GPU memory")
+    if x.device.index != torch.cuda.current_device():
+        raise ValueError(f"{name}: tensor is on {x.device}, the current device is "
+                         f"cuda:{torch.cuda.current_device()}")
+
+
+def _ptrs(*specs) -> list:
+    """Device addresses for a launch.  Each spec is (tensor, name, nbytes,
+    kind), or None for an argument the call does not read.  Every tensor is
+    checked first for type, dtype (kind), contiguity and size (at least
+    nbytes), then every tensor for its device (the current GPU), so a host
+    array, a wrong dtype or a short buffer raises TypeError / ValueError here
+    and never becomes an out-of-bounds device access."""
+    for sp in specs:
+        if sp is not None:
+            _check_shape(*sp)
+    for sp in specs:
+        if sp is not None:
+            _check_device(sp[0], sp[1])
+    return [None if sp is None else sp[0].data_ptr() for sp in specs]
+
+
+def _count(stride: int, n: int, batch: int, name: str) -> int:
+    """Items an array of per-transform stride `stride` must hold (0 = one shared)."""
+    if stride == 0:
+        return 1
+    if stride == n:
+        return max(batch, 1)
+    raise ValueError(f"{name}: stride {stride} is neither 0 (shared) nor {n} (one per transform)")
+
+
+def _stream(stream) -> int:
+    """hipStream_t for a launch: an explicit torch stream or raw handle, else
+    torch's current stream (so launches order with the caller's torch work)."""
     if stream is None:
-        return None
+        return torch.cuda.current_stream().cuda_stream
     if isinstance(stream, int):
         return stream
     return stream.cuda_stream
 
 
 # ---- host planning ---------------------------------------------------------------
+# Every variant argument defaults to "auto" (FUFFT_AUTO), in the planners and
+# the launches alike, so a filter planned with the defaults always matches a
+# launch made with the defaults.
 
 def init(device: int = 0) -> None:
     check(lib.fufft_init(device), "fufft_init")
 
 
-def supported(n: int, variant: str = "v16") -> bool:
+def supported(n: int, variant: str = "auto") -> bool:
     return bool(lib.fufft_supported(n, VARIANT[variant]))
 
 
-def plan_radices(n: int, variant: str = "v16") -> list[int]:
+def plan_radices(n: int, variant: str = "auto") -> list[int]:
     buf = (C.c_int * 64)()
     np_ = lib.fufft_plan_radices(n, VARIANT[variant], buf)
     if np_ < 0:
@@ -144,7 +198,7 @@ def plan_radices(n: int, variant: str = "v16") -> list[int]:
     return list(buf[:np_])
 
 
-def plan_chains(n: int, variant: str = "v16") -> list[int]:
+def plan_chains(n: int, variant: str = "auto") -> list[int]:
     """Per pass: 0 single twiddle chain, 1 radix-16 even/odd chains."""
     buf = (C.c_int * 64)()
     np_ = lib.fufft_plan_chains(n, VARIANT[variant], buf)
@@ -153,18 +207,19 @@ def plan_chains(n: int, variant: str = "v16") -> list[int]:
     return list(buf[:np_])
 
 
-def digit_order(n: int, variant: str = "v16") -> np.ndarray:
+def digit_order(n: int, variant: str = "auto") -> np.ndarray:
     perm = np.empty(n, dtype=np.int32)
     check(lib.fufft_digit_order(n, VARIANT[variant], perm.ctypes.data_as(C.POINTER(C.c_int32))),
           "fufft_digit_order")
     return perm
 
 
-def plan_filter(x: np.ndarray, n: int, variant: str = "v16", layout: str = "dr",
+def plan_filter(x: np.ndarray, n: int, variant: str = "auto", layout: str = "dr",
                 kind: int = FILTER_SPECTRUM, fold_inv_n: bool = True) -> np.ndarray:
     """Filter as the conv kernels read it, from a natural-order spectrum or taps."""
-    src = np.ascontiguousarray(x, dtype=np.complex64)
-    assert src.size == n
+    src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
+    if src.size != n:
+        raise ValueError(f"plan_filter: {src.size} points given, n = {n}")
     out = np.empty(n, dtype=np.complex64)
     check(lib.fufft_plan_filter_f32(n, VARIANT[variant], LAYOUT[layout], kind, int(fold_inv_n),
                                     src.ctypes.data, out.ctypes.data), "fufft_plan_filter_f32")
@@ -195,11 +250,25 @@ def get_twiddles(device: int = 0) -> str:
 
 
 # ---- launches ------------------------------------------------------------------------
+# Each wrapper checks its tensors (_dev) against the sizes the call implies
+# before the library sees them; the library then checks sizes, strides,
+# enums and alignment again and returns a status, raised as FufftError.
+
+def _filt(filt, name: str, n: int, batch: int, stride: int, mid: str):
+    """Spec of a filter (or spectrum) of n points per item and stride `stride`;
+    None where the call does not read it (mid "none" with no filter given)."""
+    if filt is None and mid == "none":
+        return None
+    return (filt, name, 8 * n * _count(stride, n, batch, name) if batch else 0, "complex")
+
 
 def conv(inp, filt, out, n: int, batch: int, filt_stride: int = 0, mid: str = "mul",
-         variant: str = "v16", layout: str = "dr", stream=None) -> None:
-    check(lib.fufft_conv_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), n, batch, MID[mid],
-                             VARIANT[variant], LAYOUT[layout], _stream(stream)), "fufft_conv_f32")
+         variant: str = "auto", layout: str = "dr", stream=None) -> None:
+    nb = 8 * n * batch
+    pi, pf, po = _ptrs((inp, "inp", nb, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid),
+                       (out, "out", nb, "complex"))
+    check(lib.fufft_conv_f32(pi, pf, filt_stride, po, n, batch, MID[mid], VARIANT[variant], LAYOUT[layout],
+                             _stream(stream)), "fufft_conv_f32")
 
 
 TIMER_STRIDE = 12
@@ -214,12 +283,16 @@ def transforms_per_workgroup(n: int, variant: str = "auto") -> int:
 
 
 def conv_timed(inp, filt, out, timing, n: int, batch: int, timing_groups: int, filt_stride: int = 0,
-               mid: str = "mul", variant: str = "v16", layout: str = "dr", stream=None) -> None:
+               mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None) -> None:
     """fufft_conv_f32 with the in-kernel phase timer; timing is a device buffer
     of timing_groups * TIMER_STRIDE uint32 words (decode with decode_timing)."""
-    check(lib.fufft_conv_timed_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), n, batch, MID[mid],
-                                   VARIANT[variant], LAYOUT[layout], _ptr(timing), timing_groups,
-                                   _stream(stream)), "fufft_conv_timed_f32")
+    nb = 8 * n * batch
+    ts = (timing, "timing", 4 * TIMER_STRIDE * timing_groups, "words") if timing_groups else None
+    pi, pf, po, pt = _ptrs((inp, "inp", nb, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid),
+                           (out, "out", nb, "complex"), ts)
+    check(lib.fufft_conv_timed_f32(pi, pf, filt_stride, po, n, batch, MID[mid], VARIANT[variant],
+                                   LAYOUT[layout], pt, timing_groups, _stream(stream)),
+          "fufft_conv_timed_f32")
 
 
 def decode_timing(words: np.ndarray) -> dict:
@@ -239,60 +312,74 @@ def decode_timing(words: np.ndarray) -> dict:
     }
 
 
-def fwd(inp, spec, n: int, batch: int, variant: str = "v16", stream=None) -> None:
-    check(lib.fufft_fwd_f32(_ptr(inp), _ptr(spec), n, batch, VARIANT[variant], _stream(stream)),
-          "fufft_fwd_f32")
+def fwd(inp, spec, n: int, batch: int, variant: str = "auto", stream=None) -> None:
+    nb = 8 * n * batch
+    pi, ps = _ptrs((inp, "inp", nb, "complex"), (spec, "spec", nb, "complex"))
+    check(lib.fufft_fwd_f32(pi, ps, n, batch, VARIANT[variant], _stream(stream)), "fufft_fwd_f32")
 
 
 def apply(spec, filt, out, n: int, batch: int, spec_stride: int = 0, filt_stride: int = 0,
-          mid: str = "mul", variant: str = "v16", layout: str = "dr", stream=None) -> None:
-    check(lib.fufft_apply_f32(_ptr(spec), spec_stride, _ptr(filt), filt_stride, _ptr(out), n,
-                              batch, MID[mid], VARIANT[variant], LAYOUT[layout], _stream(stream)),
-          "fufft_apply_f32")
+          mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None) -> None:
+    ps, pf, po = _ptrs(_filt(spec, "spec", n, batch, spec_stride, "mul"),
+                       _filt(filt, "filt", n, batch, filt_stride, mid), (out, "out", 8 * n * batch, "complex"))
+    check(lib.fufft_apply_f32(ps, spec_stride, pf, filt_stride, po, n, batch, MID[mid], VARIANT[variant],
+                              LAYOUT[layout], _stream(stream)), "fufft_apply_f32")
 
 
-def conv_r2(x, y, filt, u, v, n: int, batch: int, filt_stride: int = 0, variant: str = "v16",
+def conv_r2(x, y, filt, u, v, n: int, batch: int, filt_stride: int = 0, variant: str = "auto",
             layout: str = "dr", stream=None) -> None:
-    check(lib.fufft_conv_r2_f32(_ptr(x), _ptr(y), _ptr(filt), filt_stride, _ptr(u), _ptr(v), n,
-                                batch, VARIANT[variant], LAYOUT[layout], _stream(stream)),
-          "fufft_conv_r2_f32")
+    rb = 4 * n * batch
+    px, py, pf, pu, pv = _ptrs((x, "x", rb, "real"), (y, "y", rb, "real"),
+                               _filt(filt, "filt", n, batch, filt_stride, "mul"),
+                               (u, "u", rb, "real"), (v, "v", rb, "real"))
+    check(lib.fufft_conv_r2_f32(px, py, pf, filt_stride, pu, pv, n, batch, VARIANT[variant], LAYOUT[layout],
+                                _stream(stream)), "fufft_conv_r2_f32")
 
 
 def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int = 0,
                mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None,
                block: int = BFP_BLOCK) -> None:
     """int16-BFP fused conv; one exponent per `block` points (64 .. n, a power of two)."""
-    check(lib.fufft_conv_bfp16(_ptr(qin), _ptr(ein), _ptr(filt), filt_stride, _ptr(qout),
-                               _ptr(eout), n, batch, block, MID[mid], VARIANT[variant],
+    qb, eb = 4 * n * batch, (n * batch) // block if block > 0 else 0
+    pq, pe, pf, pqo, peo = _ptrs((qin, "qin", qb, "bfp"), (ein, "ein", eb, "exp"),
+                                 _filt(filt, "filt", n, batch, filt_stride, mid),
+                                 (qout, "qout", qb, "bfp"), (eout, "eout", eb, "exp"))
+    check(lib.fufft_conv_bfp16(pq, pe, pf, filt_stride, pqo, peo, n, batch, block, MID[mid], VARIANT[variant],
                                LAYOUT[layout], _stream(stream)), "fufft_conv_bfp16")
 
 
 def c2c(inp, out, n: int, batch: int, direction: int = FORWARD, variant: str = "auto",
         stream=None) -> None:
     """Natural-order batched C2C: forward, or the unnormalised inverse."""
-    check(lib.fufft_c2c_f32(_ptr(inp), _ptr(out), n, batch, direction, VARIANT[variant],
-                            _stream(stream)), "fufft_c2c_f32")
+    nb = 8 * n * batch
+    pi, po = _ptrs((inp, "inp", nb, "complex"), (out, "out", nb, "complex"))
+    check(lib.fufft_c2c_f32(pi, po, n, batch, direction, VARIANT[variant], _stream(stream)), "fufft_c2c_f32")
 
 
-def plan_filter_device(inp, out, n: int, count: int = 1, variant: str = "v16", layout: str = "dr",
+def plan_filter_device(inp, out, n: int, count: int = 1, variant: str = "auto", layout: str = "dr",
                        kind: int = FILTER_SPECTRUM, fold_inv_n: bool = True, stream=None) -> None:
     """fufft_plan_filter_f32 on device memory, for count filters."""
-    check(lib.fufft_plan_filter_device_f32(_ptr(inp), _ptr(out), n, count, VARIANT[variant],
-                                           LAYOUT[layout], kind, int(fold_inv_n), _stream(stream)),
+    nb = 8 * n * count
+    pi, po = _ptrs((inp, "inp", nb, "complex"), (out, "out", nb, "complex"))
+    check(lib.fufft_plan_filter_device_f32(pi, po, n, count, VARIANT[variant], LAYOUT[layout], kind,
+                                           int(fold_inv_n), _stream(stream)),
           "fufft_plan_filter_device_f32")
 
 
 def plan_filter_large_device(inp, out, n: int, count: int = 1, kind: int = FILTER_SPECTRUM,
                              fold_inv_n: bool = True, stream=None) -> None:
-    check(lib.fufft_plan_filter_large_device_f32(_ptr(inp), _ptr(out), n, count, kind,
-                                                 int(fold_inv_n), _stream(stream)),
+    nb = 8 * n * count
+    pi, po = _ptrs((inp, "inp", nb, "complex"), (out, "out", nb, "complex"))
+    check(lib.fufft_plan_filter_large_device_f32(pi, po, n, count, kind, int(fold_inv_n), _stream(stream)),
           "fufft_plan_filter_large_device_f32")
 
 
 def plan_filter2d_device(inp, out, h: int, w: int, count: int = 1, kind: int = FILTER_SPECTRUM,
-                         fold_inv_n: bool = True, stream=None) -> None:
-    check(lib.fufft_plan_filter2d_device_f32(_ptr(inp), _ptr(out), h, w, count, kind,
-                                             int(fold_inv_n), _stream(stream)),
+                         fold_inv_n: bool = True, layout: str = "dr", stream=None) -> None:
+    nb = 8 * h * w * count
+    pi, po = _ptrs((inp, "inp", nb, "complex"), (out, "out", nb, "complex"))
+    check(lib.fufft_plan_filter2d_device_f32(pi, po, h, w, count, LAYOUT[layout], kind, int(fold_inv_n),
+                                             _stream(stream)),
           "fufft_plan_filter2d_device_f32")
 
 
@@ -314,8 +401,9 @@ def large_digit_order(n: int) -> np.ndarray:
 
 def plan_filter_large(x: np.ndarray, n: int, kind: int = FILTER_SPECTRUM,
                       fold_inv_n: bool = True) -> np.ndarray:
-    src = np.ascontiguousarray(x, dtype=np.complex64)
-    assert src.size == n
+    src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
+    if src.size != n:
+        raise ValueError(f"plan_filter_large: {src.size} points given, n = {n}")
     out = np.empty(n, dtype=np.complex64)
     check(lib.fufft_plan_filter_large_f32(n, kind, int(fold_inv_n), src.ctypes.data, out.ctypes.data),
           "fufft_plan_filter_large_f32")
@@ -325,11 +413,17 @@ def plan_filter_large(x: np.ndarray, n: int, kind: int = FILTER_SPECTRUM,
 def conv_large(buf, filt, n: int, batch: int, filt_stride: int = 0, mid: str = "mul",
                stream=None) -> None:
     """Four-step conv of a batch of n-point signals, in place on buf."""
-    check(lib.fufft_conv_large_f32(_ptr(buf), _ptr(filt), filt_stride, n, batch, MID[mid],
-                                   _stream(stream)), "fufft_conv_large_f32")
+    pb, pf = _ptrs((buf, "buf", 8 * n * batch, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid))
+    check(lib.fufft_conv_large_f32(pb, pf, filt_stride, n, batch, MID[mid], _stream(stream)),
+          "fufft_conv_large_f32")
 
 
 # ---- 2D ------------------------------------------------------------------------------------
+# 2D filters carry a column order (layout): "dr" is the reference's,
+# entry (r, c) = bin (rev_h(r), rev_w(c)); "lane" is this library's faster
+# order, entry (r, c) = bin (rev_h(r), rev_w(slot(c))), slot = column_order2d.
+# The planners and the launches default to "dr", so filters planned for the
+# reference work unchanged; plan and launch with layout="lane" for speed.
 
 def plan2d(h: int, w: int) -> tuple[int, int]:
     """(values per lane of the row plan, of the column plan)."""
@@ -339,7 +433,7 @@ def plan2d(h: int, w: int) -> tuple[int, int]:
 
 
 def column_order2d(h: int, w: int) -> np.ndarray:
-    """slot[c]: the row plan's digit-order slot held by column c of 2D filters and spectra."""
+    """slot[c]: the row plan's digit-order slot held by column c of "lane" 2D filters and spectra."""
     out = np.empty(w, dtype=np.int32)
     check(lib.fufft_plan2d_column_order(h, w, out.ctypes.data_as(C.POINTER(C.c_int32))),
           "fufft_plan2d_column_order")
@@ -347,37 +441,55 @@ def column_order2d(h: int, w: int) -> np.ndarray:
 
 
 def plan_filter2d(x: np.ndarray, h: int, w: int, kind: int = FILTER_SPECTRUM,
-                  fold_inv_n: bool = True) -> np.ndarray:
-    """2D filter as the column kernels read it: entry (r, c) = bin (rev_h(r), rev_w(slot(c))),
-    slot = column_order2d(h, w)."""
+                  fold_inv_n: bool = True, layout: str = "dr") -> np.ndarray:
+    """2D filter as the column kernels read it in `layout`."""
     src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
-    assert src.size == h * w
+    if src.size != h * w:
+        raise ValueError(f"plan_filter2d: {src.size} points given, h * w = {h * w}")
     out = np.empty(h * w, dtype=np.complex64)
-    check(lib.fufft_plan_filter2d_f32(h, w, kind, int(fold_inv_n), src.ctypes.data, out.ctypes.data),
-          "fufft_plan_filter2d_f32")
+    check(lib.fufft_plan_filter2d_f32(h, w, LAYOUT[layout], kind, int(fold_inv_n), src.ctypes.data,
+                                      out.ctypes.data), "fufft_plan_filter2d_f32")
     return out
 
 
 def conv2d(inp, filt, out, h: int, w: int, batch: int, filt_stride: int = 0, mid: str = "mul",
-           stream=None) -> None:
-    check(lib.fufft_conv2d_f32(_ptr(inp), _ptr(filt), filt_stride, _ptr(out), h, w, batch, MID[mid],
+           layout: str = "dr", stream=None) -> None:
+    nb = 8 * h * w * batch
+    pi, pf, po = _ptrs((inp, "inp", nb, "complex"), _filt(filt, "filt", h * w, batch, filt_stride, mid),
+                       (out, "out", nb, "complex"))
+    check(lib.fufft_conv2d_f32(pi, pf, filt_stride, po, h, w, batch, MID[mid], LAYOUT[layout],
                                _stream(stream)), "fufft_conv2d_f32")
 
 
 def conv2d_r2(x, y, filt, u, v, work, h: int, w: int, batch: int, filt_stride: int = 0,
-              stream=None) -> None:
-    check(lib.fufft_conv2d_r2_f32(_ptr(x), _ptr(y), _ptr(filt), filt_stride, _ptr(u), _ptr(v),
-                                  _ptr(work), h, w, batch, _stream(stream)), "fufft_conv2d_r2_f32")
+              layout: str = "dr", stream=None) -> None:
+    rb = 4 * h * w * batch
+    px, py, pf, pu, pv, pw = _ptrs((x, "x", rb, "real"), (y, "y", rb, "real"),
+                                   _filt(filt, "filt", h * w, batch, filt_stride, "mul"),
+                                   (u, "u", rb, "real"), (v, "v", rb, "real"), (work, "work", 2 * rb, "complex"))
+    check(lib.fufft_conv2d_r2_f32(px, py, pf, filt_stride, pu, pv, pw, h, w, batch, LAYOUT[layout],
+                                  _stream(stream)), "fufft_conv2d_r2_f32")
 
 
 def fwd2d(inp, spec, h: int, w: int, batch: int, stream=None) -> None:
-    check(lib.fufft_fwd2d_f32(_ptr(inp), _ptr(spec), h, w, batch, _stream(stream)), "fufft_fwd2d_f32")
+    nb = 8 * h * w * batch
+    pi, ps = _ptrs((inp, "inp", nb, "complex"), (spec, "spec", nb, "complex"))
+    check(lib.fufft_fwd2d_f32(pi, ps, h, w, batch, _stream(stream)), "fufft_fwd2d_f32")
 
 
 def apply2d(spec, filt, out, h: int, w: int, batch: int, spec_stride: int = 0, filt_stride: int = 0,
-            mid: str = "mul", stream=None) -> None:
-    check(lib.fufft_apply2d_f32(_ptr(spec), spec_stride, _ptr(filt), filt_stride, _ptr(out), h, w,
-                                batch, MID[mid], _stream(stream)), "fufft_apply2d_f32")
+            mid: str = "mul", layout: str = "dr", stream=None) -> None:
+    np_ = h * w
+    ps, pf, po = _ptrs(_filt(spec, "spec", np_, batch, spec_stride, "mul"),
+                       _filt(filt, "filt", np_, batch, filt_stride, mid), (out, "out", 8 * np_ * batch, "complex"))
+    check(lib.fufft_apply2d_f32(ps, spec_stride, pf, filt_stride, po, h, w, batch, MID[mid], LAYOUT[layout],
+                                _stream(stream)), "fufft_apply2d_f32")
+
+
+def stream_copy(inp, out, nbytes: int, nontemporal: bool = False, stream=None) -> None:
+    """HBM stream ceiling: copy nbytes with the conv kernels' buffer instructions."""
+    pi, po = _ptrs((inp, "inp", nbytes, "complex"), (out, "out", nbytes, "complex"))
+    check(lib.fufft_stream_f32(pi, po, nbytes, int(nontemporal), _stream(stream)), "fufft_stream_f32")
 
 
 def bfp_exponent(absmax: float) -> int:

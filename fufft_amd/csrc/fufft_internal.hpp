@@ -111,18 +111,31 @@ hipError_t launch_outer2_pass(float2* buf, int64_t n, int64_t batch, bool dit, c
 hipError_t launch_outer_pass(float2* buf, int64_t n, int64_t batch, int64_t M, bool dit,
                              const float2* tw, hipStream_t s);
 
+// ---- HBM stream ceiling (stream.hip) -------------------------------------------------
+// copy of bytes (a multiple of 16) with 16-byte buffer loads and stores;
+// nontemporal adds the NT cache policy
+hipError_t launch_stream(const void* in, void* out, uint64_t bytes, bool nontemporal, hipStream_t s);
+
 // ---- 2D column kernels (conv2d.hip) -------------------------------------------------
 struct ColParams {
    const void*   in;       // h x w complex images, rows contiguous (COL_CONV, COL_FWD)
    const void*   spec;     // 2D digit-order spectra (COL_APPLY)
    void*         out;
-   const void*   filt;     // 2D filter, slot (r, c) = bin (rev_h(r), rev_w(c))
+   const void*   filt;     // 2D filter: entry (r, c) = bin (rev_h(r), rev_w(slot(c)))
    const float2* tw;
    uint32_t      nimg;     // images in the launch
    uint32_t      fcount;   // image i uses filter (i % fcount)
    uint32_t      scount;   // image i uses spectrum (i % scount)
    int32_t       mid;
    uint32_t      w;        // row length
+   // Filter column order.  f_dr = 0: the filter's columns are in the row
+   // spectra's lane-major order, so column c reads filter column c.  f_dr = 1:
+   // the reference's order, entry (r, s) = bin (rev_h(r), rev_w(s)); column c
+   // holds row slot s = (c mod T) * V + c / T (V values per lane of the row
+   // plan, T = w / V = 2^f_tr_log, V = 2^f_vr_log) and reads filter column s.
+   uint32_t      f_dr;
+   uint32_t      f_tr_log;
+   uint32_t      f_vr_log;
 };
 enum { COL_CONV = 0, COL_FWD = 1, COL_APPLY = 2 };
 int        col_values_per_lane(int h);      // 0 if h is not a supported column length

@@ -216,8 +216,8 @@ int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n,
                                        int64_t count, int filter_kind,
                                        int fold_inv_n, void* stream);
 int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t w,
-                                   int64_t count, int filter_kind, int fold_inv_n,
-                                   void* stream);
+                                   int64_t count, int layout, int filter_kind,
+                                   int fold_inv_n, void* stream);
 
 /* ---- int16 block floating point ----------------------------------------------
  * A point is two int16 (re in the low halfword, im in the high halfword);
@@ -248,6 +248,17 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
                      int64_t batch, int64_t block, int mid, int variant, int layout,
                      void* stream);
 
+/* ---- HBM stream ceiling (measurement) ------------------------------------------------
+ * Copies `bytes` (a multiple of 16; 16-byte aligned pointers; in != out) with
+ * the buffer instructions the conv kernels use: each 256-lane workgroup moves
+ * 32 KiB, eight 16-byte loads per lane in flight before the stores.
+ * nontemporal = 1 adds the streaming (NT) cache policy to both.  No
+ * counterpart in the reference, which quotes its device's peak bandwidth
+ * (bench_fufft.cu:506): bench.py reports this copy's GB/s as the measured HBM
+ * ceiling beside MI355X's 8 TB/s, and this copy of known size scales the
+ * rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes. */
+int fufft_stream_f32(const void* in, void* out, int64_t bytes, int nontemporal, void* stream);
+
 /* ---- four-step large N -------------------------------------------------------------
  * N = 16^lout * mid with mid a single-launch size: lout radix-16 DIF levels
  * over HBM, the fused conv on contiguous mid-point chunks in place, lout DIT
@@ -270,13 +281,22 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
  * DIF, mid, columns DIT, rows DIT (fufft_conv2d, fufft.cuh:1209-1258).
  * Runs as three launches in place on out: row forward, fused column conv,
  * row inverse (7 HBM passes for an image too large for one workgroup).
- * 2D filters and spectra: entry (r, c) holds spectrum bin
- * (mixedrev_h(r), mixedrev_w(slot(c))), where slot(c) is the row plan's
- * digit-order slot that column c holds (fufft_plan2d_column_order).  The
- * reference's own order (verify_kernel.cpp:738-748) has slot(c) = c; here the
- * rows are lane-major, slot(c) = (c % T)*V + c / T with V the row plan's
- * values per lane and T = w / V, so the row kernels store and load whole
- * contiguous runs.  fufft_plan_filter2d_f32 / _device_f32 produce this order. */
+ * 2D filters: `layout` names the column order of the filter a call reads or
+ * a planner writes.
+ *   FUFFT_LAYOUT_DR    the reference's order (verify_kernel.cpp:738-748):
+ *                      entry (r, c) holds spectrum bin (mixedrev_h(r),
+ *                      mixedrev_w(c)).
+ *   FUFFT_LAYOUT_LANE  this library's order: entry (r, c) holds bin
+ *                      (mixedrev_h(r), mixedrev_w(slot(c))), where slot(c) is
+ *                      the row plan's digit-order slot that column c of the
+ *                      row spectra holds (fufft_plan2d_column_order): the rows
+ *                      are lane-major, slot(c) = (c % T)*V + c / T with V the
+ *                      row plan's values per lane and T = w / V, so the row
+ *                      kernels store and load whole contiguous runs.  A
+ *                      column tile then reads its filter columns as one
+ *                      contiguous run per row, which DR order does not give.
+ * Both layouts give bit-identical results.  2D spectra (fufft_fwd2d_f32,
+ * fufft_apply2d_f32) are always in the FUFFT_LAYOUT_LANE order. */
 /* Values per lane of the row plan (the 1D kernel at FUFFT_AUTO for length w)
  * and of the column plan (8 up to h = 512, 16 for h = 1024, 2048); the
  * per-dimension digit orders are those of fufft_digit_order with that many
@@ -286,16 +306,17 @@ int fufft_plan2d(int64_t h, int64_t w, int* v_rows, int* v_cols);
 /* slot[c] (w entries) = the row plan's digit-order slot held by column c of
  * 2D filters and spectra.  No reference counterpart (a layout of this build). */
 int fufft_plan2d_column_order(int64_t h, int64_t w, int32_t* slot);
-int fufft_plan_filter2d_f32(int64_t h, int64_t w, int filter_kind,
+int fufft_plan_filter2d_f32(int64_t h, int64_t w, int layout, int filter_kind,
                             int fold_inv_n, const float* in, float* out);
 int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride,
                      void* out, int64_t h, int64_t w, int64_t batch, int mid,
-                     void* stream);
+                     int layout, void* stream);
 /* Two real images per complex transform with a REAL filter; work is a
  * caller-owned complex scratch of h*w*batch points (the packed images). */
 int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt,
                         int64_t filt_stride, float* u, float* v, void* work,
-                        int64_t h, int64_t w, int64_t batch, void* stream);
+                        int64_t h, int64_t w, int64_t batch, int layout,
+                        void* stream);
 /* split 2D path: fwd = rows DIF then columns DIF into spec (the 2D order above);
  * apply = spec mid filt, columns DIT, rows DIT into out.  spec_stride 0 shares
  * one spectrum across the batch. */
@@ -303,7 +324,7 @@ int fufft_fwd2d_f32(const void* in, void* spec, int64_t h, int64_t w,
                     int64_t batch, void* stream);
 int fufft_apply2d_f32(const void* spec, int64_t spec_stride, const void* filt,
                       int64_t filt_stride, void* out, int64_t h, int64_t w,
-                      int64_t batch, int mid, void* stream);
+                      int64_t batch, int mid, int layout, void* stream);
 
 #ifdef __cplusplus
 }

@@ -131,10 +131,14 @@ inline int plan_filter_large_device(const void* natural, void* planned, int64_t 
    return fufft_plan_filter_large_device_f32(natural, planned, n, count, kind, fold_inv_n ? 1 : 0, stream);
 }
 
+// 2D filters default to the reference's column order (verify_kernel.cpp:738-748);
+// FUFFT_LAYOUT_LANE is this library's faster order (fufft.h, 2D section)
 inline int plan_filter2d_device(const void* natural, void* planned, int64_t h, int64_t w, int64_t count = 1,
-                                void* stream = nullptr, int kind = FUFFT_FILTER_TAPS, bool fold_inv_n = true)
+                                void* stream = nullptr, int kind = FUFFT_FILTER_TAPS, bool fold_inv_n = true,
+                                int layout = FUFFT_LAYOUT_DR)
 {
-   return fufft_plan_filter2d_device_f32(natural, planned, h, w, count, kind, fold_inv_n ? 1 : 0, stream);
+   return fufft_plan_filter2d_device_f32(natural, planned, h, w, count, layout, kind, fold_inv_n ? 1 : 0,
+                                         stream);
 }
 
 // ---- four-step (run_large, bench_fufft.cu:357-492) ----------------------------------------
@@ -150,15 +154,16 @@ inline int conv_large(void* buf, const void* filt, int64_t n, int64_t batch, voi
 
 template<class Mid = MidMultiply>
 inline int conv2d(const void* in, const void* filt, void* out, int64_t h, int64_t w, int64_t batch,
-                  void* stream = nullptr, int64_t filt_stride = 0)
+                  void* stream = nullptr, int64_t filt_stride = 0, int layout = FUFFT_LAYOUT_DR)
 {
-   return fufft_conv2d_f32(in, filt, filt_stride, out, h, w, batch, Mid::id, stream);
+   return fufft_conv2d_f32(in, filt, filt_stride, out, h, w, batch, Mid::id, layout, stream);
 }
 
 inline int conv2d_r2(const float* x, const float* y, const void* filt, float* u, float* v, void* work,
-                     int64_t h, int64_t w, int64_t batch, void* stream = nullptr, int64_t filt_stride = 0)
+                     int64_t h, int64_t w, int64_t batch, void* stream = nullptr, int64_t filt_stride = 0,
+                     int layout = FUFFT_LAYOUT_DR)
 {
-   return fufft_conv2d_r2_f32(x, y, filt, filt_stride, u, v, work, h, w, batch, stream);
+   return fufft_conv2d_r2_f32(x, y, filt, filt_stride, u, v, work, h, w, batch, layout, stream);
 }
 
 inline int fwd2d(const void* in, void* spec, int64_t h, int64_t w, int64_t batch, void* stream = nullptr)
@@ -168,9 +173,10 @@ inline int fwd2d(const void* in, void* spec, int64_t h, int64_t w, int64_t batch
 
 template<class Mid = MidMultiply>
 inline int apply2d(const void* spec, const void* filt, void* out, int64_t h, int64_t w, int64_t batch,
-                   void* stream = nullptr, int64_t spec_stride = 0, int64_t filt_stride = 0)
+                   void* stream = nullptr, int64_t spec_stride = 0, int64_t filt_stride = 0,
+                   int layout = FUFFT_LAYOUT_DR)
 {
-   return fufft_apply2d_f32(spec, spec_stride, filt, filt_stride, out, h, w, batch, Mid::id, stream);
+   return fufft_apply2d_f32(spec, spec_stride, filt, filt_stride, out, h, w, batch, Mid::id, layout, stream);
 }
 
 }  // namespace fufft

@@ -81,6 +81,7 @@ def load_ref() -> C.CDLL | None:
     R.ref_vk_conv_r2.argtypes = [_i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32]
     R.ref_vk_bfp_quantize.argtypes = [_vp, _i32, _vp]
     R.ref_vk_bfp_quantize.restype = C.c_float
+    R.ref_vk_v16_bfp.argtypes = [_i32, _i32, _i32, _vp, _vp, _vp, C.c_float, _vp, _vp, _i32]
     for name in ("ref_vk_main", "ref_mixed_main", "ref_inplace_main", "ref_fufft_main"):
         getattr(R, name).argtypes = []
     return R

@@ -141,4 +141,26 @@ float ref_vk_bfp_quantize(const float* x, int N, int16_t* q)
    return b.scale;
 }
 
+// verify_kernel.cpp:1111-1135 (kernel_v16_bfp, the fufft_pipeline_v16_bfp
+// dataflow): batch transforms of N points, each input as int16 pairs with its
+// own fp32 scale, one shared filter (int16 pairs, one scale); writes the
+// output pairs and scales
+void ref_vk_v16_bfp(int N, int lead, int nrv, const int16_t* aq, const float* ascale,
+                    const int16_t* bq, float bscale, int16_t* oq, float* oscale, int batch)
+{
+   BfpQuant a, b, o;
+   a.qre.resize(N); a.qim.resize(N); b.qre.resize(N); b.qim.resize(N);
+   for(int i = 0; i < N; i++) { b.qre[i] = bq[2 * i]; b.qim[i] = bq[2 * i + 1]; }
+   b.scale = bscale;
+   for(int t = 0; t < batch; t++) {
+      const int16_t* at = aq + (size_t)2 * N * t;
+      for(int i = 0; i < N; i++) { a.qre[i] = at[2 * i]; a.qim[i] = at[2 * i + 1]; }
+      a.scale = ascale[t];
+      kernel_v16_bfp(N, lead, nrv, CPP_OPT, a, b, o);
+      int16_t* ot = oq + (size_t)2 * N * t;
+      for(int i = 0; i < N; i++) { ot[2 * i] = o.qre[i]; ot[2 * i + 1] = o.qim[i]; }
+      oscale[t] = o.scale;
+   }
+}
+
 }  // extern "C"

@@ -62,3 +62,11 @@ def cols_to_dr(x, h, w):
     out = np.empty_like(a)
     out[:, :, slot] = a
     return out.reshape(np.shape(x))
+
+
+def filt2d_dr(x, h, w, layout):
+    """A 2D filter or spectrum planned in `layout` ("dr": the reference's
+    order already; "lane": the library's column order) in the reference's
+    order, slot (r, c) = bin (mixedrev_h(r), mixedrev_w(c)), which the oracle
+    reads."""
+    return np.asarray(x) if layout == "dr" else cols_to_dr(x, h, w)

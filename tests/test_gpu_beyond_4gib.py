@@ -116,7 +116,7 @@ def test_conv2d_per_image_filters_beyond_4gib(dev):
     out = torch.empty_like(x)
     idx = [0, batch // 2, batch - 1]
     print(f"case conv2d beyond 4 GiB {h}x{w} batch={batch} samples={idx}", flush=True)
-    ff.conv2d(x, f, out, h, w, batch=batch, filt_stride=np_img)
+    ff.conv2d(x, f, out, h, w, batch=batch, filt_stride=np_img, layout="lane")
     torch.cuda.synchronize()
     ti = torch.tensor(idx, device=dev)
     a_s = x.view(batch, np_img)[ti].cpu().numpy()

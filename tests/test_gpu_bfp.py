@@ -109,10 +109,10 @@ def test_bfp_block_rejects_bad_lengths(dev):
     import torch
     n = 4096
     d = torch.zeros(2 * n, dtype=torch.int16, device=dev)
-    de = torch.zeros(n // 64, dtype=torch.int8, device=dev)
+    de = torch.zeros(n // 32, dtype=torch.int8, device=dev)     # room for 32-point blocks: the library decides
     f = torch.zeros(n, dtype=torch.complex64, device=dev)
     for block in (32, 96, 2 * n):
-        with pytest.raises(RuntimeError):
+        with pytest.raises(ff.FufftError):
             ff.conv_bfp16(d, de, f, d, de, n=n, batch=1, block=block)
 
 

@@ -10,7 +10,7 @@ the device-planned filter within 2e-6 of fp64.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, cols_to_dr, crandn, cuniform
+from conftest import bits_equal, cols_to_dr, crandn, cuniform, filt2d_dr
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -176,25 +176,28 @@ def test_plan_device_large(dev, n, rng):
     assert O.rel_l2(got_t, host_t) <= 1e-6
 
 
+@pytest.mark.parametrize("layout", ["lane", "dr"])
 @pytest.mark.parametrize("h,w", [(256, 256), (512, 512), (1024, 512)])
-def test_plan_device_2d(dev, h, w, rng):
+def test_plan_device_2d(dev, h, w, layout, rng):
     import torch
     import fufft_amd as ff
     count = 2
     taps = cuniform(rng, (count, h, w))
     spec = np.fft.fft2(taps.astype(np.complex128)).astype(np.complex64)
-    print(f"case plan2d {h}x{w}", flush=True)
+    print(f"case plan2d {h}x{w} layout={layout}", flush=True)
     dt, ds = to_dev(taps, dev), to_dev(spec, dev)
     out_t, out_s = torch.empty_like(dt), torch.empty_like(ds)
-    ff.plan_filter2d_device(dt, out_t, h, w, count, kind=ff.FILTER_TAPS)
-    ff.plan_filter2d_device(ds, out_s, h, w, count, kind=ff.FILTER_SPECTRUM)
+    ff.plan_filter2d_device(dt, out_t, h, w, count, kind=ff.FILTER_TAPS, layout=layout)
+    ff.plan_filter2d_device(ds, out_s, h, w, count, kind=ff.FILTER_SPECTRUM, layout=layout)
     got_t, got_s = from_dev(out_t), from_dev(out_s)
-    host_s = np.stack([ff.plan_filter2d(spec[i], h, w, kind=ff.FILTER_SPECTRUM) for i in range(count)])
+    host_s = np.stack([ff.plan_filter2d(spec[i], h, w, kind=ff.FILTER_SPECTRUM, layout=layout)
+                       for i in range(count)])
     assert bits_equal(got_s.reshape(count, -1), host_s)
     vr, vc = ff.plan2d(h, w)
     want_t = scaled(O.fwd2d(taps, h, w, O.kernel_plan(h, vc), O.kernel_plan(w, vr)), 1.0 / (h * w))
-    assert bits_equal(cols_to_dr(got_t.reshape(-1), h, w), want_t)
-    host_t = np.stack([ff.plan_filter2d(taps[i], h, w, kind=ff.FILTER_TAPS) for i in range(count)])
+    assert bits_equal(filt2d_dr(got_t.reshape(-1), h, w, layout), want_t)
+    host_t = np.stack([ff.plan_filter2d(taps[i], h, w, kind=ff.FILTER_TAPS, layout=layout)
+                       for i in range(count)])
     assert O.rel_l2(got_t.reshape(count, -1), host_t) <= 1e-6
 
 

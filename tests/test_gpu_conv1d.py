@@ -119,8 +119,8 @@ def test_split_broadcast_one_spectrum_many_filters(dev, rng):
     da, df = to_dev(a, dev), to_dev(fdr, dev)
     dspec = torch.empty_like(da)
     dout = torch.empty((nf * n,), dtype=torch.complex64, device=dev)
-    ff.fwd(da, dspec, n=n, batch=1)
-    ff.apply(dspec, df, dout, n=n, batch=nf, spec_stride=0, filt_stride=n)
+    ff.fwd(da, dspec, n=n, batch=1, variant="v16")
+    ff.apply(dspec, df, dout, n=n, batch=nf, spec_stride=0, filt_stride=n, variant="v16")
     got = from_dev(dout)
     spec1 = O.fwd(a, n, plan)
     assert bits_equal(got, O.apply(spec1, fdr, n, nf, plan, spec_stride=0, filt_stride=n))
@@ -166,14 +166,14 @@ def test_full_size_properties(dev, rng):
     df = to_dev(spec[O.mixedrev(plan)], dev)
     dout = torch.empty_like(da)
     print("case full-size n=4096 batch=32768", flush=True)
-    ff.conv(da, df, dout, n=n, batch=batch)
+    ff.conv(da, df, dout, n=n, batch=batch, variant="v16")
     # sample 64 signals spread over the batch: bit-identical to the oracle
     idx = np.linspace(0, batch - 1, 64).astype(np.int64)
     a_s = da.view(batch, n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
     got_s = dout.view(batch, n)[torch.from_numpy(idx).to(dev)].cpu().numpy()
     assert bits_equal(got_s.reshape(-1), O.conv(a_s, spec[O.mixedrev(plan)], n, plan))
     # round trip with no mid operation returns N * input for every signal
-    ff.conv(da, df, dout, n=n, batch=batch, mid="none")
+    ff.conv(da, df, dout, n=n, batch=batch, mid="none", variant="v16")
     err = torch.linalg.vector_norm(dout / n - da) / torch.linalg.vector_norm(da)
     assert float(err) < 1e-6
 

@@ -92,6 +92,9 @@ def test_large_rejects_bad_args(dev):
     buf = torch.zeros(8192 * 2, dtype=torch.complex64, device=dev)
     with pytest.raises(ff.FufftError):
         ff.conv_large(buf, buf, n=4096, batch=1)            # below the four-step range
-    with pytest.raises(ff.FufftError):
+    with pytest.raises(ValueError):                         # the binding rejects the stride
         ff.conv_large(buf, buf, n=8192, batch=1, filt_stride=5)
+    with pytest.raises(ff.FufftError):                      # and so does the library
+        ff.check(ff.lib.fufft_conv_large_f32(buf.data_ptr(), buf.data_ptr(), 5, 8192, 1, 0, None),
+                 "fufft_conv_large_f32")
     ff.conv_large(buf, buf, n=8192, batch=0)                # empty batch is a no-op

@@ -149,23 +149,48 @@ def test_fourstep_equals_libm_oracle(ref_tw, n, rng):
     assert O.rel_l2(got, O.conv_spec_f64(a, spec, n)) <= TOL_F32
 
 
-@pytest.mark.parametrize("h,w", [(256, 512), (512, 512)])
-def test_conv2d_equals_libm_oracle(ref_tw, h, w, rng):
+def rev8(x, digits):
+    """base-8 digit reversal (the reference's rev8, verify_kernel.cpp:738-743)"""
+    r = 0
+    for _ in range(digits):
+        r = r * 8 + (x & 7)
+        x >>= 3
+    return r
+
+
+@pytest.mark.parametrize("layout", ["dr", "lane"])
+@pytest.mark.parametrize("h,w", [(512, 512), (512, 4096)])
+def test_conv2d_equals_libm_oracle(ref_tw, h, w, layout, rng):
+    """The reference's 2D test setup (test_2d, verify_kernel.cpp:724-748):
+    signal and filter U[-1, 1), the filter times 1/(h w), and the filter
+    handed over in its order, slot (r, c) = natural bin (rev8(r), rev8(c)).
+    Fed as is (layout "dr") or moved to the library's column order ("lane"),
+    the GPU equals the LIBM-mode oracle (pinned bit for bit to the compiled
+    kernel_conv2d) bit for bit."""
     import torch
     import fufft_amd as ff
     dev = ref_tw
     vr, vc = ff.plan2d(h, w)
     ph, pw = O.kernel_plan(h, vc), O.kernel_plan(w, vr)
-    # at these shapes the GPU's row and column plans are the reference's
-    # radix-8 plans (kernel_conv2d runs radix 8 in both dimensions)
+    # at these shapes (powers of 8) the GPU's row and column plans are the
+    # reference's radix-8 plans (kernel_conv2d runs radix 8 in both dimensions)
     assert (ph.radices, pw.radices) == (O.ref_plan(h, 8).radices, O.ref_plan(w, 8).radices)
+    sh, sw = len(ph.radices), len(pw.radices)
     a = cuniform(rng, (2, h, w))
-    filt = ff.plan_filter2d(cuniform(rng, h * w), h, w)
-    print(f"case reftw conv2d {h}x{w}", flush=True)
+    b = cuniform(rng, (h, w)) * np.float32(1.0 / (h * w))
+    b_dr = np.ascontiguousarray(b[np.ix_([rev8(r, sh) for r in range(h)],
+                                         [rev8(c, sw) for c in range(w)])]).reshape(-1)
+    if layout == "dr":
+        filt = b_dr
+    else:
+        slot = ff.column_order2d(h, w)
+        filt = np.ascontiguousarray(b_dr.reshape(h, w)[:, slot]).reshape(-1)
+        assert bits_equal(cols_to_dr(filt, h, w), b_dr)
+    print(f"case reftw conv2d {h}x{w} layout={layout}", flush=True)
     da = to_dev(a, dev)
     out = torch.empty_like(da)
-    ff.conv2d(da, to_dev(filt, dev), out, h, w, batch=2)
-    assert bits_equal(host(out), O.conv2d(a, cols_to_dr(filt, h, w), h, w, ph, pw, tw=O.TW_LIBM))
+    ff.conv2d(da, to_dev(filt, dev), out, h, w, batch=2, layout=layout)
+    assert bits_equal(host(out), O.conv2d(a, b_dr, h, w, ph, pw, tw=O.TW_LIBM))
 
 
 @pytest.mark.parametrize("n", [512, 4096])

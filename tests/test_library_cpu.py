@@ -90,7 +90,11 @@ def test_filter_planning_large_and_2d(rng):
     vr, vc = ff.plan2d(h, w)
     S = np.fft.fft2(taps2.reshape(h, w).astype(np.complex128)) / (h * w)
     rh, rw = O.mixedrev(O.kernel_plan(h, vc)), O.mixedrev(O.kernel_plan(w, vr))
-    got2 = ff.plan_filter2d(taps2, h, w, kind=ff.FILTER_TAPS)
+    got2 = ff.plan_filter2d(taps2, h, w, kind=ff.FILTER_TAPS, layout="lane")
+    # the reference's order: slot (r, c) = bin (rev_h(r), rev_w(c))
+    got2_dr = ff.plan_filter2d(taps2, h, w, kind=ff.FILTER_TAPS, layout="dr")
+    want2_dr = S[np.ix_(rh, rw)].reshape(-1)
+    assert np.max(np.abs(got2_dr - want2_dr)) <= 2e-7 * np.max(np.abs(want2_dr))
     # columns in the library's order: column c holds row slot (c % T) * vr + c // T
     slot = ff.column_order2d(h, w)
     T = w // vr
@@ -175,10 +179,16 @@ def test_status_codes_without_gpu_calls():
         assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 4096, 1, block, 0, 1, 0, None) == ff.ERR_INVALID
     assert L.fufft_conv_large_f32(fake, fake, 0, 4096, 1, 0, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_conv_large_f32(fake, fake, 3, 32768, 1, 0, None) == ff.ERR_INVALID
-    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 128, 512, 1, 0, None) == ff.ERR_UNSUPPORTED
-    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 100, 1, 0, None) == ff.ERR_UNSUPPORTED
-    assert L.fufft_conv2d_f32(fake, fake, 5, fake, 512, 512, 1, 0, None) == ff.ERR_INVALID
-    assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake, 512, 512, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 128, 512, 1, 0, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 100, 1, 0, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv2d_f32(fake, fake, 5, fake, 512, 512, 1, 0, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 512, 1, 0, 7, None) == ff.ERR_INVALID
+    assert L.fufft_conv2d_r2_f32(fake, fake, fake, 0, fake, fake, fake, 512, 512, 1, 7, None) == ff.ERR_INVALID
+    assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake, 512, 512, 2, 0, 0, None) == ff.ERR_INVALID
+    assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake + 16, 512, 512, 2, 0, 7, None) == ff.ERR_INVALID
+    # 1D apply: a spectrum shared by the batch must not be the output
+    assert L.fufft_apply_f32(fake, 0, fake, 0, fake, 4096, 2, 0, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_plan_filter2d_f32(512, 512, 7, 0, 1, fake, fake) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(None, 64, 64, None, None) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(fake, 65, 64, fake, fake) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(fake, 64, 0, fake, fake) == ff.ERR_INVALID
@@ -188,7 +198,8 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_plan_filter_device_f32(fake, fake, 4096, 1, 2, 0, 0, 1, None) == ff.ERR_INVALID
     assert L.fufft_plan_filter_device_f32(fake, fake + 16, 4096, 1, 2, 0, 5, 1, None) == ff.ERR_INVALID
     assert L.fufft_plan_filter_large_device_f32(fake, fake, 4096, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
-    assert L.fufft_plan_filter2d_device_f32(fake, fake, 512, 100, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter2d_device_f32(fake, fake, 512, 100, 1, 0, 1, 1, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter2d_device_f32(fake, fake + 16, 512, 512, 1, 7, 1, 1, None) == ff.ERR_INVALID
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("misaligned pointer")
 
 
