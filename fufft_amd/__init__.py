@@ -24,7 +24,8 @@ except ImportError:  # pragma: no cover - torch is part of the image
 
 _LIB_PATH = Path(__file__).resolve().parent / "libfufft_amd.so"
 
-OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN = 0, -1, -2, -3, -4
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
+SCRATCH_BYTES = 64 << 20          # FUFFT_SCRATCH_BYTES
 MID = {"mul": 0, "conj": 1, "none": 2}
 VARIANT = {"v16": 0, "r8": 1, "auto": 2}
 LAYOUT = {"dr": 0, "lane": 1}
@@ -83,6 +84,7 @@ def _load() -> C.CDLL:
         "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, i32, vp, vp], i32),
         "fufft_conv2d_f32": ([vp, vp, i64, vp, i64, i64, i64, i32, i32, vp], i32),
         "fufft_conv2d_r2_f32": ([vp, vp, vp, i64, vp, vp, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_conv2d_r2_noalloc_f32": ([vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, vp], i32),
         "fufft_fwd2d_f32": ([vp, vp, i64, i64, i64, vp], i32),
         "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, i32, vp], i32),
         "fufft_c2c_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
@@ -469,6 +471,18 @@ def conv2d_r2(x, y, filt, u, v, work, h: int, w: int, batch: int, filt_stride: i
                                    (u, "u", rb, "real"), (v, "v", rb, "real"), (work, "work", 2 * rb, "complex"))
     check(lib.fufft_conv2d_r2_f32(px, py, pf, filt_stride, pu, pv, pw, h, w, batch, LAYOUT[layout],
                                   _stream(stream)), "fufft_conv2d_r2_f32")
+
+
+def conv2d_r2_noalloc(x, y, filt, u, v, h: int, w: int, batch: int, filt_stride: int = 0,
+                      layout: str = "dr", stream=None) -> None:
+    """conv2d_r2 without a workspace: the library's static scratch holds the
+    packed images (SCRATCH_BYTES per GPU; calls that overlap on one GPU race)."""
+    rb = 4 * h * w * batch
+    px, py, pf, pu, pv = _ptrs((x, "x", rb, "real"), (y, "y", rb, "real"),
+                               _filt(filt, "filt", h * w, batch, filt_stride, "mul"),
+                               (u, "u", rb, "real"), (v, "v", rb, "real"))
+    check(lib.fufft_conv2d_r2_noalloc_f32(px, py, pf, filt_stride, pu, pv, h, w, batch, LAYOUT[layout],
+                                          _stream(stream)), "fufft_conv2d_r2_noalloc_f32")
 
 
 def fwd2d(inp, spec, h: int, w: int, batch: int, stream=None) -> None:

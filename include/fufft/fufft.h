@@ -39,6 +39,8 @@ extern "C" {
 #define FUFFT_ERR_UNSUPPORTED  -2   /* size / variant combination not built    */
 #define FUFFT_ERR_HIP          -3   /* HIP runtime error (init, launch)        */
 #define FUFFT_ERR_ALIGN        -4   /* misaligned pointer (16 B fp32, 4 B BFP)  */
+#define FUFFT_ERR_SCRATCH      -5   /* one image larger than the static scratch
+                                       (fufft_conv2d_r2_noalloc_f32)            */
 
 /* ---- enums ----------------------------------------------------------------- */
 /* mid operation between forward and inverse (Mid policies, fufft.cuh:616-650) */
@@ -317,6 +319,24 @@ int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt,
                         int64_t filt_stride, float* u, float* v, void* work,
                         int64_t h, int64_t w, int64_t batch, int layout,
                         void* stream);
+/* Two-for-one 2D conv without a workspace.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results (bit for bit) as fufft_conv2d_r2_f32 without `work`:
+ * the packed images go through a static device array of FUFFT_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends, in
+ * sub-batches of at most FUFFT_SCRATCH_BYTES / (8*h*w) images.  An image
+ * larger than the array (8*h*w > FUFFT_SCRATCH_BYTES, e.g. 2048 x 8192)
+ * returns FUFFT_ERR_SCRATCH.  The call allocates nothing.  Every call on one
+ * GPU uses that GPU's one array, which keeps the last call's contents (each
+ * call writes every element it reads): calls that overlap on one GPU (two
+ * streams, two host threads) race on it and must be serialised.  Call
+ * fufft_init(device) first to keep the one-time twiddle upload out of the
+ * call and out of graph capture. */
+#define FUFFT_SCRATCH_BYTES (64ll << 20)
+int fufft_conv2d_r2_noalloc_f32(const float* x, const float* y, const void* filt,
+                                int64_t filt_stride, float* u, float* v, int64_t h,
+                                int64_t w, int64_t batch, int layout, void* stream);
 /* split 2D path: fwd = rows DIF then columns DIF into spec (the 2D order above);
  * apply = spec mid filt, columns DIT, rows DIT into out.  spec_stride 0 shares
  * one spectrum across the batch. */

@@ -189,6 +189,9 @@ def test_status_codes_without_gpu_calls():
     # 1D apply: a spectrum shared by the batch must not be the output
     assert L.fufft_apply_f32(fake, 0, fake, 0, fake, 4096, 2, 0, 2, 0, None) == ff.ERR_INVALID
     assert L.fufft_plan_filter2d_f32(512, 512, 7, 0, 1, fake, fake) == ff.ERR_INVALID
+    # the workspace-free 2D call refuses an image larger than its static scratch before any GPU call
+    assert L.fufft_conv2d_r2_noalloc_f32(fake, fake, fake, 0, fake, fake, 2048, 8192, 1, 1, None) == ff.ERR_SCRATCH
+    assert L.fufft_conv2d_r2_noalloc_f32(fake, fake, fake, 0, fake, fake, 512, 512, 1, 7, None) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(None, 64, 64, None, None) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(fake, 65, 64, fake, fake) == ff.ERR_INVALID
     assert L.fufft_bfp_quantize(fake, 64, 0, fake, fake) == ff.ERR_INVALID
@@ -201,6 +204,7 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_plan_filter2d_device_f32(fake, fake, 512, 100, 1, 0, 1, 1, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_plan_filter2d_device_f32(fake, fake + 16, 512, 512, 1, 7, 1, 1, None) == ff.ERR_INVALID
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("misaligned pointer")
+    assert "scratch" in L.fufft_status_string(ff.ERR_SCRATCH).decode()
 
 
 def test_cpp_mirror_header_builds_and_runs(tmp_path):
