@@ -174,7 +174,7 @@ bfp_kernel(const BfpParams p)
    float2 r[V];
 #pragma unroll
    for(int q = 0; q < V; q++) {
-      const uint32_t word = qb.ldu((uint32_t)L * 4u, q * T * 4);
+      const uint32_t word = qb.ldu<POL_NT>((uint32_t)L * 4u, q * T * 4);
       int e;
       if constexpr(BIG) {
          e = __builtin_amdgcn_readlane(ein_lane, q);
@@ -223,7 +223,7 @@ bfp_kernel(const BfpParams p)
    auto store = [&](int q, float yr, float yi) {
       const uint32_t word = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, yi),
                                                   __builtin_bit_cast(uint32_t, yr), 0x05040100u);
-      ob.stu(word, (uint32_t)L * 4u, q * T * 4);
+      ob.stu<POL_NT>(word, (uint32_t)L * 4u, q * T * 4);
    };
    // Adding 1.5 * 2^23 rounds |v| < 2^22 to the nearest integer, ties to even
    // (= rint), and leaves it in the low mantissa bits.  With the exact scale

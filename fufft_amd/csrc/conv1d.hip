@@ -46,6 +46,10 @@ conv1d_kernel(const Conv1dParams p)
    constexpr bool C2C_INV   = KIND == K_C2C_INV;
    constexpr bool PLAN      = KIND == K_PLAN_TAPS;
    constexpr bool TIMED     = KIND == K_CONV_TIMED;
+   // the signal read and the result written once per launch stream past the
+   // caches in the single-launch conv and C2C; the four-step middle, the split
+   // and 2D row kernels keep the default policy
+   constexpr int  IO_POL    = (KIND == K_CONV || TIMED || C2C_FWD || C2C_INV) ? POL_NT : POL_DEFAULT;
    constexpr int  EL_IN     = REAL_IN ? 4 : 8;
    constexpr int  EL_OUT    = REAL_OUT ? 4 : 8;
 
@@ -77,7 +81,7 @@ conv1d_kernel(const Conv1dParams p)
    Twiddles<PL> tw;
    tw.load(p.tw, L);
    // both halves in this launch: the forward's last twiddled chain serves the inverse
-   constexpr int KEEP_F = (KIND == K_CONV || KIND == K_CONV_R2 || TIMED) ? KEEP_STORE : KEEP_NONE;
+   constexpr int KEEP_F = (KIND == K_CONV || KIND == K_CONV_MID || KIND == K_CONV_R2 || TIMED) ? KEEP_STORE : KEEP_NONE;
    constexpr int KEEP_I = KEEP_F == KEEP_STORE ? KEEP_USE : KEEP_NONE;
    KeptChain<PL> kc;
    float2 r[V];
@@ -111,7 +115,7 @@ conv1d_kernel(const Conv1dParams p)
       } else {
          const Buf xb(static_cast<const char*>(p.in0) + wb, WB);
 #pragma unroll
-         for(int q = 0; q < V; q++) r[q] = xb.ld2(lane_pos * 8u, q * T * 8);
+         for(int q = 0; q < V; q++) r[q] = xb.ld2<IO_POL>(lane_pos * 8u, q * T * 8);
       }
       stamp(1);
       if constexpr(C2C_INV) natural_to_digit<PL, LD, LANES, true>(r, A, L);
@@ -123,7 +127,7 @@ conv1d_kernel(const Conv1dParams p)
       digit_to_natural<PL, LD, LANES>(r, A, L);
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
 #pragma unroll
-      for(int q = 0; q < V; q++) ob.st2(r[q], lane_pos * 8u, q * T * 8);
+      for(int q = 0; q < V; q++) ob.st2<IO_POL>(r[q], lane_pos * 8u, q * T * 8);
       return;
    } else if constexpr(PLAN) {
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
@@ -179,7 +183,7 @@ conv1d_kernel(const Conv1dParams p)
       } else {
          const Buf ob(static_cast<char*>(p.out0) + wb, WB);
 #pragma unroll
-         for(int q = 0; q < V; q++) ob.st2(r[q], lane_pos * 8u, q * T * 8);
+         for(int q = 0; q < V; q++) ob.st2<IO_POL>(r[q], lane_pos * 8u, q * T * 8);
       }
       if constexpr(TIMED) {
          stamp(5);
@@ -234,6 +238,10 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
 {
    switch(kind) {
       case K_CONV:    return launch_mid<N, V, LAYOUT, K_CONV>(p, s);
+      case K_CONV_MID:
+         // the four-step middle runs radix 8 at N = 512 .. 4096 only
+         if constexpr(V == 8 && N <= 4096) return launch_mid<N, V, LAYOUT, K_CONV_MID>(p, s);
+         else                              return hipErrorInvalidValue;
       case K_CONV_R2: return launch_one<N, V, LAYOUT, K_CONV_R2, MID_MUL>(p, s);
       case K_FWD:     return launch_one<N, V, LAYOUT, K_FWD, MID_NONE>(p, s);
       case K_APPLY:   return launch_mid<N, V, LAYOUT, K_APPLY>(p, s);

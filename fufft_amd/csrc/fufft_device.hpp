@@ -249,6 +249,14 @@ __device__ __forceinline__ void twiddle_group(float2 (&r)[NR], float2 w1)
 // offset, and per-tap offsets ride in the scalar offset field, so a lane keeps
 // one VGPR of addressing instead of a 64-bit pointer per tap.  Accesses beyond
 // num_records bytes read zero and drop writes.
+// cache policy of a buffer access on gfx950: NT (bit 1) streams data that is
+// touched once -- a signal read and a result written -- past the caches, so
+// they stay with data that is reused (the filter, twiddles, LDS spills).
+// Measured on the 1D conv and BFP kernels at every size: +2 to +3.5%, and on
+// a plain copy 5.5 -> 6.2 TB/s.  The four-step middle does not use it: its
+// data is read again by the next launch from the last-level cache.
+enum { POL_DEFAULT = 0, POL_NT = 2 };
+
 struct Buf {
    __amdgpu_buffer_rsrc_t r;
    // dword 3 of the resource: 32-bit data format, as gfx9 untyped access expects
@@ -261,17 +269,19 @@ struct Buf {
    {
       return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
    }
+   template<int POL = POL_DEFAULT>
    __device__ __forceinline__ float2 ld2(uint32_t voff, uint32_t soff) const
    {
-      return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+      return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL));
    }
    __device__ __forceinline__ float4 ld4(uint32_t voff, uint32_t soff) const
    {
       return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
    }
+   template<int POL = POL_DEFAULT>
    __device__ __forceinline__ uint32_t ldu(uint32_t voff, uint32_t soff) const
    {
-      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+      return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, POL);
    }
    __device__ __forceinline__ int ldi8(uint32_t voff, uint32_t soff) const
    {
@@ -281,19 +291,21 @@ struct Buf {
    {
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, voff, soff, 0);
    }
+   template<int POL = POL_DEFAULT>
    __device__ __forceinline__ void st2(float2 v, uint32_t voff, uint32_t soff) const
    {
       typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), r, voff, soff, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, v), r, voff, soff, POL);
    }
    __device__ __forceinline__ void st4(float4 v, uint32_t voff, uint32_t soff) const
    {
       typedef uint32_t u4 __attribute__((ext_vector_type(4)));
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, v), r, voff, soff, 0);
    }
+   template<int POL = POL_DEFAULT>
    __device__ __forceinline__ void stu(uint32_t v, uint32_t voff, uint32_t soff) const
    {
-      __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(v, r, voff, soff, POL);
    }
 };
 

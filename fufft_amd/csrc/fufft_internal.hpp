@@ -35,8 +35,11 @@ inline hipError_t ensure_dynamic_lds(const void* kernel, size_t bytes, std::atom
 // layout fl (digit order or lane-major).
 // K_CONV_TIMED: K_CONV with the phase timer (a timestamp after the load, the
 // forward DIF, the mid operation, the inverse DIT and the store).
+// K_CONV_MID: K_CONV as the four-step middle (radix 8, N <= 4096), whose
+// chunks the next launch reads again: default cache policy, where K_CONV
+// streams its signal and result past the caches (POL_NT).
 enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5,
-       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9 };
+       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9, K_CONV_MID = 10 };
 
 // phase timer record of one workgroup (K_CONV_TIMED), TIMER_STRIDE words:
 // [0] HW_ID, [1] XCC_ID, [2] marks, [3] s_memrealtime ticks (100 MHz) from

@@ -41,7 +41,7 @@ LLVM = Path("/opt/rocm/llvm/bin")
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 
 KINDS = {0: "conv", 1: "conv_r2", 2: "fwd", 3: "apply", 4: "fwd_r2", 5: "apply_r2",
-         6: "c2c_fwd", 7: "c2c_inv", 8: "plan_taps", 9: "conv_timed"}
+         6: "c2c_fwd", 7: "c2c_inv", 8: "plan_taps", 9: "conv_timed", 10: "conv_mid"}
 MIDS = {0: "mul", 1: "conj", 2: "none"}
 LAYOUTS = {0: "xor", 1: "pad", 2: "xchg"}
 
@@ -186,8 +186,10 @@ def plan(n: int, v: int) -> list:
 def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
     """Per-lane fp32 arithmetic and LDS accesses, per-wavefront vector-memory
     instructions, of one kernel (digit-order filter)."""
+    if kind == "conv_mid":               # the four-step middle: the conv with another cache policy
+        kind = "conv"
     ps = plan(n, v)
-    one_dir = sum((v // r) * (DFT_OPS[r] + (4 * (2 * r - 3) if M > 1 else 0)) for r, M in ps)
+    one_dir =sum((v // r) * (DFT_OPS[r] + (4 * (2 * r - 3) if M > 1 else 0)) for r, M in ps)
     exchanges = len(ps) - 1
     twiddle_slots = sum(v // r for r, M in ps if M > 1)
     two = kind in ("conv", "conv_r2", "conv_timed")
