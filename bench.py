@@ -8,6 +8,11 @@ line carries the fp32 figure as `value` and the int16-BFP figure for the same
 N and batch under "bfp", plus a short fp32 sweep over the other
 configs[1] sizes under "sweep".  Prints ONE JSON line.
 
+The filter is planned once on the host (--layout lane: the library's
+lane-major pair layout, at the variant fufft_fastest_variant picks for it --
+radix 16 at N = 4096; --layout dr: the reference's digit order).  The line
+also carries the headline workload with the other layout ("dr_layout").
+
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 
 Timing, the same for the headline and every other leg: a correctness check
@@ -60,7 +65,11 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--n", type=int, default=4096)
     p.add_argument("--points-log2", type=int, default=27)
-    p.add_argument("--variant", default="auto")
+    p.add_argument("--variant", default="fastest",
+                   help="r8 | v16 | auto | fastest (fufft_fastest_variant for --layout)")
+    p.add_argument("--layout", default="lane", choices=["lane", "dr"],
+                   help="filter layout of the fp32 and BFP legs: the library's lane-major pairs "
+                        "(fastest) or the reference's digit order")
     p.add_argument("--sweep", default="512,1024,2048",
                    help="extra fp32 sizes timed with --sweep-steps launches each ('' for none)")
     p.add_argument("--sweep-steps", type=int, default=50)
@@ -151,9 +160,16 @@ def per_launch_us(torch, fn, count, stream):
     return [a.elapsed_time(b) * 1e3 for a, b in ev]
 
 
-def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, settle_s=0.0, per_launch=0):
-    """fp32 fused conv at size n over pts points: (seconds per launch, rel L2 of
-    a sample), plus the one-by-one launch durations in us when per_launch > 0."""
+def pick_variant(ff, n, variant, layout):
+    """The variant a leg runs: --variant as given, "fastest" through the library."""
+    return ff.fastest_variant(n, layout) if variant == "fastest" else ff.resolve_variant(n, variant)
+
+
+def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, settle_s=0.0, per_launch=0,
+               layout="dr"):
+    """fp32 fused conv at size n over pts points, the filter planned in
+    `layout`: (seconds per launch, rel L2 of a sample), plus the one-by-one
+    launch durations in us when per_launch > 0."""
     batch = pts // n
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
@@ -161,10 +177,10 @@ def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, set
     out = torch.empty_like(x)
     rng = np.random.default_rng(seed)
     taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS)).to(dev)
+    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS)).to(dev)
 
     def step():
-        ff.conv(x, filt, out, n=n, batch=batch, variant=variant, stream=stream)
+        ff.conv(x, filt, out, n=n, batch=batch, variant=variant, layout=layout, stream=stream)
 
     # correctness before timing: fp64 numpy on a sample of signals
     step()
@@ -335,10 +351,10 @@ def bench_2d(torch, ff, dev, pts, steps, warmup, stream, seed):
     }
 
 
-def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64):
+def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64, variant="auto", layout="dr"):
     """int16-BFP fused conv: Gaussian x 10^u per signal (u ~ U[-3, 3]), quantised on
     the host by the library codec (one exponent per `block` points), one shared
-    fp32 filter spectrum."""
+    fp32 filter spectrum planned in `layout`."""
     batch = pts // n
     rng = np.random.default_rng(seed)
     x = np.empty((batch, n), dtype=np.complex64)
@@ -352,12 +368,13 @@ def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64):
         x[b0:b1].imag = im * s
     q, e = ff.bfp_quantize(x, block=block)
     taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter(taps, n, variant="auto", kind=ff.FILTER_TAPS)).to(dev)
+    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS)).to(dev)
     dq, de = torch.from_numpy(q).to(dev), torch.from_numpy(e).to(dev)
     qo, eo = torch.empty_like(dq), torch.empty_like(de)
 
     def step():
-        ff.conv_bfp16(dq, de, filt, qo, eo, n=n, batch=batch, stream=stream, block=block)
+        ff.conv_bfp16(dq, de, filt, qo, eo, n=n, batch=batch, stream=stream, block=block, variant=variant,
+                      layout=layout)
 
     step()
     torch.cuda.synchronize()
@@ -416,7 +433,7 @@ def _timed_threads(threads, seconds, per_call, call):
     return sum(counts), time.perf_counter() - t0
 
 
-def cpu_baseline(sizes, bfp_sizes, head_n, seconds, threads):
+def cpu_baseline(sizes, bfp_sizes, head_n, seconds, threads, lanes):
     """The reference's CPU conv paths on the GPU box's host cores, on bounded
     samples of the bench workloads (Re/Im N(0,1) signals, one shared filter),
     one thread per usable core, each thread looping over its own batch:
@@ -425,8 +442,9 @@ def cpu_baseline(sizes, bfp_sizes, head_n, seconds, threads):
       cos/sin (cpu_mixed.cpp:121-174, 260-266), per N in `sizes`; the headline
       `value` is this row at head_n;
     - fp32 transcription: verify_kernel.cpp's CPU transcription of the device
-      dataflow at the plan the GPU runs (kernel_pipeline_ip for radix 8,
-      kernel_pipeline_v16 for radix 16; verify_kernel.cpp:211-244, 1051-1082);
+      dataflow at the plan the GPU runs in this bench (lanes[n] values per
+      lane: kernel_pipeline_ip for radix 8, kernel_pipeline_v16 for radix 16;
+      verify_kernel.cpp:211-244, 1051-1082);
     - BFP transcription: verify_kernel.cpp's kernel_v16_bfp (1111-1135), the
       int16-BFP dataflow with one fp32 scale per transform, per N in bfp_sizes.
 
@@ -458,7 +476,7 @@ def cpu_baseline(sizes, bfp_sizes, head_n, seconds, threads):
         done, el = _timed_threads(threads, per_row, per, f64)
         rows["fp64_cpu_mixed"][str(n)] = {"gpoints_s": gpts(done, el, n), "signals": done, "seconds": round(el, 2)}
 
-        v = 8 if n in (512, 4096, 8192) else 16        # the plan FUFFT_AUTO runs on the GPU
+        v = lanes[n]                                   # the plan the GPU legs run
         plan = O.ref_plan(n, v)
         lead = plan.radices[0] if plan.radices[0] != v else 1
         nv = sum(1 for r in plan.radices if r == v)
@@ -549,8 +567,9 @@ def main():
 
     # the headline is timed like every other leg: correctness check first, then
     # SETTLE_S of untimed launches, then exactly --warmup and --steps launches
-    avg, rel, each = bench_fp32(torch, ff, dev, n, pts, args.variant, args.steps, args.warmup, stream, 1234,
-                                SETTLE_S, per_launch=50)
+    var = pick_variant(ff, n, args.variant, args.layout)
+    avg, rel, each = bench_fp32(torch, ff, dev, n, pts, var, args.steps, args.warmup, stream, 1234,
+                                SETTLE_S, per_launch=50, layout=args.layout)
     if not rel <= 2e-6:
         print(json.dumps({"error": f"fp32 accuracy check failed at N={n}: rel L2 {rel:.3e}"}))
         sys.exit(1)
@@ -578,8 +597,9 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": f"fused fp32 cyclic conv, N={n}, batch {batch} (2^{args.points_log2} points), "
-                               f"one shared filter, mid=multiply, variant={ff.resolve_variant(n, args.variant)}",
-                   "n": n, "batch": batch, "points": pts},
+                               f"one shared filter planned on the host, mid=multiply, variant={var}, "
+                               f"filter layout={args.layout}",
+                   "n": n, "batch": batch, "points": pts, "variant": var, "filter_layout": args.layout},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "model_bytes_per_point": 24,
@@ -592,6 +612,16 @@ def main():
         "accuracy": {"rel_l2_vs_fp64_sample": rel},
     }
 
+    # the same workload with the reference's digit-order filter, at its faster variant
+    other = "dr" if args.layout == "lane" else "lane"
+    ovar = pick_variant(ff, n, "fastest", other)
+    a, r = bench_fp32(torch, ff, dev, n, pts, ovar, args.sweep_steps, 3, stream, 1234, SETTLE_S, layout=other)
+    if not r <= 2e-6:
+        print(json.dumps({"error": f"fp32 accuracy check failed at N={n} ({other}): rel L2 {r:.3e}"}))
+        sys.exit(1)
+    line[f"{other}_layout"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                               "variant": ovar, "rel_l2": r}
+
     if not args.no_vendor:
         vt, vrel = bench_vendor_chain(torch, dev, n, pts, args.sweep_steps, 3, stream, 1234)
         line["vendor_chain"] = {"what": "torch.fft (rocFFT) forward -> multiply -> inverse, same workload",
@@ -602,10 +632,12 @@ def main():
     for s in [int(v) for v in args.sweep.split(",") if v.strip()]:
         if s == n:
             continue
-        a, r = bench_fp32(torch, ff, dev, s, pts, args.variant, args.sweep_steps, 3, stream, 77 + s, SETTLE_S)
+        sv = pick_variant(ff, s, args.variant, args.layout)
+        a, r = bench_fp32(torch, ff, dev, s, pts, sv, args.sweep_steps, 3, stream, 77 + s, SETTLE_S,
+                          layout=args.layout)
         sweep[str(s)] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
                          "frac_24B": round(24.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
-                         "variant": ff.resolve_variant(s, args.variant), "rel_l2": r}
+                         "variant": sv, "filter_layout": args.layout, "rel_l2": r}
         if not r <= 2e-6:
             print(json.dumps({"error": f"fp32 accuracy check failed at N={s}: rel L2 {r:.3e}"}))
             sys.exit(1)
@@ -615,8 +647,9 @@ def main():
     if not args.no_bfp:
         bfp = {}
         for s in [int(v) for v in args.bfp_sizes.split(",") if v.strip()]:
+            bv = pick_variant(ff, s, args.variant, args.layout)
             a, r, worst = bench_bfp(torch, ff, dev, s, pts, args.steps if s == n else args.sweep_steps,
-                                    args.warmup if s == n else 3, stream, 99 + s)
+                                    args.warmup if s == n else 3, stream, 99 + s, variant=bv, layout=args.layout)
             if not r <= 1e-4:
                 print(json.dumps({"error": f"BFP accuracy check failed at N={s}: rel L2 {r:.3e}"}))
                 sys.exit(1)
@@ -625,12 +658,13 @@ def main():
                            "achieved_12B_gbs": round(12.0 * pts / a / 1e9, 1),
                            "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
                            "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst,
-                           "variant": ff.resolve_variant(s, "auto")}
+                           "variant": bv, "filter_layout": args.layout}
             if s == n:
                 # both legs timed the same way: check, SETTLE_S, --warmup, --steps
                 bfp[str(s)]["speedup_vs_fp32"] = round(g / gpts, 3)
                 # one exponent per signal: the reference's per-transform scale
-                a, r, worst = bench_bfp(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 99 + s, block=s)
+                a, r, worst = bench_bfp(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 99 + s, block=s,
+                                        variant=bv, layout=args.layout)
                 if not r <= 1e-4:
                     print(json.dumps({"error": f"BFP (block = N) accuracy check failed at N={s}: rel L2 {r:.3e}"}))
                     sys.exit(1)
@@ -675,8 +709,9 @@ def main():
     if not args.no_cpu_baseline:
         cores, affinity, quota = usable_cores()
         sizes = sorted({512, 1024, 2048, 4096, n})
+        lanes = {s: 8 if pick_variant(ff, s, args.variant, args.layout) == "r8" else 16 for s in sizes}
         cb = cpu_baseline(sizes, [int(v) for v in args.bfp_sizes.split(",") if v.strip()], n,
-                          args.cpu_seconds, cores)
+                          args.cpu_seconds, cores, lanes)
         cb["host"] = {"affinity_cpus": affinity, "cgroup_cpu_quota": quota, "threads": cores}
         line["cpu_baseline"] = cb
     print(json.dumps(line))

@@ -36,10 +36,21 @@ VALUES_PER_LANE = {"v16": 16, "r8": 8}
 
 
 def resolve_variant(n: int, variant: str) -> str:
-    """The lane layout FUFFT_AUTO picks for n (mirrors the library's rule)."""
+    """The lane layout FUFFT_AUTO picks for n (mirrors the library's rule: the
+    faster one with a digit-order filter, fastest_variant(n, "dr"))."""
     if variant != "auto":
         return variant
     return "r8" if n in (512, 4096, 8192) else "v16"
+
+
+def fastest_variant(n: int, layout: str = "lane") -> str:
+    """The faster variant for an n-point conv whose filter is in `layout`
+    (fufft_fastest_variant): with "lane", "r8" at n = 512 and "v16" from
+    n = 1024 on.  Plan the filter and launch with it."""
+    v = lib.fufft_fastest_variant(n, LAYOUT[layout])
+    if v < 0:
+        raise FufftError(v, "fufft_fastest_variant")
+    return "r8" if v == VARIANT["r8"] else "v16"
 
 
 class FufftError(RuntimeError):
@@ -59,6 +70,7 @@ def _load() -> C.CDLL:
         "fufft_init": ([i32], i32),
         "fufft_status_string": ([i32], C.c_char_p),
         "fufft_supported": ([i64, i32], i32),
+        "fufft_fastest_variant": ([i64, i32], i32),
         "fufft_plan_radices": ([i64, i32, C.POINTER(C.c_int)], i32),
         "fufft_digit_order": ([i64, i32, C.POINTER(C.c_int32)], i32),
         "fufft_plan_chains": ([i64, i32, C.POINTER(C.c_int)], i32),

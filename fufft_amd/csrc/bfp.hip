@@ -190,8 +190,9 @@ bfp_kernel(const BfpParams p)
    forward_dif<PL, LD, (T < 64 ? 64 : T), 64, KEEP_STORE>(r, A, L, tw, kc);
    {
       const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
-      const uint32_t fo = (modulo_count(t, p.fcount) * N + (p.fl == FLT_DR ? L * V : L)) * 8u;
-      mid_op<PL, MID>(r, fb, fo, (p.fl == FLT_DR ? 1 : T) * 8u);
+      const uint32_t f0 = modulo_count(t, p.fcount) * N * 8u;
+      if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, f0 + L * V * 8u, 16u);
+      else               mid_op_pairs<PL, MID>(r, fb, f0 + L * 16u, T * 16u);
    }
    inverse_dit<PL, LD, (T < 64 ? 64 : T), 64, KEEP_USE>(r, A, L, tw, kc);
 

@@ -25,6 +25,21 @@ namespace fufft {
 
 constexpr int cpb_for(int T) { return T >= 128 ? 1 : 256 / T; }
 
+// A lane's V digit-order values (slots L*V + k of the transform at point
+// offset base) as 16-byte pairs: contiguous in digit order, at 2(L + m*T)
+// lane-major (FLT_LANE).  One uniform branch; each side computes only its own
+// offsets.
+template<int V, int T>
+__device__ __forceinline__ void store_spectrum(const Buf& ob, const float2 (&r)[V], uint32_t base, int L, int layout)
+{
+   const bool lane = layout == FLT_LANE;
+   const uint32_t so = (base + (lane ? 2u : (uint32_t)V) * (uint32_t)L) * 8u;
+   const uint32_t ms = lane ? (uint32_t)T * 16u : 16u;
+#pragma unroll
+   for(int m = 0; m < V / 2; m++)
+      ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * ms);
+}
+
 template<int N, int V, int LAYOUT, int KIND, int MID>
 __global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
 conv1d_kernel(const Conv1dParams p)
@@ -89,10 +104,15 @@ conv1d_kernel(const Conv1dParams p)
    if constexpr(FROM_SPEC) {
       const Buf sb(p.spec, p.scount * (uint32_t)N * 8u);
       if(p.sl == FLT_LANE) {
-         // lane-major: slot L*V + k at position L + k*T, one coalesced load per k
-         const uint32_t so = (modulo_count(t, p.scount) * N + L) * 8u;
+         // lane-major pairs: slots L*V + 2m, 2m + 1 at 2(L + m*T), one
+         // contiguous KiB per 16-byte load of a wavefront
+         const uint32_t so = modulo_count(t, p.scount) * N * 8u + L * 16u;
 #pragma unroll
-         for(int k = 0; k < V; k++) r[k] = sb.ld2(so, k * T * 8);
+         for(int m = 0; m < V / 2; m++) {
+            const float4 q = sb.ld4(so, m * T * 16);
+            r[2 * m] = make_float2(q.x, q.y);
+            r[2 * m + 1] = make_float2(q.z, q.w);
+         }
       } else {
          // digit order: slots L*V .. L*V+V-1, two complex per 16-byte load
          const uint32_t so = (modulo_count(t, p.scount) * N + L * V) * 8u;
@@ -102,6 +122,15 @@ conv1d_kernel(const Conv1dParams p)
             r[2 * m] = make_float2(q.x, q.y);
             r[2 * m + 1] = make_float2(q.z, q.w);
          }
+      }
+      // Radix 8 (8 wavefronts per SIMD): the filter loads of the mid operation
+      // wait until the spectrum has arrived (the empty asm reads every value).
+      // Issued together with the spectrum loads they cost 3% at N = 4096 (358
+      // against 370 Gpt/s, same box); at radix 16 (4 wavefronts per SIMD) the
+      // wait costs up to 6% (N = 1024: 304 against 322).
+      if constexpr(V == 8) {
+#pragma unroll
+         for(int k = 0; k < V; k++) asm volatile("" :: "v"(r[k].x), "v"(r[k].y));
       }
    } else {
       const size_t wb = (size_t)t0 * N * EL_IN;
@@ -133,38 +162,22 @@ conv1d_kernel(const Conv1dParams p)
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
 #pragma unroll
       for(int k = 0; k < V; k++) r[k] = make_float2(r[k].x * p.scale, r[k].y * p.scale);
-      if(p.fl == FLT_DR) {
-         const uint32_t so = ((t - t0) * N + L * V) * 8u;
-#pragma unroll
-         for(int m = 0; m < V / 2; m++)
-            ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * 16);
-      } else {
-#pragma unroll
-         for(int k = 0; k < V; k++) ob.st2(r[k], lane_pos * 8u, k * T * 8);
-      }
+      store_spectrum<V, T>(ob, r, (t - t0) * N, L, p.fl);
       return;
    } else if constexpr(TO_SPEC) {
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
-      if(p.sl == FLT_LANE) {
-         // lane-major: every store of a wavefront is one contiguous run.  The
-         // digit-order store below writes 16 bytes per lane 64 or 128 bytes
-         // apart (32 cache lines per wavefront store) and runs 14-18% slower.
-#pragma unroll
-         for(int k = 0; k < V; k++) ob.st2(r[k], lane_pos * 8u, k * T * 8);
-      } else {
-         const uint32_t so = ((t - t0) * N + L * V) * 8u;
-#pragma unroll
-         for(int m = 0; m < V / 2; m++)
-            ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * 16);
-      }
+      // lane-major: every store of a wavefront is one contiguous run.  The
+      // digit-order store writes 16 bytes per lane 64 or 128 bytes apart (32
+      // or 64 cache lines per wavefront store) and runs 14-18% slower.
+      store_spectrum<V, T>(ob, r, (t - t0) * N, L, p.sl);
       return;
    } else {
       if constexpr(!C2C_INV) {
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
          const uint32_t fb0 = modulo_count(t, p.fcount) * N;
          // a uniform branch on the filter layout: each side computes only its own offset
-         if(p.fl == FLT_DR) mid_op<PL, MID>(r, fb, (fb0 + L * V) * 8u, 8u);
-         else               mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
+         if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, (fb0 + L * V) * 8u, 16u);
+         else               mid_op_pairs<PL, MID>(r, fb, fb0 * 8u + L * 16u, T * 16u);
       }
       stamp(3);
       inverse_dit<PL, LD, LANES, 64, KEEP_I>(r, A, L, tw, kc);

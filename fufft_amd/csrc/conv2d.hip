@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(C * (H / V)) col_kernel(const ColParams p)
    } else {
       {
          const Buf fb(static_cast<const char*>(p.filt) + (size_t)modulo_count(img, p.fcount) * ibytes, ibytes);
-         const uint32_t fc = p.f_dr ? (((c & ((1u << p.f_tr_log) - 1u)) << p.f_vr_log) | (c >> p.f_tr_log)) : c;
+         const uint32_t fc = p.f_dr ? lane_slot(c, p.f_tr_log, p.f_vr_log) : c;
          mid_op<PL, MID>(r, fb, (uint32_t)(L * V) * W8 + fc * 8u, W8);
       }
       inverse_dit<PL, LD, C * T, 64 / C, KEEP_I>(r, A, L, tw, kc);

@@ -26,6 +26,22 @@ inline hipError_t ensure_dynamic_lds(const void* kernel, size_t bytes, std::atom
    return e;
 }
 
+// Lane-major filter and spectrum layout (FUFFT_LAYOUT_LANE) of an n-point
+// plan with V = 2^vlog values per lane and T = n / V = 2^tlog lanes: lane L's
+// digit-order slots L*V + 2m and L*V + 2m + 1 sit side by side at positions
+// 2(L + m*T) and 2(L + m*T) + 1.  Each 16-byte load of a wavefront then reads
+// one contiguous KiB (8 cache lines), where digit order spreads it over 64 or
+// 32 lines.  lane_slot maps a position to the slot it holds, lane_position a
+// slot to its position.
+__host__ __device__ constexpr uint32_t lane_slot(uint32_t pos, uint32_t tlog, uint32_t vlog)
+{
+   return (((pos >> 1) & ((1u << tlog) - 1u)) << vlog) | ((pos >> (tlog + 1)) << 1) | (pos & 1u);
+}
+__host__ __device__ constexpr uint32_t lane_position(uint32_t slot, uint32_t tlog, uint32_t vlog)
+{
+   return (((slot >> vlog) | (((slot & ((1u << vlog) - 1u)) >> 1) << tlog)) << 1) | (slot & 1u);
+}
+
 // ---- 1D fused pipeline (conv1d.hip) ------------------------------------------------
 // K_FWD_R2 / K_APPLY_R2: the forward half reading two real arrays, the
 // inverse half writing two real arrays (2D two-for-one rows).
@@ -134,8 +150,8 @@ struct ColParams {
    // Filter column order.  f_dr = 0: the filter's columns are in the row
    // spectra's lane-major order, so column c reads filter column c.  f_dr = 1:
    // the reference's order, entry (r, s) = bin (rev_h(r), rev_w(s)); column c
-   // holds row slot s = (c mod T) * V + c / T (V values per lane of the row
-   // plan, T = w / V = 2^f_tr_log, V = 2^f_vr_log) and reads filter column s.
+   // holds row slot s = lane_slot(c, f_tr_log, f_vr_log) (V = 2^f_vr_log values
+   // per lane of the row plan, T = w / V = 2^f_tr_log) and reads filter column s.
    uint32_t      f_dr;
    uint32_t      f_tr_log;
    uint32_t      f_vr_log;

@@ -488,33 +488,50 @@ __device__ __forceinline__ void natural_to_digit(float2 (&r)[PL::V], float2* A, 
 enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
 // filter layouts: DR = digit order, slot i holds bin mixedrev(i) (what the
 // reference's MidMultiply reads, fufft.cuh:635); LANE = the same values laid
-// out lane-major, lane L's k-th value at L + k*T (the reference's bperm,
-// fufft.cuh:1444-1446), which keeps the read coalesced
+// out lane-major in pairs, lane L's values 2m and 2m + 1 at 2(L + m*T) and
+// 2(L + m*T) + 1 (lane_position; the reference's bperm, fufft.cuh:1444-1446,
+// lays them out lane-major one value at a time), so that every 16-byte filter
+// load of a wavefront reads one contiguous KiB
 enum { FLT_DR = 0, FLT_LANE = 1 };
 
-// The lane's V filter values sit at byte offsets voff + k*kstep of the filter
-// buffer.  MID is a template parameter: a runtime branch between the two
-// products makes the compiler keep both results live across the join.
-// With kstep == 8 (the digit-order layout) the V values are contiguous and
-// are read two per 16-byte load, halving the vector-memory instructions.
+template<int MID>
+__device__ __forceinline__ float2 mid_product(float2 a, float2 b)
+{
+   return (MID == MID_MUL) ? cmul(a, b) : cmul_conj(a, b);
+}
+
+// The lane's V filter values as V/2 pairs, values 2m and 2m + 1 in the 16
+// bytes at voff + m*mstep: mstep = 16 in digit order (the V values are
+// contiguous), 16*T lane-major.  MID is a template parameter: a runtime
+// branch between the two products makes the compiler keep both results live
+// across the join.
+template<class PL, int MID>
+__device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t mstep)
+{
+   if constexpr(MID != MID_NONE) {
+      float2 b[PL::V];
+#pragma unroll
+      for(int m = 0; m < PL::V / 2; m++) {
+         const float4 q = f.ld4(voff, m * mstep);
+         b[2 * m] = make_float2(q.x, q.y);
+         b[2 * m + 1] = make_float2(q.z, q.w);
+      }
+#pragma unroll
+      for(int k = 0; k < PL::V; k++) r[k] = mid_product<MID>(r[k], b[k]);
+   }
+}
+
+// The lane's V filter values one at a time, value k at voff + k*kstep (the
+// 2D column kernels: one image row apart).
 template<class PL, int MID>
 __device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t kstep)
 {
    if constexpr(MID != MID_NONE) {
       float2 b[PL::V];
-      if(kstep == 8u) {
 #pragma unroll
-         for(int m = 0; m < PL::V / 2; m++) {
-            const float4 q = f.ld4(voff, m * 16);
-            b[2 * m] = make_float2(q.x, q.y);
-            b[2 * m + 1] = make_float2(q.z, q.w);
-         }
-      } else {
+      for(int k = 0; k < PL::V; k++) b[k] = f.ld2(voff, k * kstep);
 #pragma unroll
-         for(int k = 0; k < PL::V; k++) b[k] = f.ld2(voff, k * kstep);
-      }
-#pragma unroll
-      for(int k = 0; k < PL::V; k++) r[k] = (MID == MID_MUL) ? cmul(r[k], b[k]) : cmul_conj(r[k], b[k]);
+      for(int k = 0; k < PL::V; k++) r[k] = mid_product<MID>(r[k], b[k]);
    }
 }
 

@@ -7,7 +7,7 @@
 // output position (r, c) of an h x w item (h = 1 in 1D) receives bin
 // (rev_h(r), rev_w(c')) times scale, each rev a bit-group reversal over the
 // plan's radix widths in pass order, c' = c or, lane-major, the digit-order
-// slot that position c holds.  One thread per output point, so the
+// slot that position c holds (lane_slot).  One thread per output point, so the
 // writes are coalesced and the reads gather; planning runs once per filter,
 // not on the conv's hot path.  (Taps are planned by the conv kernels' own
 // forward half, K_PLAN_TAPS.)
@@ -41,10 +41,10 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherParams p)
    const uint32_t r = o >> p.dw.bits;
    uint32_t c = o & ((1u << p.dw.bits) - 1u);
    if(p.lane_v) {
-      // lane-major along the row (1D filters, 2D columns): position L + k*T
-      // holds digit-order slot L*V + k
-      const uint32_t T = (1u << p.dw.bits) / (uint32_t)p.lane_v;
-      c = (c % T) * (uint32_t)p.lane_v + c / T;
+      // lane-major along the row (1D filters, 2D columns): the digit-order
+      // slot that position c holds
+      const uint32_t vlog = 31u - (uint32_t)__builtin_clz((uint32_t)p.lane_v);
+      c = lane_slot(c, p.dw.bits - vlog, vlog);
    }
    const uint32_t src = (group_reverse_dev(r, p.dh) << p.dw.bits) | group_reverse_dev(c, p.dw);
    const float2 v = p.in[item * per + src];

@@ -51,15 +51,23 @@ extern "C" {
 /* lane layout / radix family */
 #define FUFFT_V16  0   /* 16 values per lane, radix 16 (fufft_pipeline_v16)  */
 #define FUFFT_R8   1   /* 8 values per lane, radix 8 (fufft_pipeline_ip)     */
-#define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X, one
-                          rule for the fp32 and the BFP conv: FUFFT_R8 at
-                          N = 512, 4096 and 8192, FUFFT_V16 elsewhere.  The filter
-                          must be planned with the same variant. */
+#define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X with
+                          the digit-order filter (FUFFT_LAYOUT_DR), one rule
+                          for the fp32 and the BFP conv: FUFFT_R8 at N = 512,
+                          4096 and 8192, FUFFT_V16 elsewhere.  The filter must
+                          be planned with the same variant.  For the
+                          lane-major filter see fufft_fastest_variant. */
 
 /* filter layouts */
 #define FUFFT_LAYOUT_DR    0  /* slot i holds bin mixedrev(i) (MidMultiply, fufft.cuh:635) */
-#define FUFFT_LAYOUT_LANE  1  /* lane-major: value of slot V*L+k at L+k*(N/V)
-                                 (bperm of fufft_pipeline_v16f, fufft.cuh:1444-1446) */
+#define FUFFT_LAYOUT_LANE  1  /* lane-major pairs, T = N/V: the values of slots
+                                 V*L+2m and V*L+2m+1 at 2(L+m*T) and 2(L+m*T)+1,
+                                 so every 16-byte filter load of a wavefront
+                                 reads one contiguous KiB (the bperm layout of
+                                 fufft_pipeline_v16f, fufft.cuh:1444-1446, is
+                                 lane-major one value at a time).  With it
+                                 FUFFT_V16 is the fastest variant at
+                                 N = 1024 .. 8192 and FUFFT_R8 at N = 512. */
 
 /* filter_kind for fufft_plan_filter_f32 */
 #define FUFFT_FILTER_SPECTRUM  0  /* input is a natural-order spectrum             */
@@ -71,6 +79,14 @@ int fufft_init(int device);
 const char* fufft_status_string(int status);
 /* 1 if a single-launch kernel exists for (n, variant), else 0 */
 int fufft_supported(int64_t n, int variant);
+/* The faster variant (FUFFT_R8 or FUFFT_V16) for an n-point conv whose filter
+ * is in `layout`, as measured on MI355X for the fp32 and the BFP conv alike;
+ * FUFFT_AUTO is this for FUFFT_LAYOUT_DR.  With FUFFT_LAYOUT_LANE it is
+ * FUFFT_R8 at n = 512 and FUFFT_V16 at every other n, the fastest plan of
+ * this library at n = 1024 .. 16384.  Plan the filter and launch with the
+ * variant it returns.  No reference counterpart (the reference's caller
+ * picks the kernel template). */
+int fufft_fastest_variant(int64_t n, int layout);
 
 /* ---- host planning (no GPU needed) ------------------------------------------
  * Pass plan in DIF order: lead radix first, then radix 16 (or 8); returns the
@@ -292,7 +308,8 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
  *                      (mixedrev_h(r), mixedrev_w(slot(c))), where slot(c) is
  *                      the row plan's digit-order slot that column c of the
  *                      row spectra holds (fufft_plan2d_column_order): the rows
- *                      are lane-major, slot(c) = (c % T)*V + c / T with V the
+ *                      are in the 1D FUFFT_LAYOUT_LANE order, column
+ *                      c = 2(L + m*T) + j holding slot V*L + 2m + j with V the
  *                      row plan's values per lane and T = w / V, so the row
  *                      kernels store and load whole contiguous runs.  A
  *                      column tile then reads its filter columns as one

@@ -28,6 +28,11 @@ enum class Variant : int { V16 = FUFFT_V16, R8 = FUFFT_R8, Auto = FUFFT_AUTO };
 inline const char* status_string(int status) { return fufft_status_string(status); }
 inline int init(int device = 0) { return fufft_init(device); }
 inline bool supported(int64_t n, Variant v = Variant::Auto) { return fufft_supported(n, (int)v) != 0; }
+// the faster variant for a filter layout (FUFFT_LAYOUT_LANE: radix 16 from n = 1024 on)
+inline Variant fastest_variant(int64_t n, int layout = FUFFT_LAYOUT_LANE)
+{
+   return fufft_fastest_variant(n, layout) == FUFFT_R8 ? Variant::R8 : Variant::V16;
+}
 
 // ---- host planning (bench_fufft.cu:63-82, 156-170) ---------------------------------------
 

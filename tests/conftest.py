@@ -52,6 +52,21 @@ def bits_equal(a, b) -> bool:
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def lane_major(fdr, n, v):
+    """Digit-order filters or spectra (rows of n) in the lane-major pair layout
+    (FUFFT_LAYOUT_LANE): lane L's slots L*v + 2m and L*v + 2m + 1 at positions
+    2(L + m*T) and 2(L + m*T) + 1, T = n // v."""
+    t = n // v
+    f = np.asarray(fdr).reshape(-1, t, v // 2, 2)
+    return np.ascontiguousarray(f.transpose(0, 2, 1, 3)).reshape(np.shape(fdr))
+
+
+def lane_slot(c, n, v):
+    """The digit-order slot that lane-major position c holds (inverse of lane_major)."""
+    t = n // v
+    return ((c // 2) % t) * v + 2 * ((c // 2) // t) + c % 2
+
+
 def cols_to_dr(x, h, w):
     """A 2D filter or spectrum in the library's column order (lane-major rows,
     fufft_plan2d_column_order) re-ordered to the reference's digit order,

@@ -10,7 +10,7 @@ the device-planned filter within 2e-6 of fp64.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, cols_to_dr, crandn, cuniform, filt2d_dr
+from conftest import bits_equal, cols_to_dr, crandn, cuniform, filt2d_dr, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -131,8 +131,7 @@ def test_plan_device_1d(dev, variant, n, layout, rng):
     v = V[variant]
     want_t = scaled(O.fwd(taps, n, O.kernel_plan(n, v)), 1.0 / n).reshape(count, n)
     if layout == "lane":
-        t = n // v
-        want_t = np.ascontiguousarray(want_t.reshape(count, t, v).transpose(0, 2, 1)).reshape(count, n)
+        want_t = lane_major(want_t, n, v)
     assert bits_equal(got_t, want_t)
     assert O.rel_l2(got_t, host_t) <= 1e-6
 

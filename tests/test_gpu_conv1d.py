@@ -7,7 +7,7 @@ against fp64 (the north_star bound for fp32).
 import numpy as np
 import pytest
 
-from conftest import bits_equal, crandn, cuniform
+from conftest import bits_equal, crandn, cuniform, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -38,12 +38,6 @@ def run_conv(dev, a, filt, n, filt_stride, mid, variant, layout, inplace=False):
     ff.conv(da, df, dout, n=n, batch=a.size // n, filt_stride=filt_stride, mid=mid,
             variant=variant, layout=layout)
     return from_dev(dout).reshape(-1)
-
-
-def lane_major(fdr, n, v):
-    """filter slot v*L + k moved to L + k*T (the reference's bperm)"""
-    t = n // v
-    return np.ascontiguousarray(fdr.reshape(-1, t, v).transpose(0, 2, 1)).reshape(-1)
 
 
 @pytest.mark.parametrize("variant,n", SIZES)

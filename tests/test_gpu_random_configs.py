@@ -6,7 +6,7 @@ targeted tests do not list still run.  Every case prints its parameters first.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, crandn
+from conftest import bits_equal, crandn, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -28,16 +28,6 @@ def draw(seed):
                 per_signal=bool(rng.integers(2)), inplace=bool(rng.integers(2)),
                 direction=[-1, 1][rng.integers(2)], block=int(2 ** rng.integers(6, int(np.log2(n)) + 1)),
                 seed=seed)
-
-
-def lane_major(fdr, n, v):
-    """digit-order filters (rows of n) -> the lane-major layout: slot L*V + k at L + k*T"""
-    t = n // v
-    f = np.asarray(fdr).reshape(-1, n)
-    out = np.empty_like(f)
-    s = np.arange(n)
-    out[:, (s // v) + (s % v) * t] = f[:, s]
-    return out.reshape(-1)
 
 
 @pytest.mark.parametrize("seed", range(40))

@@ -82,7 +82,8 @@ def test_occupancy_radix8_vs_radix16(conv):
 
 def test_counters_agree_with_model_and_isa(conv):
     """profiles/conv_f32_n4096.md: SQ_INSTS_VALU, SQ_INSTS_LDS and SQ_INSTS_VMEM
-    per wavefront of the headline kernel, conv1d_kernel<4096, 8, xchg, conv, mul>."""
+    per wavefront of the headline kernel, conv1d_kernel<4096, 16, xchg, conv, mul>
+    (radix-16 lanes, lane-major pair filter)."""
     text = (ROOT / "profiles" / "conv_f32_n4096.md").read_text()
 
     def per_wave(counter):
@@ -90,7 +91,7 @@ def test_counters_agree_with_model_and_isa(conv):
         assert m, counter
         return float(m.group(1))
 
-    r = pick(conv, "conv", 4096, 8)
+    r = pick(conv, "conv", 4096, 16)
     m = r["model"]
     assert abs(per_wave("SQ_INSTS_VALU") - r["valu"]) <= 2
     assert per_wave("SQ_INSTS_LDS") == r["lds"]

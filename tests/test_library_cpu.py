@@ -15,7 +15,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from conftest import crandn
+from conftest import crandn, lane_major, lane_slot
 from oracle import oracle as O
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -51,6 +51,14 @@ def test_auto_variant_rule():
         want = "r8" if n in (512, 4096, 8192) else "v16"
         assert ff.resolve_variant(n, "auto") == want
         assert ff.plan_radices(n, "auto") == ff.plan_radices(n, want)
+        # FUFFT_AUTO is the faster variant for the digit-order filter
+        assert ff.fastest_variant(n, "dr") == want
+        # with the lane-major filter radix 16 wins from n = 1024 on
+        assert ff.fastest_variant(n, "lane") == ("r8" if n == 512 else "v16")
+        assert ff.supported(n, ff.fastest_variant(n, "lane"))
+    for bad in (100, 128, 32768):
+        with pytest.raises(ff.FufftError):
+            ff.fastest_variant(bad, "lane")
 
 
 @pytest.mark.parametrize("n", [8192, 32768, 65536, 131072])
@@ -74,8 +82,11 @@ def test_filter_planning_1d_layouts(rng):
     dr2 = ff.plan_filter(spec, n, variant="r8", kind=ff.FILTER_SPECTRUM)
     assert np.array_equal(dr2, (spec.astype(np.complex128) / n).astype(np.complex64)[perm])
     lane = ff.plan_filter(spec, n, variant="r8", layout="lane", kind=ff.FILTER_SPECTRUM)
+    assert np.array_equal(lane, lane_major(dr2, n, v))
+    # the pairs: lane L's values 2m, 2m + 1 side by side at 2(L + m*T)
     t = n // v
-    assert np.array_equal(lane, dr2.reshape(t, v).T.reshape(-1))
+    for L, m in ((0, 0), (3, 1), (t - 1, v // 2 - 1)):
+        assert np.array_equal(lane[2 * (L + m * t): 2 * (L + m * t) + 2], dr2[L * v + 2 * m: L * v + 2 * m + 2])
 
 
 def test_filter_planning_large_and_2d(rng):
@@ -95,10 +106,9 @@ def test_filter_planning_large_and_2d(rng):
     got2_dr = ff.plan_filter2d(taps2, h, w, kind=ff.FILTER_TAPS, layout="dr")
     want2_dr = S[np.ix_(rh, rw)].reshape(-1)
     assert np.max(np.abs(got2_dr - want2_dr)) <= 2e-7 * np.max(np.abs(want2_dr))
-    # columns in the library's order: column c holds row slot (c % T) * vr + c // T
+    # columns in the library's order: the rows' lane-major pair layout
     slot = ff.column_order2d(h, w)
-    T = w // vr
-    assert np.array_equal(slot, [(c % T) * vr + c // T for c in range(w)])
+    assert np.array_equal(slot, [lane_slot(c, w, vr) for c in range(w)])
     assert sorted(slot) == list(range(w))
     want2 = S[np.ix_(rh, rw[slot])].reshape(-1)
     assert np.max(np.abs(got2 - want2)) <= 2e-7 * np.max(np.abs(want2))
