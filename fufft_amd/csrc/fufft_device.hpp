@@ -231,6 +231,24 @@ __device__ __forceinline__ void tw_evenodd(float2 (&r)[NR], float2 w1)
    }
 }
 
+// the even/odd chains that also hand back the powers they generated, w[k] = W^(jk)
+template<int OFF, int STRIDE, int NR>
+__device__ __forceinline__ void tw_evenodd_keep(float2 (&r)[NR], float2 w1, float2 (&w)[16])
+{
+   const float2 w2 = cmul(w1, w1);
+   w[1] = w1;
+   w[2] = w2;
+   r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w1);
+   float2 ze = w2, zo = cmul(w2, w1);
+   w[3] = zo;
+#pragma unroll
+   for(int m = 1; m < 8; m++) {
+      r[OFF + 2 * m * STRIDE]       = cmul(r[OFF + 2 * m * STRIDE], ze);
+      r[OFF + (2 * m + 1) * STRIDE] = cmul(r[OFF + (2 * m + 1) * STRIDE], zo);
+      if(m < 7) { ze = cmul(ze, w2); zo = cmul(zo, w2); w[2 * m + 2] = ze; w[2 * m + 3] = zo; }
+   }
+}
+
 // chain selection: in-workgroup radix-16 passes use the even/odd chains, every
 // other pass (lead radices, the four-step outer radix-16 level) the single
 // chain -- exactly as in the reference's kernels

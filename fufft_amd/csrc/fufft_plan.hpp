@@ -240,17 +240,19 @@ struct Twiddles {
 // same W^j -- and only the mid operation and the M = 1 butterflies lie between
 // them, so the chain the forward pass generated is kept in registers and the
 // inverse pass reads its conjugates instead of rebuilding it (R - 2 complex
-// products per group).  Done for radix-8 lanes (one group per lane, 7 powers),
-// which run at 8 wavefronts per SIMD with VGPRs to spare for the short live
-// range.  Results are unchanged bit for bit (tw_kept_conj).  Only for pure
-// powers of 8: there the kernels stay within 64 VGPRs (8 wavefronts per SIMD);
-// with a leading radix-2/4 pass (N = 1024, 2048, 8192) the kept chain pushed
-// them to 66-74 VGPRs, i.e. 6-7 wavefronts, which costs more than it saves.
+// products per group).  Done for one group per lane at pure powers of the
+// lane radix: radix 8 (7 powers) stays within 64 VGPRs, i.e. 8 wavefronts per
+// SIMD (with a leading radix-2/4 pass, N = 1024, 2048, 8192, the kept chain
+// pushed it to 66-74 VGPRs, 6-7 wavefronts, which costs more than it saves);
+// radix 16 (15 powers, N = 256 and 4096) goes from 77 to 110 VGPRs at
+// N = 4096 under the 128 its LDS-held 4 wavefronts per SIMD allow, and runs
+// 1% (fp32) to 1.5% (BFP) faster.  Results are unchanged bit for bit
+// (tw_kept_conj).
 template<class PL>
 struct KeptChain {
    static constexpr int P = PL::NP >= 2 ? PL::NP - 2 : 0;
    static constexpr int R = PL::radix(P);
-   static constexpr bool enabled = PL::NP >= 2 && PL::V == 8 && PL::LEAD == 1 && R == 8 && PL::stride(P) > 1;
+   static constexpr bool enabled = PL::NP >= 2 && PL::LEAD == 1 && R == PL::V && PL::stride(P) > 1;
    float2 w[enabled ? R : 1];
 };
 
@@ -275,7 +277,10 @@ __device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<
          }
          dftR<R, SIGN, g, G>(r);
          if constexpr(!DIT) {
-            if constexpr(keep && KEEP == KEEP_STORE) tw_single_keep<R, g, G>(r, w1, kc.w);
+            if constexpr(keep && KEEP == KEEP_STORE) {
+               if constexpr(R == 16) tw_evenodd_keep<g, G>(r, w1, kc.w);
+               else                  tw_single_keep<R, g, G>(r, w1, kc.w);
+            }
             else                                     twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
          }
       } else {

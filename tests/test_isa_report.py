@@ -76,8 +76,11 @@ def test_model_matches_compiled_kernel(conv, n, v, kind, mid):
 def test_occupancy_radix8_vs_radix16(conv):
     for n in (512, 1024, 2048, 4096, 8192):
         assert pick(conv, "conv", n, 8)["waves_per_simd"] == 8, n
+    # radix 16 at N = 4096: 4 wavefronts per SIMD by LDS (one transform of 34 KiB
+    # per 4-wavefront workgroup), which the kept radix-16 chain's VGPRs (at most
+    # 128 for 4 wavefronts) do not lower
     r16 = pick(conv, "conv", 4096, 16)
-    assert r16["waves_per_simd"] == 4 and r16["limited_by"] == "LDS"
+    assert r16["waves_per_simd"] == 4 and r16["limited_by"] in ("LDS", "VGPRs") and r16["vgpr"] <= 128
 
 
 def test_counters_agree_with_model_and_isa(conv):
