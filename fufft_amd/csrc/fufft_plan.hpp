@@ -240,19 +240,24 @@ struct Twiddles {
 // same W^j -- and only the mid operation and the M = 1 butterflies lie between
 // them, so the chain the forward pass generated is kept in registers and the
 // inverse pass reads its conjugates instead of rebuilding it (R - 2 complex
-// products per group).  Done for one group per lane at pure powers of the
-// lane radix: radix 8 (7 powers) stays within 64 VGPRs, i.e. 8 wavefronts per
-// SIMD (with a leading radix-2/4 pass, N = 1024, 2048, 8192, the kept chain
-// pushed it to 66-74 VGPRs, 6-7 wavefronts, which costs more than it saves);
-// radix 16 (15 powers, N = 256 and 4096) goes from 77 to 110 VGPRs at
-// N = 4096 under the 128 its LDS-held 4 wavefronts per SIMD allow, and runs
-// 1% (fp32) to 1.5% (BFP) faster.  Results are unchanged bit for bit
-// (tw_kept_conj).
+// products per group).  Done where that pass has one group per lane (its
+// radix is the lane radix) and the registers allow it:
+//  - radix 8 (7 powers) at pure powers of 8 stays within 64 VGPRs, i.e. 8
+//    wavefronts per SIMD; with a leading radix-2/4 pass (N = 1024, 2048, 8192)
+//    the kept chain pushed it to 66-74 VGPRs, 6-7 wavefronts, which costs more
+//    than it saves;
+//  - radix 16 (15 powers) runs 4 wavefronts per SIMD, held by LDS, so up to
+//    128 VGPRs are free: N = 256 and 4096 go from 77 to 110 VGPRs, N = 512 to
+//    2048 (behind a lead pass) to 113-124; N = 8192 and 16384 would pass 128.
+//    Same box: fp32 N = 4096 +1.1%, 1024 / 2048 +0.3 to +1%; BFP N = 4096
+//    +1.5%, 1024 +2.9%, 2048 +1.3%.
+// Results are unchanged bit for bit (tw_kept_conj).
 template<class PL>
 struct KeptChain {
    static constexpr int P = PL::NP >= 2 ? PL::NP - 2 : 0;
    static constexpr int R = PL::radix(P);
-   static constexpr bool enabled = PL::NP >= 2 && PL::LEAD == 1 && R == PL::V && PL::stride(P) > 1;
+   static constexpr bool regs = PL::LEAD == 1 || (PL::V == 16 && PL::T <= 128);
+   static constexpr bool enabled = PL::NP >= 2 && regs && R == PL::V && PL::stride(P) > 1;
    float2 w[enabled ? R : 1];
 };
 

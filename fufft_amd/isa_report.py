@@ -15,8 +15,8 @@ per-point operation model, and which resource limits resident warps).  Here:
 - model_conv() counts the fp32 arithmetic the pipeline needs per lane
   (butterflies: 4 / 16 / 56 / 168 operations for radix 2 / 4 / 8 / 16; stage
   twiddles: 2R - 3 complex products of 2 MUL + 2 FMA per twiddled group,
-  i.e. R - 1 applied and R - 2 generated, less the R - 2 a fused kernel at
-  a pure power of its radix carries from its forward to its inverse; the mid product: 4 per
+  i.e. R - 1 applied and R - 2 generated, less the R - 2 a fused kernel
+  carries from its forward to its inverse where it keeps that chain; the mid product: 4 per
   value), the
   LDS traffic (V writes and V reads per lane per exchange) and the
   vector-memory instructions per wavefront;
@@ -194,10 +194,12 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
     twiddle_slots = sum(v // r for r, M in ps if M > 1)
     two = kind in ("conv", "conv_r2", "conv_timed")
     arith = one_dir * (2 if two else 1)
-    # lanes at a pure power of their radix carry the forward's last twiddle chain
-    # to the inverse: R - 2 fewer complex products per lane (KeptChain), 6 at
-    # radix 8 and 14 at radix 16
-    if two and all(r == v for r, _ in ps) and len(ps) >= 2:
+    # the forward's last twiddled pass hands its chain to the inverse when that
+    # pass has one group per lane and the registers allow it (KeptChain): pure
+    # powers of the radix, and radix 16 up to N = 2048 behind a lead pass;
+    # R - 2 fewer complex products per lane, 6 at radix 8 and 14 at radix 16
+    if two and len(ps) >= 2 and ps[-2][0] == v and ps[-2][1] > 1 and \
+            (all(r == v for r, _ in ps) or (v == 16 and n // v <= 128)):
         arith -= 4 * (v - 2)
     if kind in ("conv", "conv_r2", "conv_timed", "apply", "apply_r2") and mid != "none":
         arith += 4 * v
