@@ -8,7 +8,7 @@ BASELINE config-3 style input: per-signal N(0,1) scaled by 10^u, u ~ U[-3, 3].
 import numpy as np
 import pytest
 
-from conftest import crandn
+from conftest import crandn, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -175,6 +175,40 @@ def test_bfp_full_batch_every_size(dev, n, variant, block):
     e_s = de.view(batch, nb)[idx].cpu().numpy()
     v = 8 if ff.resolve_variant(n, variant) == "r8" else 16
     oq, oe = O.bfp_conv(q_s, e_s, filt, n, O.kernel_plan(n, v), block=block)
+    torch.cuda.synchronize()
+    assert np.array_equal(eo.view(batch, nb)[idx].cpu().numpy(), oe.reshape(16, -1))
+    assert np.array_equal(qo.view(batch, 2 * n)[idx].cpu().numpy(), oq.reshape(16, -1))
+    del dq, de, qo, eo
+
+
+@pytest.mark.parametrize("n", [512, 1024, 2048, 4096, 8192, 16384])
+def test_bfp_full_batch_lane_layout_fastest_variant(dev, n):
+    """The bench's BFP plan: the filter planned lane-major at the variant
+    fufft_fastest_variant picks for it, 2^27 points, 64-point blocks; 16
+    transforms spread over the batch bit-identical to the oracle (which reads
+    the same filter in digit order)."""
+    import torch
+    import fufft_amd as ff
+    variant = ff.fastest_variant(n, "lane")
+    v = 8 if variant == "r8" else 16
+    batch = (1 << 27) // n
+    nb = n // 64
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3 * n + 1)
+    dq = torch.randint(-32767, 32768, (2 * batch * n,), dtype=torch.int16, device=dev, generator=gen)
+    de = torch.randint(-30, 10, (batch * nb,), dtype=torch.int8, device=dev, generator=gen)
+    rng = np.random.default_rng(3 * n)
+    taps = crandn(rng, n)
+    fdr = ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS)
+    flane = ff.plan_filter(taps, n, variant=variant, layout="lane", kind=ff.FILTER_TAPS)
+    assert np.array_equal(flane, lane_major(fdr, n, v))
+    qo, eo = torch.empty_like(dq), torch.empty_like(de)
+    print(f"case bfp full-batch lane n={n} variant={variant} batch={batch}", flush=True)
+    ff.conv_bfp16(dq, de, to_dev(flane, dev), qo, eo, n=n, batch=batch, variant=variant, layout="lane")
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
+    q_s = dq.view(batch, 2 * n)[idx].cpu().numpy()
+    e_s = de.view(batch, nb)[idx].cpu().numpy()
+    oq, oe = O.bfp_conv(q_s, e_s, fdr, n, O.kernel_plan(n, v), block=64)
     torch.cuda.synchronize()
     assert np.array_equal(eo.view(batch, nb)[idx].cpu().numpy(), oe.reshape(16, -1))
     assert np.array_equal(qo.view(batch, 2 * n)[idx].cpu().numpy(), oq.reshape(16, -1))

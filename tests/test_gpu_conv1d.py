@@ -172,11 +172,13 @@ def test_full_size_properties(dev, rng):
     assert float(err) < 1e-6
 
 
+@pytest.mark.parametrize("layout", ["dr", "lane"])
 @pytest.mark.parametrize("variant,n", SIZES)
-def test_full_batch_every_size(dev, variant, n):
-    """2^27 points at every size: full occupancy, every workgroup slot of the
-    GPU busy, where an exchange race would show; 16 signals spread over the
-    batch (first and last included) bit-identical to the oracle."""
+def test_full_batch_every_size(dev, variant, n, layout):
+    """2^27 points at every size and both filter layouts: full occupancy, every
+    workgroup slot of the GPU busy, where an exchange race would show; 16
+    signals spread over the batch (first and last included) bit-identical to
+    the oracle."""
     import torch
     import fufft_amd as ff
     batch = (1 << 27) // n
@@ -188,8 +190,9 @@ def test_full_batch_every_size(dev, variant, n):
     plan = O.kernel_plan(n, V[variant])
     fdr = spec[O.mixedrev(plan)]
     dout = torch.empty_like(da)
-    print(f"case full-batch variant={variant} n={n} batch={batch}", flush=True)
-    ff.conv(da, to_dev(fdr, dev), dout, n=n, batch=batch, variant=variant)
+    fdev = lane_major(fdr, n, V[variant]) if layout == "lane" else fdr
+    print(f"case full-batch variant={variant} n={n} layout={layout} batch={batch}", flush=True)
+    ff.conv(da, to_dev(fdev, dev), dout, n=n, batch=batch, variant=variant, layout=layout)
     idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
     a_s = da.view(batch, n)[idx].cpu().numpy()
     got = dout.view(batch, n)[idx].cpu().numpy().reshape(-1)
