@@ -28,7 +28,7 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN, ERR_SCRATCH = 0, -1, -2, -
 SCRATCH_BYTES = 64 << 20          # FUFFT_SCRATCH_BYTES
 MID = {"mul": 0, "conj": 1, "none": 2}
 VARIANT = {"v16": 0, "r8": 1, "auto": 2}
-LAYOUT = {"dr": 0, "lane": 1}
+LAYOUT = {"dr": 0, "lane": 1, "bperm": 2}
 FILTER_SPECTRUM, FILTER_TAPS = 0, 1
 FORWARD, INVERSE = -1, 1
 BFP_BLOCK = 64

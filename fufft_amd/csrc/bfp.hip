@@ -120,9 +120,11 @@ constexpr int bfp_min_waves(int v, int layout) { return (v == 8 && layout != LAY
 // (the fp32 kernel of that plan does not, so it keeps the padded layout).
 constexpr int bfp_lds_layout(int n, int v) { return (void)n, (void)v, LAYOUT_XCHG; }
 
-template<int N, int V, int LAYOUT, int MID, bool BIG>
-__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
-bfp_kernel(const BfpParams p)
+// The kernel body; BPERM: the filter in the reference's bperm layout, a
+// kernel of its own so that the digit-order and pair kernels carry no code
+// for it.
+template<int N, int V, int LAYOUT, int MID, bool BIG, bool BPERM>
+__device__ __forceinline__ void bfp_body(const BfpParams& p)
 {
    using PL = Plan<N, V>;
    using LD = Lds<V, LAYOUT>;
@@ -191,8 +193,9 @@ bfp_kernel(const BfpParams p)
    {
       const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
       const uint32_t f0 = modulo_count(t, p.fcount) * N * 8u;
-      if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, f0 + L * V * 8u, 16u);
-      else               mid_op_pairs<PL, MID>(r, fb, f0 + L * 16u, T * 16u);
+      if constexpr(BPERM)    mid_op<PL, MID>(r, fb, f0 + L * 8u, T * 8u);
+      else if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, f0 + L * V * 8u, 16u);
+      else                    mid_op_pairs<PL, MID>(r, fb, f0 + L * 16u, T * 16u);
    }
    inverse_dit<PL, LD, (T < 64 ? 64 : T), 64, KEEP_USE>(r, A, L, tw, kc);
 
@@ -253,6 +256,20 @@ bfp_kernel(const BfpParams p)
    }
 }
 
+template<int N, int V, int LAYOUT, int MID, bool BIG>
+__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
+bfp_kernel(const BfpParams p)
+{
+   bfp_body<N, V, LAYOUT, MID, BIG, false>(p);
+}
+
+template<int N, int V, int LAYOUT, int MID, bool BIG>
+__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
+bfp_bperm_kernel(const BfpParams p)
+{
+   bfp_body<N, V, LAYOUT, MID, BIG, true>(p);
+}
+
 template<int N, int V, int LAYOUT, int MID>
 static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
 {
@@ -261,11 +278,19 @@ static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
    if(p.log_block < 6 || (1 << p.log_block) > N) return hipErrorInvalidValue;
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2)
                     + (big ? (size_t)CPB * bfp_bmax_words(N) * 4 : 0);
+   const bool bp = MID != MID_NONE && p.fl == FLT_BPERM;
    const void* k = big ? reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID, true>)
                        : reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID, false>);
+   // (the XOR layout is a comparison option and has no bperm kernels)
+   if constexpr(MID != MID_NONE && LAYOUT != LAYOUT_XOR) {
+      if(bp) k = big ? reinterpret_cast<const void*>(&bfp_bperm_kernel<N, V, LAYOUT, MID, true>)
+                     : reinterpret_cast<const void*>(&bfp_bperm_kernel<N, V, LAYOUT, MID, false>);
+   } else {
+      if(bp) return hipErrorInvalidValue;
+   }
    if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
-   static std::atomic<uint64_t> lds_ok[2]{};
-   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok[big]); e != hipSuccess) return e;
+   static std::atomic<uint64_t> lds_ok[4]{};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok[2 * bp + big]); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
    BfpParams arg = p;
    void* argv[] = { &arg };

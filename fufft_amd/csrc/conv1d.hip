@@ -40,9 +40,11 @@ __device__ __forceinline__ void store_spectrum(const Buf& ob, const float2 (&r)[
       ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * ms);
 }
 
-template<int N, int V, int LAYOUT, int KIND, int MID>
-__global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
-conv1d_kernel(const Conv1dParams p)
+// The kernel body.  BPERM: the filter is in the reference's bperm layout
+// (8-byte loads); it gets a kernel of its own so that the digit-order and
+// pair kernels carry no code for it.
+template<int N, int V, int LAYOUT, int KIND, int MID, bool BPERM>
+__device__ __forceinline__ void conv1d_body(const Conv1dParams& p)
 {
    using PL = Plan<N, V>;
    using LD = Lds<V, LAYOUT>;
@@ -162,7 +164,12 @@ conv1d_kernel(const Conv1dParams p)
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
 #pragma unroll
       for(int k = 0; k < V; k++) r[k] = make_float2(r[k].x * p.scale, r[k].y * p.scale);
-      store_spectrum<V, T>(ob, r, (t - t0) * N, L, p.fl);
+      if(p.fl == FLT_BPERM) {
+#pragma unroll
+         for(int k = 0; k < V; k++) ob.st2(r[k], lane_pos * 8u, k * T * 8);
+      } else {
+         store_spectrum<V, T>(ob, r, (t - t0) * N, L, p.fl);
+      }
       return;
    } else if constexpr(TO_SPEC) {
       const Buf ob(static_cast<char*>(p.out0) + (size_t)t0 * N * 8, TPW * N * 8);
@@ -176,8 +183,9 @@ conv1d_kernel(const Conv1dParams p)
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
          const uint32_t fb0 = modulo_count(t, p.fcount) * N;
          // a uniform branch on the filter layout: each side computes only its own offset
-         if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, (fb0 + L * V) * 8u, 16u);
-         else               mid_op_pairs<PL, MID>(r, fb, fb0 * 8u + L * 16u, T * 16u);
+         if constexpr(BPERM)    mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
+         else if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, (fb0 + L * V) * 8u, 16u);
+         else                    mid_op_pairs<PL, MID>(r, fb, fb0 * 8u + L * 16u, T * 16u);
       }
       stamp(3);
       inverse_dit<PL, LD, LANES, 64, KEEP_I>(r, A, L, tw, kc);
@@ -221,14 +229,46 @@ conv1d_kernel(const Conv1dParams p)
 }
 
 template<int N, int V, int LAYOUT, int KIND, int MID>
+__global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
+conv1d_kernel(const Conv1dParams p)
+{
+   conv1d_body<N, V, LAYOUT, KIND, MID, false>(p);
+}
+
+// the calls that read a filter, with a bperm filter
+template<int N, int V, int LAYOUT, int KIND, int MID>
+__global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
+conv1d_bperm_kernel(const Conv1dParams p)
+{
+   conv1d_body<N, V, LAYOUT, KIND, MID, true>(p);
+}
+
+// (the XOR layout is a comparison option and has no bperm kernels)
+template<int LAYOUT, int KIND, int MID>
+constexpr bool reads_bperm_filter()
+{
+   return LAYOUT != LAYOUT_XOR && MID != MID_NONE &&
+          (KIND == K_CONV || KIND == K_CONV_TIMED || KIND == K_CONV_R2 || KIND == K_APPLY);
+}
+
+template<int N, int V, int LAYOUT, int KIND, int MID>
 static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
 {
    constexpr int T = N / V, CPB = cpb_for(T);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2);
+   bool bp = false;
    const void* k = reinterpret_cast<const void*>(&conv1d_kernel<N, V, LAYOUT, KIND, MID>);
+   if constexpr(reads_bperm_filter<LAYOUT, KIND, MID>()) {
+      if(p.fl == FLT_BPERM) {
+         bp = true;
+         k = reinterpret_cast<const void*>(&conv1d_bperm_kernel<N, V, LAYOUT, KIND, MID>);
+      }
+   } else {
+      if(MID != MID_NONE && p.fl == FLT_BPERM) return hipErrorInvalidValue;
+   }
    if(!modulo_count_ok(p.fcount, p.ntrans) || !modulo_count_ok(p.scount, p.ntrans)) return hipErrorInvalidValue;
-   static std::atomic<uint64_t> lds_ok{0};
-   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
+   static std::atomic<uint64_t> lds_ok[2]{};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok[bp]); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
    Conv1dParams arg = p;
    void* argv[] = { &arg };

@@ -97,6 +97,7 @@ struct GatherParams {
    float2*       out;      // planned filters (must not alias in)
    uint64_t      total;    // points over all items
    int32_t       lane_v;   // lane-major columns: values per lane of the row plan; 0 = digit order
+   int32_t       bperm;    // with lane_v: the reference's bperm (slot L*V + k at L + k*T), not pairs
    float         scale;
    GatherDigits  dh, dw;   // rows (dh.np = 0 in 1D) and row digits
 };

@@ -501,8 +501,10 @@ enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
 // out lane-major in pairs, lane L's values 2m and 2m + 1 at 2(L + m*T) and
 // 2(L + m*T) + 1 (lane_position; the reference's bperm, fufft.cuh:1444-1446,
 // lays them out lane-major one value at a time), so that every 16-byte filter
-// load of a wavefront reads one contiguous KiB
-enum { FLT_DR = 0, FLT_LANE = 1 };
+// load of a wavefront reads one contiguous KiB; BPERM = the reference's bperm
+// itself, lane L's k-th value at L + k*T (8-byte loads, one contiguous 512
+// bytes per wavefront load), accepted so that its filters pass as they are
+enum { FLT_DR = 0, FLT_LANE = 1, FLT_BPERM = 2 };
 
 template<int MID>
 __device__ __forceinline__ float2 mid_product(float2 a, float2 b)

@@ -42,9 +42,10 @@ __global__ void __launch_bounds__(256) gather_kernel(const GatherParams p)
    uint32_t c = o & ((1u << p.dw.bits) - 1u);
    if(p.lane_v) {
       // lane-major along the row (1D filters, 2D columns): the digit-order
-      // slot that position c holds
+      // slot that position c holds -- pairs, or the reference's bperm
       const uint32_t vlog = 31u - (uint32_t)__builtin_clz((uint32_t)p.lane_v);
-      c = lane_slot(c, p.dw.bits - vlog, vlog);
+      const uint32_t tlog = p.dw.bits - vlog;
+      c = p.bperm ? ((c & ((1u << tlog) - 1u)) << vlog) | (c >> tlog) : lane_slot(c, tlog, vlog);
    }
    const uint32_t src = (group_reverse_dev(r, p.dh) << p.dw.bits) | group_reverse_dev(c, p.dw);
    const float2 v = p.in[item * per + src];

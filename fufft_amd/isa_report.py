@@ -216,13 +216,14 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
     stores = {"conv_r2": 2 * v, "apply_r2": 2 * v, "fwd": v // 2, "fwd_r2": v // 2,
               "plan_taps": v // 2}.get(kind, v)
     # code for the other side of a runtime layout branch sits in the kernel but does not run:
-    # the lane-major filter read and the lane-major spectrum read of the inverse-only
-    # kernels (V/2 16-byte loads each).  The planning and spectrum stores take one code
-    # path for both layouts (the offsets are selected), so no store is left untaken.
+    # the lane-major pair filter read (V/2 16-byte loads), the lane-major spectrum read of the
+    # inverse-only kernels (V/2) and the bperm store of the taps planner (V 8-byte stores).  The
+    # digit-order and pair spectrum stores take one code path (the offsets are selected); a
+    # bperm filter read has kernels of its own (conv1d_bperm_kernel, bfp_bperm_kernel).
     untaken_loads = v // 2 if (kind in ("conv", "conv_r2", "conv_timed", "apply", "apply_r2") and mid != "none") else 0
     if kind in ("apply", "apply_r2"):
         untaken_loads += v // 2
-    untaken = {"loads": untaken_loads, "stores": 0}
+    untaken = {"loads": untaken_loads, "stores": v if kind == "plan_taps" else 0}
     return {"fp32_arith_per_lane": arith, "lds_access_8B_per_lane": lds, "vmem_loads_per_wave": loads,
             "vmem_stores_per_wave": stores, "untaken_branch": untaken, "passes": ps}
 

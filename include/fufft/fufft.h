@@ -68,6 +68,11 @@ extern "C" {
                                  lane-major one value at a time).  With it
                                  FUFFT_V16 is the fastest variant at
                                  N = 1024 .. 8192 and FUFFT_R8 at N = 512. */
+#define FUFFT_LAYOUT_BPERM 2  /* the reference's bperm (fufft_pipeline_v16f,
+                                 fufft.cuh:1444-1446; verify_kernel.cpp:
+                                 1381-1387): the value of slot V*L+k at
+                                 L+k*(N/V).  1D calls only; a filter built for
+                                 the reference's _v16f passes as it is. */
 
 /* filter_kind for fufft_plan_filter_f32 */
 #define FUFFT_FILTER_SPECTRUM  0  /* input is a natural-order spectrum             */

@@ -61,6 +61,13 @@ def lane_major(fdr, n, v):
     return np.ascontiguousarray(f.transpose(0, 2, 1, 3)).reshape(np.shape(fdr))
 
 
+def bperm(fdr, n, v):
+    """Digit-order filters (rows of n) in the reference's bperm layout
+    (FUFFT_LAYOUT_BPERM, verify_kernel.cpp:1381-1387): slot L*v + k at L + k*T."""
+    t = n // v
+    return np.ascontiguousarray(np.asarray(fdr).reshape(-1, t, v).transpose(0, 2, 1)).reshape(np.shape(fdr))
+
+
 def lane_slot(c, n, v):
     """The digit-order slot that lane-major position c holds (inverse of lane_major)."""
     t = n // v

@@ -10,7 +10,7 @@ the device-planned filter within 2e-6 of fp64.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, cols_to_dr, crandn, cuniform, filt2d_dr, lane_major
+from conftest import bits_equal, cols_to_dr, crandn, cuniform, filt2d_dr, lane_major, bperm
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -110,7 +110,7 @@ def test_c2c_rejects_bad_args(dev):
 
 @pytest.mark.parametrize("variant,n", [("v16", 256), ("v16", 4096), ("r8", 512), ("r8", 4096),
                                        ("r8", 8192), ("v16", 16384)])
-@pytest.mark.parametrize("layout", ["dr", "lane"])
+@pytest.mark.parametrize("layout", ["dr", "lane", "bperm"])
 def test_plan_device_1d(dev, variant, n, layout, rng):
     import torch
     import fufft_amd as ff
@@ -132,6 +132,8 @@ def test_plan_device_1d(dev, variant, n, layout, rng):
     want_t = scaled(O.fwd(taps, n, O.kernel_plan(n, v)), 1.0 / n).reshape(count, n)
     if layout == "lane":
         want_t = lane_major(want_t, n, v)
+    elif layout == "bperm":
+        want_t = bperm(want_t, n, v)
     assert bits_equal(got_t, want_t)
     assert O.rel_l2(got_t, host_t) <= 1e-6
 

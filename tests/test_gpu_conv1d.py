@@ -7,7 +7,7 @@ against fp64 (the north_star bound for fp32).
 import numpy as np
 import pytest
 
-from conftest import bits_equal, crandn, cuniform, lane_major
+from conftest import bits_equal, bperm, crandn, cuniform, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -68,6 +68,8 @@ def test_per_signal_filter_and_lane_layout(dev, variant, n, rng):
     print(f"case per-signal variant={variant} n={n}", flush=True)
     assert bits_equal(run_conv(dev, a, fdr, n, n, "mul", variant, "dr"), want)
     assert bits_equal(run_conv(dev, a, lane_major(fdr, n, v), n, n, "mul", variant, "lane"), want)
+    # the reference's own bperm layout (fufft_pipeline_v16f's filter) passes as it is
+    assert bits_equal(run_conv(dev, a, bperm(fdr, n, v), n, n, "mul", variant, "bperm"), want)
 
 
 @pytest.mark.parametrize("n", [1024, 4096])

@@ -6,7 +6,7 @@ targeted tests do not list still run.  Every case prints its parameters first.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, crandn, lane_major
+from conftest import bits_equal, bperm, crandn, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -24,7 +24,7 @@ def draw(seed):
     batch = int(rng.integers(1, max(2, min(37, (1 << 19) // n))))
     return dict(op=op, variant=variant, n=n, batch=batch,
                 mid=["mul", "conj", "none"][rng.integers(3)],
-                layout=["dr", "lane"][rng.integers(2)],
+                layout=["dr", "lane", "bperm"][rng.integers(3)],
                 per_signal=bool(rng.integers(2)), inplace=bool(rng.integers(2)),
                 direction=[-1, 1][rng.integers(2)], block=int(2 ** rng.integers(6, int(np.log2(n)) + 1)),
                 seed=seed)
@@ -41,7 +41,7 @@ def test_random_config(dev, seed):
     plan = O.kernel_plan(n, v)
     nf = batch if c["per_signal"] else 1
     fdr = (crandn(rng, (nf, n)) / n).astype(np.complex64).reshape(-1)
-    fdev = lane_major(fdr, n, v) if c["layout"] == "lane" else fdr
+    fdev = {"dr": fdr, "lane": lane_major(fdr, n, v), "bperm": bperm(fdr, n, v)}[c["layout"]]
     stride = n if c["per_signal"] else 0
     dt = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
     if c["op"] == "conv":
@@ -69,7 +69,7 @@ def test_random_config(dev, seed):
         fr = (rng.uniform(-1, 1, (nf, n)) / n).astype(np.complex64)      # real filter taps' spectrum
         taps_plan = np.concatenate([ff.plan_filter(fr[i], n, variant=c["variant"], kind=ff.FILTER_TAPS)
                                     for i in range(nf)])
-        fdev2 = lane_major(taps_plan, n, v) if c["layout"] == "lane" else taps_plan
+        fdev2 = {"dr": taps_plan, "lane": lane_major(taps_plan, n, v), "bperm": bperm(taps_plan, n, v)}[c["layout"]]
         u, w = torch.empty(batch * n, device=dev), torch.empty(batch * n, device=dev)
         ff.conv_r2(dt(x), dt(y), dt(fdev2), u, w, n=n, batch=batch, filt_stride=stride,
                    variant=c["variant"], layout=c["layout"])

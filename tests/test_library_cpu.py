@@ -15,7 +15,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from conftest import crandn, lane_major, lane_slot
+from conftest import bperm, crandn, lane_major, lane_slot
 from oracle import oracle as O
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -83,6 +83,15 @@ def test_filter_planning_1d_layouts(rng):
     assert np.array_equal(dr2, (spec.astype(np.complex128) / n).astype(np.complex64)[perm])
     lane = ff.plan_filter(spec, n, variant="r8", layout="lane", kind=ff.FILTER_SPECTRUM)
     assert np.array_equal(lane, lane_major(dr2, n, v))
+    # the reference's bperm (verify_kernel.cpp:1381-1387): bperm[L + k*T] = b_dr[V*L + k]
+    bp = ff.plan_filter(spec, n, variant="r8", layout="bperm", kind=ff.FILTER_SPECTRUM)
+    assert np.array_equal(bp, bperm(dr2, n, v))
+    t = n // v
+    assert np.array_equal(bp[3 + 5 * t], dr2[v * 3 + 5])
+    # 2D filters take the reference's order or the library's, not bperm
+    with pytest.raises(ff.FufftError) as ei:
+        ff.plan_filter2d(crandn(rng, 256 * 256), 256, 256, layout="bperm")
+    assert ei.value.status == ff.ERR_INVALID
     # the pairs: lane L's values 2m, 2m + 1 side by side at 2(L + m*T)
     t = n // v
     for L, m in ((0, 0), (3, 1), (t - 1, v // 2 - 1)):
