@@ -19,7 +19,7 @@ The module switches the table back to the default source when it ends.
 import numpy as np
 import pytest
 
-from conftest import bits_equal, cols_to_dr, crandn, cuniform
+from conftest import bits_equal, bperm, cols_to_dr, crandn, cuniform, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -76,6 +76,14 @@ def test_gpu_equals_reference_on_golden_fixture(ref_tw, name):
         out = torch.empty_like(da)
         ff.conv(da, to_dev(case["bdr"], dev), out, n=n, batch=a.size // n, filt_stride=n, variant=kind)
         assert bits_equal(host(out), case["out"])
+        # the same filters in the reference's bperm layout and in the library's
+        # lane-major pairs give the compiled reference's outputs too
+        v = 16 if kind == "v16" else 8
+        for layout, moved in (("bperm", bperm(case["bdr"], n, v)), ("lane", lane_major(case["bdr"], n, v))):
+            out2 = torch.empty_like(da)
+            ff.conv(da, to_dev(moved, dev), out2, n=n, batch=a.size // n, filt_stride=n, variant=kind,
+                    layout=layout)
+            assert bits_equal(host(out2), case["out"]), layout
     elif kind == "split":
         n = int(case["n"])
         a = case["a"]
