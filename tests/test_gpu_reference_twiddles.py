@@ -201,20 +201,27 @@ def test_conv2d_equals_libm_oracle(ref_tw, h, w, layout, rng):
     assert bits_equal(host(out), O.conv2d(a, b_dr, h, w, ph, pw, tw=O.TW_LIBM))
 
 
+@pytest.mark.parametrize("layout", ["dr", "lane"])
 @pytest.mark.parametrize("n", [512, 4096])
-def test_bfp_equals_libm_oracle(ref_tw, n, rng):
+def test_bfp_equals_libm_oracle(ref_tw, n, layout, rng):
+    """The BFP conv at FUFFT_AUTO with the digit-order filter, and at the bench's
+    plan (lane-major filter, fufft_fastest_variant), equals the LIBM-mode oracle."""
     import torch
     import fufft_amd as ff
     dev = ref_tw
     batch = 16
+    variant = "auto" if layout == "dr" else ff.fastest_variant(n, "lane")
+    v = 8 if ff.resolve_variant(n, variant) == "r8" else 16
     x = (crandn(rng, (batch, n)) * 10.0 ** rng.uniform(-3, 3, (batch, 1))).astype(np.complex64)
     q, e = ff.bfp_quantize(x)
-    filt = ff.plan_filter(crandn(rng, n), n, variant="auto", kind=ff.FILTER_TAPS)
-    print(f"case reftw bfp n={n}", flush=True)
+    taps = crandn(rng, n)
+    filt = ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS)
+    fdev = ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS)
+    print(f"case reftw bfp n={n} layout={layout} v={v}", flush=True)
     dq, de = to_dev(q, dev), to_dev(e, dev)
     qo, eo = torch.empty_like(dq), torch.empty_like(de)
-    ff.conv_bfp16(dq, de, to_dev(filt, dev), qo, eo, n=n, batch=batch)
-    oq, oe = O.bfp_conv(q, e, filt, n, O.kernel_plan(n, 8), tw=O.TW_LIBM)
+    ff.conv_bfp16(dq, de, to_dev(fdev, dev), qo, eo, n=n, batch=batch, variant=variant, layout=layout)
+    oq, oe = O.bfp_conv(q, e, filt, n, O.kernel_plan(n, v), tw=O.TW_LIBM)
     assert np.array_equal(host(eo), oe)
     assert np.array_equal(host(qo), oq)
 
