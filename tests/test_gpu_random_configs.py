@@ -3,6 +3,8 @@ bit for bit: the size, lane width, batch (ragged), mid operation, filter
 layout, filter stride and aliasing are drawn per case, so combinations the
 targeted tests do not list still run.  Every case prints its parameters first.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -30,7 +32,16 @@ def draw(seed):
                 seed=seed)
 
 
-@pytest.mark.parametrize("seed", range(40))
+def seeds():
+    """40 seeds by default; FUFFT_RANDOM_SEEDS=a:b runs seeds a .. b-1 instead (longer sweeps)."""
+    spec = os.environ.get("FUFFT_RANDOM_SEEDS")
+    if not spec:
+        return range(40)
+    lo, hi = (int(x) for x in spec.split(":"))
+    return range(lo, hi)
+
+
+@pytest.mark.parametrize("seed", seeds())
 def test_random_config(dev, seed):
     import torch
     import fufft_amd as ff
