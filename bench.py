@@ -110,7 +110,7 @@ SETTLE_S = 0.1          # set from --settle in main()
 
 def time_launches(torch, fn, steps, warmup, stream, settle_s=0.0):
     """Seconds for `steps` launches of fn after `warmup` untimed ones.  With
-    settle_s > 0 (the secondary figures, not the headline) untimed launches
+    settle_s > 0 (every leg passes --settle; PMC runs pass 0) untimed launches
     continue until settle_s seconds have passed: after an idle gap -- host-side
     input generation or a correctness check -- the part runs 8-13% slow for
     the first tens of milliseconds while its clocks ramp."""

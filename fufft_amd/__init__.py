@@ -71,6 +71,7 @@ def _load() -> C.CDLL:
         "fufft_status_string": ([i32], C.c_char_p),
         "fufft_supported": ([i64, i32], i32),
         "fufft_fastest_variant": ([i64, i32], i32),
+        "fufft_mid_reads_filter": ([i32], i32),
         "fufft_plan_radices": ([i64, i32, C.POINTER(C.c_int)], i32),
         "fufft_digit_order": ([i64, i32, C.POINTER(C.c_int32)], i32),
         "fufft_plan_chains": ([i64, i32, C.POINTER(C.c_int)], i32),
@@ -268,10 +269,37 @@ def get_twiddles(device: int = 0) -> str:
 # before the library sees them; the library then checks sizes, strides,
 # enums and alignment again and returns a status, raised as FufftError.
 
-def _filt(filt, name: str, n: int, batch: int, stride: int, mid: str):
+def _mid(mid) -> int:
+    """The C ABI id of a mid operation: a name of MID, or an id as it is (a
+    policy added to the library's kernel sources has an id and no name here)."""
+    if isinstance(mid, str):
+        if mid not in MID:
+            raise ValueError(f"mid must be one of {sorted(MID)} or a policy id, not {mid!r}")
+        return MID[mid]
+    return int(mid)
+
+
+_MID_READS_FILTER = {MID["mul"]: True, MID["conj"]: True, MID["none"]: False}
+
+
+def mid_reads_filter(mid) -> bool:
+    """Whether the mid operation reads a filter: known here for the three
+    named ones, asked of the library (fufft_mid_reads_filter) for any other
+    id; FufftError for an id no policy of this build has."""
+    m = _mid(mid)
+    if m in _MID_READS_FILTER:
+        return _MID_READS_FILTER[m]
+    r = lib.fufft_mid_reads_filter(m)
+    if r < 0:
+        raise FufftError(r, "fufft_mid_reads_filter")
+    return bool(r)
+
+
+def _filt(filt, name: str, n: int, batch: int, stride: int, mid):
     """Spec of a filter (or spectrum) of n points per item and stride `stride`;
-    None where the call does not read it (mid "none" with no filter given)."""
-    if filt is None and mid == "none":
+    None where the call does not read it (a mid operation that reads no
+    filter, with no filter given)."""
+    if filt is None and not mid_reads_filter(mid):
         return None
     return (filt, name, 8 * n * _count(stride, n, batch, name) if batch else 0, "complex")
 
@@ -281,7 +309,7 @@ def conv(inp, filt, out, n: int, batch: int, filt_stride: int = 0, mid: str = "m
     nb = 8 * n * batch
     pi, pf, po = _ptrs((inp, "inp", nb, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid),
                        (out, "out", nb, "complex"))
-    check(lib.fufft_conv_f32(pi, pf, filt_stride, po, n, batch, MID[mid], VARIANT[variant], LAYOUT[layout],
+    check(lib.fufft_conv_f32(pi, pf, filt_stride, po, n, batch, _mid(mid), VARIANT[variant], LAYOUT[layout],
                              _stream(stream)), "fufft_conv_f32")
 
 
@@ -304,7 +332,7 @@ def conv_timed(inp, filt, out, timing, n: int, batch: int, timing_groups: int, f
     ts = (timing, "timing", 4 * TIMER_STRIDE * timing_groups, "words") if timing_groups else None
     pi, pf, po, pt = _ptrs((inp, "inp", nb, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid),
                            (out, "out", nb, "complex"), ts)
-    check(lib.fufft_conv_timed_f32(pi, pf, filt_stride, po, n, batch, MID[mid], VARIANT[variant],
+    check(lib.fufft_conv_timed_f32(pi, pf, filt_stride, po, n, batch, _mid(mid), VARIANT[variant],
                                    LAYOUT[layout], pt, timing_groups, _stream(stream)),
           "fufft_conv_timed_f32")
 
@@ -336,7 +364,7 @@ def apply(spec, filt, out, n: int, batch: int, spec_stride: int = 0, filt_stride
           mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None) -> None:
     ps, pf, po = _ptrs(_filt(spec, "spec", n, batch, spec_stride, "mul"),
                        _filt(filt, "filt", n, batch, filt_stride, mid), (out, "out", 8 * n * batch, "complex"))
-    check(lib.fufft_apply_f32(ps, spec_stride, pf, filt_stride, po, n, batch, MID[mid], VARIANT[variant],
+    check(lib.fufft_apply_f32(ps, spec_stride, pf, filt_stride, po, n, batch, _mid(mid), VARIANT[variant],
                               LAYOUT[layout], _stream(stream)), "fufft_apply_f32")
 
 
@@ -358,7 +386,7 @@ def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int 
     pq, pe, pf, pqo, peo = _ptrs((qin, "qin", qb, "bfp"), (ein, "ein", eb, "exp"),
                                  _filt(filt, "filt", n, batch, filt_stride, mid),
                                  (qout, "qout", qb, "bfp"), (eout, "eout", eb, "exp"))
-    check(lib.fufft_conv_bfp16(pq, pe, pf, filt_stride, pqo, peo, n, batch, block, MID[mid], VARIANT[variant],
+    check(lib.fufft_conv_bfp16(pq, pe, pf, filt_stride, pqo, peo, n, batch, block, _mid(mid), VARIANT[variant],
                                LAYOUT[layout], _stream(stream)), "fufft_conv_bfp16")
 
 
@@ -428,7 +456,7 @@ def conv_large(buf, filt, n: int, batch: int, filt_stride: int = 0, mid: str = "
                stream=None) -> None:
     """Four-step conv of a batch of n-point signals, in place on buf."""
     pb, pf = _ptrs((buf, "buf", 8 * n * batch, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid))
-    check(lib.fufft_conv_large_f32(pb, pf, filt_stride, n, batch, MID[mid], _stream(stream)),
+    check(lib.fufft_conv_large_f32(pb, pf, filt_stride, n, batch, _mid(mid), _stream(stream)),
           "fufft_conv_large_f32")
 
 
@@ -471,7 +499,7 @@ def conv2d(inp, filt, out, h: int, w: int, batch: int, filt_stride: int = 0, mid
     nb = 8 * h * w * batch
     pi, pf, po = _ptrs((inp, "inp", nb, "complex"), _filt(filt, "filt", h * w, batch, filt_stride, mid),
                        (out, "out", nb, "complex"))
-    check(lib.fufft_conv2d_f32(pi, pf, filt_stride, po, h, w, batch, MID[mid], LAYOUT[layout],
+    check(lib.fufft_conv2d_f32(pi, pf, filt_stride, po, h, w, batch, _mid(mid), LAYOUT[layout],
                                _stream(stream)), "fufft_conv2d_f32")
 
 
@@ -508,7 +536,7 @@ def apply2d(spec, filt, out, h: int, w: int, batch: int, spec_stride: int = 0, f
     np_ = h * w
     ps, pf, po = _ptrs(_filt(spec, "spec", np_, batch, spec_stride, "mul"),
                        _filt(filt, "filt", np_, batch, filt_stride, mid), (out, "out", 8 * np_ * batch, "complex"))
-    check(lib.fufft_apply2d_f32(ps, spec_stride, pf, filt_stride, po, h, w, batch, MID[mid], LAYOUT[layout],
+    check(lib.fufft_apply2d_f32(ps, spec_stride, pf, filt_stride, po, h, w, batch, _mid(mid), LAYOUT[layout],
                                 _stream(stream)), "fufft_apply2d_f32")
 
 

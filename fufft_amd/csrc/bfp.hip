@@ -278,11 +278,11 @@ static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
    if(p.log_block < 6 || (1 << p.log_block) > N) return hipErrorInvalidValue;
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2)
                     + (big ? (size_t)CPB * bfp_bmax_words(N) * 4 : 0);
-   const bool bp = MID != MID_NONE && p.fl == FLT_BPERM;
+   const bool bp = mid_reads_filter<MID> && p.fl == FLT_BPERM;
    const void* k = big ? reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID, true>)
                        : reinterpret_cast<const void*>(&bfp_kernel<N, V, LAYOUT, MID, false>);
    // (the XOR layout is a comparison option and has no bperm kernels)
-   if constexpr(MID != MID_NONE && LAYOUT != LAYOUT_XOR) {
+   if constexpr(mid_reads_filter<MID> && LAYOUT != LAYOUT_XOR) {
       if(bp) k = big ? reinterpret_cast<const void*>(&bfp_bperm_kernel<N, V, LAYOUT, MID, true>)
                      : reinterpret_cast<const void*>(&bfp_bperm_kernel<N, V, LAYOUT, MID, false>);
    } else {
@@ -300,18 +300,9 @@ static hipError_t launch_bfp_one(const BfpParams& p, hipStream_t s)
 template<int N, int V>
 static hipError_t launch_bfp_nv(int layout, const BfpParams& p, hipStream_t s)
 {
-   if(layout == LAYOUT_XOR) {
-      switch(p.mid) {
-         case MID_MUL:  return launch_bfp_one<N, V, LAYOUT_XOR, MID_MUL>(p, s);
-         case MID_CONJ: return launch_bfp_one<N, V, LAYOUT_XOR, MID_CONJ>(p, s);
-         default:       return launch_bfp_one<N, V, LAYOUT_XOR, MID_NONE>(p, s);
-      }
-   }
-   switch(p.mid) {
-      case MID_MUL:  return launch_bfp_one<N, V, bfp_lds_layout(N, V), MID_MUL>(p, s);
-      case MID_CONJ: return launch_bfp_one<N, V, bfp_lds_layout(N, V), MID_CONJ>(p, s);
-      default:       return launch_bfp_one<N, V, bfp_lds_layout(N, V), MID_NONE>(p, s);
-   }
+   if(layout == LAYOUT_XOR)
+      return with_mid(p.mid, [&](auto m) { return launch_bfp_one<N, V, LAYOUT_XOR, decltype(m)::value>(p, s); });
+   return with_mid(p.mid, [&](auto m) { return launch_bfp_one<N, V, bfp_lds_layout(N, V), decltype(m)::value>(p, s); });
 }
 
 bool bfp_supported(int n, int v)

@@ -247,7 +247,7 @@ conv1d_bperm_kernel(const Conv1dParams p)
 template<int LAYOUT, int KIND, int MID>
 constexpr bool reads_bperm_filter()
 {
-   return LAYOUT != LAYOUT_XOR && MID != MID_NONE &&
+   return LAYOUT != LAYOUT_XOR && mid_reads_filter<MID> &&
           (KIND == K_CONV || KIND == K_CONV_TIMED || KIND == K_CONV_R2 || KIND == K_APPLY);
 }
 
@@ -264,7 +264,7 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
          k = reinterpret_cast<const void*>(&conv1d_bperm_kernel<N, V, LAYOUT, KIND, MID>);
       }
    } else {
-      if(MID != MID_NONE && p.fl == FLT_BPERM) return hipErrorInvalidValue;
+      if(mid_reads_filter<MID> && p.fl == FLT_BPERM) return hipErrorInvalidValue;
    }
    if(!modulo_count_ok(p.fcount, p.ntrans) || !modulo_count_ok(p.scount, p.ntrans)) return hipErrorInvalidValue;
    static std::atomic<uint64_t> lds_ok[2]{};
@@ -278,12 +278,7 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
 template<int N, int V, int LAYOUT, int KIND>
 static hipError_t launch_mid(const Conv1dParams& p, hipStream_t s)
 {
-   switch(p.mid) {
-      case MID_MUL:  return launch_one<N, V, LAYOUT, KIND, MID_MUL>(p, s);
-      case MID_CONJ: return launch_one<N, V, LAYOUT, KIND, MID_CONJ>(p, s);
-      case MID_NONE: return launch_one<N, V, LAYOUT, KIND, MID_NONE>(p, s);
-      default:       return hipErrorInvalidValue;
-   }
+   return with_mid(p.mid, [&](auto m) { return launch_one<N, V, LAYOUT, KIND, decltype(m)::value>(p, s); });
 }
 
 template<int N, int V, int LAYOUT>
@@ -309,12 +304,7 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
       case K_CONV_TIMED:
          // the timed build exists for the default LDS layout only
          if constexpr(LAYOUT == default_lds_layout(N, V)) {
-            switch(p.mid) {
-               case MID_MUL:  return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_MUL>(p, s);
-               case MID_CONJ: return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_CONJ>(p, s);
-               case MID_NONE: return launch_one<N, V, LAYOUT, K_CONV_TIMED, MID_NONE>(p, s);
-               default:       return hipErrorInvalidValue;
-            }
+            return launch_mid<N, V, LAYOUT, K_CONV_TIMED>(p, s);
          } else {
             return hipErrorInvalidValue;
          }

@@ -108,12 +108,7 @@ static hipError_t launch_col_mid(const ColParams& p, hipStream_t s)
    if constexpr(KIND == COL_FWD) {
       return launch_col_one<H, KIND, MID_NONE>(p, s);
    } else {
-      switch(p.mid) {
-         case MID_MUL:  return launch_col_one<H, KIND, MID_MUL>(p, s);
-         case MID_CONJ: return launch_col_one<H, KIND, MID_CONJ>(p, s);
-         case MID_NONE: return launch_col_one<H, KIND, MID_NONE>(p, s);
-         default:       return hipErrorInvalidValue;
-      }
+      return with_mid(p.mid, [&](auto m) { return launch_col_one<H, KIND, decltype(m)::value>(p, s); });
    }
 }
 

@@ -75,7 +75,7 @@ struct Conv1dParams {
    uint32_t      ntrans;   // transforms in the launch
    uint32_t      fcount;   // transform t uses filter (t % fcount)
    uint32_t      scount;   // transform t uses spectrum (t % scount)
-   int32_t       mid;      // MID_MUL / MID_CONJ / MID_NONE
+   int32_t       mid;      // a registered mid policy id (FUFFT_MID_POLICIES)
    int32_t       fl;       // FLT_DR / FLT_LANE (filter read; K_PLAN_TAPS: layout written)
    int32_t       sl;       // FLT_DR / FLT_LANE: spectrum K_FWD writes, K_APPLY reads
    float         scale;    // K_PLAN_TAPS: factor applied to the spectrum

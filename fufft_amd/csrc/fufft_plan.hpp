@@ -495,7 +495,79 @@ __device__ __forceinline__ void natural_to_digit(float2 (&r)[PL::V], float2* A, 
 }
 
 // ---- the mid operation at the M = 1 boundary -----------------------------------------
+// What a fused kernel does to each spectrum value between its forward and its
+// inverse transform, in registers: the counterpart of the reference's Mid
+// policies MidNothing / MidMultiply / MidConjMultiply (fufft.cuh:616-650),
+// which rewrite the shared-memory buffer in a pass of their own.  As there, a
+// new fusion costs a struct:
+//
+//    struct MidFoo {
+//       static constexpr bool reads_filter = ...;   // false: no filter operand is read
+//       __device__ static float2 apply(float2 a, float2 b);
+//    };
+//
+// with a the spectrum value and b the filter value of the same slot (zero when
+// reads_filter is false), plus one line in FUFFT_MID_POLICIES giving its id,
+// the value the C ABI's `mid` argument takes.  Every kernel with a mid
+// operation (the fused 1D and int16-BFP convs, the split apply, the 2D column
+// kernels, the four-step middle) is then instantiated for it, and every entry
+// point that takes `mid` accepts the id.
+struct MidMultiply {
+   static constexpr bool reads_filter = true;
+   __device__ __forceinline__ static float2 apply(float2 a, float2 b) { return cmul(a, b); }
+};
+struct MidConjMultiply {
+   static constexpr bool reads_filter = true;
+   __device__ __forceinline__ static float2 apply(float2 a, float2 b) { return cmul_conj(a, b); }
+};
+struct MidNothing {
+   static constexpr bool reads_filter = false;
+   __device__ __forceinline__ static float2 apply(float2 a, float2) { return a; }
+};
+
+#define FUFFT_MID_POLICIES(X) \
+   X(0, MidMultiply)          \
+   X(1, MidConjMultiply)      \
+   X(2, MidNothing)
+
+// the ids of the three above, for the kernel kinds that fix their operation
 enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
+
+template<int MID> struct MidById;
+#define FUFFT_MID_BY_ID(id, S) template<> struct MidById<id> { using type = S; };
+FUFFT_MID_POLICIES(FUFFT_MID_BY_ID)
+#undef FUFFT_MID_BY_ID
+template<int MID> using MidOf = typename MidById<MID>::type;
+template<int MID> constexpr bool mid_reads_filter = MidOf<MID>::reads_filter;
+
+// host side: is `mid` a registered id, and does its operation read a filter
+constexpr bool mid_known(int mid)
+{
+#define FUFFT_MID_KNOWN(id, S) if(mid == id) return true;
+   FUFFT_MID_POLICIES(FUFFT_MID_KNOWN)
+#undef FUFFT_MID_KNOWN
+   return false;
+}
+constexpr bool mid_needs_filter(int mid)
+{
+#define FUFFT_MID_FILTER(id, S) if(mid == id) return S::reads_filter;
+   FUFFT_MID_POLICIES(FUFFT_MID_FILTER)
+#undef FUFFT_MID_FILTER
+   return false;
+}
+
+// f(std::integral_constant<int, id>{}) for the policy registered as `mid`;
+// hipErrorInvalidValue for an unknown id
+template<class F>
+hipError_t with_mid(int mid, F&& f)
+{
+   switch(mid) {
+#define FUFFT_MID_CASE(id, S) case id: return f(std::integral_constant<int, id>{});
+      FUFFT_MID_POLICIES(FUFFT_MID_CASE)
+#undef FUFFT_MID_CASE
+      default: return hipErrorInvalidValue;
+   }
+}
 // filter layouts: DR = digit order, slot i holds bin mixedrev(i) (what the
 // reference's MidMultiply reads, fufft.cuh:635); LANE = the same values laid
 // out lane-major in pairs, lane L's values 2m and 2m + 1 at 2(L + m*T) and
@@ -506,21 +578,16 @@ enum { MID_MUL = 0, MID_CONJ = 1, MID_NONE = 2 };
 // bytes per wavefront load), accepted so that its filters pass as they are
 enum { FLT_DR = 0, FLT_LANE = 1, FLT_BPERM = 2 };
 
-template<int MID>
-__device__ __forceinline__ float2 mid_product(float2 a, float2 b)
-{
-   return (MID == MID_MUL) ? cmul(a, b) : cmul_conj(a, b);
-}
-
 // The lane's V filter values as V/2 pairs, values 2m and 2m + 1 in the 16
 // bytes at voff + m*mstep: mstep = 16 in digit order (the V values are
 // contiguous), 16*T lane-major.  MID is a template parameter: a runtime
-// branch between the two products makes the compiler keep both results live
+// branch between two products makes the compiler keep both results live
 // across the join.
 template<class PL, int MID>
 __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t mstep)
 {
-   if constexpr(MID != MID_NONE) {
+   using Op = MidOf<MID>;
+   if constexpr(Op::reads_filter) {
       float2 b[PL::V];
 #pragma unroll
       for(int m = 0; m < PL::V / 2; m++) {
@@ -529,21 +596,29 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
          b[2 * m + 1] = make_float2(q.z, q.w);
       }
 #pragma unroll
-      for(int k = 0; k < PL::V; k++) r[k] = mid_product<MID>(r[k], b[k]);
+      for(int k = 0; k < PL::V; k++) r[k] = Op::apply(r[k], b[k]);
+   } else {
+#pragma unroll
+      for(int k = 0; k < PL::V; k++) r[k] = Op::apply(r[k], make_float2(0.f, 0.f));
    }
 }
 
 // The lane's V filter values one at a time, value k at voff + k*kstep (the
-// 2D column kernels: one image row apart).
+// reference's bperm layout: T values apart; the 2D column kernels: one image
+// row apart).
 template<class PL, int MID>
 __device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t kstep)
 {
-   if constexpr(MID != MID_NONE) {
+   using Op = MidOf<MID>;
+   if constexpr(Op::reads_filter) {
       float2 b[PL::V];
 #pragma unroll
       for(int k = 0; k < PL::V; k++) b[k] = f.ld2(voff, k * kstep);
 #pragma unroll
-      for(int k = 0; k < PL::V; k++) r[k] = mid_product<MID>(r[k], b[k]);
+      for(int k = 0; k < PL::V; k++) r[k] = Op::apply(r[k], b[k]);
+   } else {
+#pragma unroll
+      for(int k = 0; k < PL::V; k++) r[k] = Op::apply(r[k], make_float2(0.f, 0.f));
    }
 }
 

@@ -43,7 +43,12 @@ extern "C" {
                                        (fufft_conv2d_r2_noalloc_f32)            */
 
 /* ---- enums ----------------------------------------------------------------- */
-/* mid operation between forward and inverse (Mid policies, fufft.cuh:616-650) */
+/* mid operation between forward and inverse (Mid policies, fufft.cuh:616-650).
+ * Each id names a policy struct registered in the library's kernel sources
+ * (FUFFT_MID_POLICIES in fufft_amd/csrc/fufft_plan.hpp): as in the reference,
+ * a new fusion costs a struct, plus its id here; every call that takes `mid`
+ * then accepts it.  fufft_mid_reads_filter tells a caller of a given build
+ * which ids exist and which read a filter. */
 #define FUFFT_MID_MUL   0   /* A * B        convolution  (MidMultiply)      */
 #define FUFFT_MID_CONJ  1   /* A * conj(B)  correlation  (MidConjMultiply)  */
 #define FUFFT_MID_NONE  2   /* round trip, N * input      (MidNothing)       */
@@ -92,6 +97,11 @@ int fufft_supported(int64_t n, int variant);
  * variant it returns.  No reference counterpart (the reference's caller
  * picks the kernel template). */
 int fufft_fastest_variant(int64_t n, int layout);
+/* 1 if `mid` is a mid policy of this build that reads a filter (the filter
+ * pointer must then be valid), 0 if it is one that reads none (the filter
+ * pointer may be NULL), FUFFT_ERR_INVALID if no policy has that id.  No
+ * reference counterpart (there a policy is a type the caller instantiates). */
+int fufft_mid_reads_filter(int mid);
 
 /* ---- host planning (no GPU needed) ------------------------------------------
  * Pass plan in DIF order: lead radix first, then radix 16 (or 8); returns the

@@ -18,10 +18,14 @@
 
 namespace fufft {
 
-// Mid policies: the reference's functor types, reduced to the C ABI enum.
+// Mid policies: the reference's functor types, reduced to the C ABI ids (the
+// device side of each is a struct of the library's kernel sources).
 struct MidMultiply     { static constexpr int id = FUFFT_MID_MUL; };
 struct MidConjMultiply { static constexpr int id = FUFFT_MID_CONJ; };
 struct MidNothing      { static constexpr int id = FUFFT_MID_NONE; };
+// 1: the policy `mid` reads a filter; 0: it reads none; FUFFT_ERR_INVALID: no such policy
+inline int mid_reads_filter(int mid) { return fufft_mid_reads_filter(mid); }
+template<class Mid> inline bool reads_filter() { return fufft_mid_reads_filter(Mid::id) == 1; }
 
 enum class Variant : int { V16 = FUFFT_V16, R8 = FUFFT_R8, Auto = FUFFT_AUTO };
 

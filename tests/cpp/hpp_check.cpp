@@ -23,6 +23,8 @@ int main()
    if(!fufft::supported(n) || fufft::supported(100)) return 7;
    if(fufft::fastest_variant(4096) != fufft::Variant::V16 || fufft::fastest_variant(512) != fufft::Variant::R8 ||
       fufft::fastest_variant(4096, FUFFT_LAYOUT_DR) != fufft::Variant::R8) return 14;
+   if(!fufft::reads_filter<fufft::MidMultiply>() || !fufft::reads_filter<fufft::MidConjMultiply>() ||
+      fufft::reads_filter<fufft::MidNothing>() || fufft::mid_reads_filter(3) != FUFFT_ERR_INVALID) return 15;
    if(fufft::c2c<FUFFT_INVERSE>(nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID) return 8;
    if(fufft::plan_filter_device(nullptr, nullptr, n) != FUFFT_ERR_INVALID) return 9;
    if(fufft::pipeline_timed<fufft::MidMultiply>(nullptr, nullptr, nullptr, n, 1, nullptr, 0) != FUFFT_ERR_INVALID) return 10;

@@ -226,6 +226,35 @@ def test_status_codes_without_gpu_calls():
     assert "scratch" in L.fufft_status_string(ff.ERR_SCRATCH).decode()
 
 
+def test_mid_policy_registry():
+    """The mid ids the library registers (MidMultiply, MidConjMultiply,
+    MidNothing: fufft.cuh:616-650) and which read a filter; an id no policy
+    has is refused by every call that takes one, before any device work, and
+    by the binding whether given as a name or an id."""
+    import fufft_amd as ff
+    L = ff.lib
+    assert [L.fufft_mid_reads_filter(m) for m in (0, 1, 2)] == [1, 1, 0]
+    for bad in (-1, 3, 99):
+        assert L.fufft_mid_reads_filter(bad) == ff.ERR_INVALID
+    assert [ff.mid_reads_filter(m) for m in ("mul", "conj", "none")] == [True, True, False]
+    assert ff.mid_reads_filter(ff.MID["conj"]) is True
+    with pytest.raises(ff.FufftError):
+        ff.mid_reads_filter(3)
+    with pytest.raises(ValueError, match="mid must be"):
+        ff.mid_reads_filter("product")
+    fake = 1 << 20
+    # a filter pointer may be NULL exactly where the policy reads none
+    assert L.fufft_conv_f32(fake, None, 0, fake, 4096, 1, 0, 2, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_f32(fake, None, 0, fake, 4096, 1, 1, 2, 0, None) == ff.ERR_INVALID
+    for mid in (3, -1):
+        assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, 1, mid, 2, 0, None) == ff.ERR_INVALID
+        assert L.fufft_apply_f32(fake, 4096, fake, 0, fake + 16, 4096, 1, mid, 2, 0, None) == ff.ERR_INVALID
+        assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 4096, 1, 64, mid, 1, 0, None) == ff.ERR_INVALID
+        assert L.fufft_conv_large_f32(fake, fake, 0, 32768, 1, mid, None) == ff.ERR_INVALID
+        assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 512, 1, mid, 0, None) == ff.ERR_INVALID
+        assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake + 16, 512, 512, 1, mid, 0, None) == ff.ERR_INVALID
+
+
 def test_cpp_mirror_header_builds_and_runs(tmp_path):
     """include/fufft/fufft.hpp compiles with g++ and links against the library."""
     import shutil
