@@ -391,6 +391,44 @@ def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64, var
     return secs / steps, rel_l2(got, want), float(per_sig.max())
 
 
+def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="v16"):
+    """int16-BFP conv in the reference's own format (fufft_conv_bfp16_scaled: one
+    fp32 scale per transform, an int16 filter with one scale), on the same
+    Gaussian x 10^u input as bench_bfp, quantised by the reference's rule."""
+    batch = pts // n
+    rng = np.random.default_rng(seed)
+    q = np.empty(2 * pts, dtype=np.int16)
+    sc = np.empty(batch, dtype=np.float32)
+    chunk = max(1, (1 << 22) // n)
+    x16 = None
+    for b0 in range(0, batch, chunk):
+        b1 = min(batch, b0 + chunk)
+        s = (10.0 ** rng.uniform(-3, 3, (b1 - b0, 1))).astype(np.float32)
+        xc = (rng.standard_normal((b1 - b0, n), dtype=np.float32) * s
+              + 1j * (rng.standard_normal((b1 - b0, n), dtype=np.float32) * s)).astype(np.complex64)
+        if b0 == 0:
+            x16 = xc[:16].copy()
+        q[2 * n * b0: 2 * n * b1], sc[b0:b1] = ff.bfp_scaled_quantize(xc, n)
+    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+    fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS), n)
+    dq, ds = torch.from_numpy(q).to(dev), torch.from_numpy(sc).to(dev)
+    dfq, dfs = torch.from_numpy(fq).to(dev), torch.from_numpy(fs).to(dev)
+    qo, so = torch.empty_like(dq), torch.empty_like(ds)
+    del q
+
+    def step():
+        ff.conv_bfp16_scaled(dq, ds, dfq, dfs, qo, so, n=n, batch=batch, variant=variant, stream=stream)
+
+    step()
+    torch.cuda.synchronize()
+    got = ff.bfp_scaled_dequantize(qo[: 32 * n].cpu().numpy(), so[:16].cpu().numpy(), n).reshape(16, n)
+    want = np.fft.ifft(np.fft.fft(x16.astype(np.complex128), axis=1)
+                       * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    secs = time_launches(torch, step, steps, warmup, stream, SETTLE_S)
+    del dq, ds, dfq, dfs, qo, so
+    return secs / steps, rel_l2(got, want)
+
+
 def usable_cores():
     """(cores, affinity, quota): host cores this process may run on -- its CPU
     affinity (os.sched_getaffinity), capped by a cgroup CPU quota where one is
@@ -670,6 +708,16 @@ def main():
                     sys.exit(1)
                 bfp[str(s)]["block_n"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
                                           "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst}
+            # the reference's own format (fp32 scale per transform, int16 filter) at its plan
+            a, r = bench_bfp_scaled(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 199 + s)
+            if not r <= 1e-4:
+                print(json.dumps({"error": f"BFP (reference format) accuracy check failed at N={s}: "
+                                           f"rel L2 {r:.3e}"}))
+                sys.exit(1)
+            bfp[str(s)]["reference_format"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                                               "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                                               "rel_l2_vs_fp64_unquantised": r, "variant": "v16",
+                                               "filter": "int16, digit order, one scale"}
         line["bfp"] = bfp
 
     large = {}

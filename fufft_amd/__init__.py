@@ -88,6 +88,9 @@ def _load() -> C.CDLL:
         "fufft_bfp_quantize": ([vp, i64, i64, vp, vp], i32),
         "fufft_bfp_dequantize": ([vp, vp, i64, i64, vp], i32),
         "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, i32, i32, vp], i32),
+        "fufft_conv_bfp16_scaled": ([vp, vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_bfp_scaled_quantize": ([vp, i64, i64, vp, vp], i32),
+        "fufft_bfp_scaled_dequantize": ([vp, vp, i64, i64, vp], i32),
         "fufft_large_plan": ([i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
         "fufft_large_digit_order": ([i64, C.POINTER(C.c_int32)], i32),
         "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
@@ -132,6 +135,7 @@ if torch is not None:
         "real": (torch.float32,),
         "bfp": (torch.int16, torch.int32),                    # int16 pairs, 4 bytes per point
         "exp": (torch.int8, torch.uint8),
+        "scale": (torch.float32,),
         "words": (torch.int32,),
     }
 
@@ -390,6 +394,22 @@ def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int 
                                LAYOUT[layout], _stream(stream)), "fufft_conv_bfp16")
 
 
+def conv_bfp16_scaled(qin, sin, qfilt, sfilt, qout, sout, n: int, batch: int, filt_stride: int = 0,
+                      mid: str = "mul", variant: str = "auto", stream=None) -> None:
+    """int16-BFP fused conv in the reference's own format (fufft_pipeline_v16_bfp):
+    one fp32 scale per transform (sin / sout, batch floats), the filter as
+    int16 pairs in digit order with one fp32 scale per filter."""
+    qb = 4 * n * batch
+    nf = _count(filt_stride, n, batch, "qfilt") if batch else 0
+    reads = mid_reads_filter(mid)
+    fq = None if (qfilt is None and not reads) else (qfilt, "qfilt", 4 * n * nf, "bfp")
+    fs = None if (sfilt is None and not reads) else (sfilt, "sfilt", 4 * nf, "scale")
+    pq, ps, pfq, pfs, pqo, pso = _ptrs((qin, "qin", qb, "bfp"), (sin, "sin", 4 * batch, "scale"), fq, fs,
+                                       (qout, "qout", qb, "bfp"), (sout, "sout", 4 * batch, "scale"))
+    check(lib.fufft_conv_bfp16_scaled(pq, ps, pfq, pfs, filt_stride, pqo, pso, n, batch, _mid(mid),
+                                      VARIANT[variant], _stream(stream)), "fufft_conv_bfp16_scaled")
+
+
 def c2c(inp, out, n: int, batch: int, direction: int = FORWARD, variant: str = "auto",
         stream=None) -> None:
     """Natural-order batched C2C: forward, or the unnormalised inverse."""
@@ -557,6 +577,28 @@ def bfp_quantize(x: np.ndarray, block: int = BFP_BLOCK) -> tuple[np.ndarray, np.
     check(lib.fufft_bfp_quantize(src.ctypes.data, src.size, block, q.ctypes.data, e.ctypes.data),
           "fufft_bfp_quantize")
     return q, e[: src.size // block]
+
+
+def bfp_scaled_quantize(x: np.ndarray, n: int) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's codec (fufft_bfp_scaled_quantize): int16 pairs and one
+    fp32 scale per transform of n points."""
+    src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
+    if src.size % n:
+        raise ValueError(f"{src.size} points are not whole transforms of {n}")
+    q = np.empty(2 * src.size, dtype=np.int16)
+    sc = np.empty(max(src.size // n, 1), dtype=np.float32)
+    check(lib.fufft_bfp_scaled_quantize(src.ctypes.data, n, src.size // n, q.ctypes.data, sc.ctypes.data),
+          "fufft_bfp_scaled_quantize")
+    return q, sc[: src.size // n]
+
+
+def bfp_scaled_dequantize(q: np.ndarray, scale: np.ndarray, n: int) -> np.ndarray:
+    count = q.size // (2 * n)
+    x = np.empty(count * n, dtype=np.complex64)
+    check(lib.fufft_bfp_scaled_dequantize(np.ascontiguousarray(q).ctypes.data,
+                                          np.ascontiguousarray(scale, dtype=np.float32).ctypes.data, n, count,
+                                          x.ctypes.data), "fufft_bfp_scaled_dequantize")
+    return x
 
 
 def bfp_dequantize(q: np.ndarray, e: np.ndarray, block: int = BFP_BLOCK) -> np.ndarray:

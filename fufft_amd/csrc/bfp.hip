@@ -174,9 +174,21 @@ __device__ __forceinline__ void bfp_body(const BfpParams& p)
 
    const Buf qb(static_cast<const char*>(p.qin) + (size_t)tu * N * 4, N * 4);
    float2 r[V];
+   uint32_t wd[V];
+#pragma unroll
+   for(int q = 0; q < V; q++) wd[q] = qb.ldu<POL_NT>((uint32_t)L * 4u, q * T * 4);
+   // Radix 16 at N = 2048 and 4096: every signal load goes out before the
+   // first dequantisation (the empty asm reads them all).  Left to itself the
+   // scheduler interleaves loads and dequantisation, 5-8 waits among the 16
+   // loads; issued together: +3% / +1.7% (396 -> 408, 377 -> 384 Gpt/s, same
+   // box).  At N = 16384 it costs 3.7% and elsewhere it is even.
+   if constexpr(V == 16 && N >= 2048 && N <= 4096) {
+#pragma unroll
+      for(int q = 0; q < V; q++) asm volatile("" :: "v"(wd[q]));
+   }
 #pragma unroll
    for(int q = 0; q < V; q++) {
-      const uint32_t word = qb.ldu<POL_NT>((uint32_t)L * 4u, q * T * 4);
+      const uint32_t word = wd[q];
       int e;
       if constexpr(BIG) {
          e = __builtin_amdgcn_readlane(ein_lane, q);
@@ -303,6 +315,193 @@ static hipError_t launch_bfp_nv(int layout, const BfpParams& p, hipStream_t s)
    if(layout == LAYOUT_XOR)
       return with_mid(p.mid, [&](auto m) { return launch_bfp_one<N, V, LAYOUT_XOR, decltype(m)::value>(p, s); });
    return with_mid(p.mid, [&](auto m) { return launch_bfp_one<N, V, bfp_lds_layout(N, V), decltype(m)::value>(p, s); });
+}
+
+// ---- the reference's own format: one fp32 scale per transform -------------------------
+// fufft_pipeline_v16_bfp (fufft.cuh:1614-1701) as its CPU transcription
+// states it (kernel_v16_bfp, bfp_quantize; verify_kernel.cpp:1092-1135): a
+// transform's points are int16 pairs with one fp32 scale, x = q * scale; the
+// filter is int16 pairs in digit order with one fp32 scale per filter,
+// b = qb * scale_b, multiplied in at the M = 1 boundary; the result's scale is
+// mx / 32767 with mx = max(absmax of the transform's fp32 result, 1e-30), and
+// q = rint(clamp(v * (32767 / mx), -32767, 32767)).  Between the codecs runs
+// the fp32 pipeline of conv1d.hip, so with the reference's base twiddles the
+// words and scales are the transcription's bit for bit.  The abs-max is exact
+// in any order: a transform's lanes reduce it in registers (DPP and permlane
+// moves, the bits of non-negative floats compared as unsigned), and the
+// wavefronts of a transform wider than 64 lanes meet in one LDS word.
+
+// maximum over each group of T lanes (T = 16, 32: the lanes of one transform
+// inside a wavefront; T >= 64: the whole wavefront), in every lane
+template<int T>
+__device__ __forceinline__ uint32_t lanes_max(uint32_t x)
+{
+   static_assert(T >= 16, "a transform fills at least one row of 16 lanes");
+   x = umax(x, dpp_u<0xB1>(x));            // quad_perm [1,0,3,2]
+   x = umax(x, dpp_u<0x4E>(x));            // quad_perm [2,3,0,1]
+   x = umax(x, dpp_u<0x124>(x));           // row_ror:4
+   x = umax(x, dpp_u<0x128>(x));           // row_ror:8: the row of 16
+   if constexpr(T >= 32) x = swap_max16(x);
+   if constexpr(T >= 64) x = swap_max32(x);
+   return x;
+}
+
+template<int N, int V, int LAYOUT, int MID>
+__global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
+bfp_scaled_kernel(const BfpScaledParams p)
+{
+   using PL = Plan<N, V>;
+   using LD = Lds<V, LAYOUT>;
+   using Op = MidOf<MID>;
+   constexpr int T     = PL::T;
+   constexpr int CPB   = bfp_cpb(T);
+   constexpr int SLOT  = LD::size(N);
+   constexpr int LANES = T < 64 ? 64 : T;
+   constexpr int TPW   = T < 64 ? 64 / T : 1;     // transforms per wavefront
+
+   extern __shared__ float2 lds[];
+   const int slot = threadIdx.x / T;
+   const int L    = threadIdx.x % T;
+   const uint32_t t = blockIdx.x * CPB + slot;
+   if(t >= p.ntrans) return;                      // T > 64 => CPB == 1: whole group leaves
+   // the wavefront's first transform and this lane's point offset from it
+   const uint32_t t0 = (T >= 64) ? (uint32_t)uniform((int)t)
+                                 : blockIdx.x * CPB + (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
+   const uint32_t lane_pos = (T >= 64) ? (uint32_t)L : (t - t0) * N + L;
+   const uint32_t tu = (T >= 64) ? t0 : t;        // uniform where a wavefront is one transform
+
+   float2* A = lds + slot * SLOT;
+   // wavefronts of one transform (T > 64) meet in this word, zeroed here and
+   // ordered before the atomics by the exchanges' workgroup barriers
+   uint32_t* amax = reinterpret_cast<uint32_t*>(lds + CPB * SLOT);
+   if constexpr(T > 64) {
+      if(L == 0) amax[0] = 0u;
+   }
+   Twiddles<PL> tw;
+   tw.load(p.tw, L);
+
+   const float sa = p.sin[tu];
+   const Buf qb(static_cast<const char*>(p.qin) + (size_t)t0 * N * 4, TPW * N * 4);
+   // every signal load goes out before the first dequantisation (the empty
+   // asm reads them all): left to itself the scheduler interleaves loads and
+   // multiplies with up to 12 waits among the 16 loads, and radix 16 at
+   // N = 1024 / 8192 / 16384 runs 367 / 232 / 229 Gpt/s against 426 / 282 /
+   // 262 (same box; other plans even)
+   float2 r[V];
+   uint32_t wd[V];
+#pragma unroll
+   for(int q = 0; q < V; q++) wd[q] = qb.ldu<POL_NT>(lane_pos * 4u, q * T * 4);
+#pragma unroll
+   for(int q = 0; q < V; q++) asm volatile("" :: "v"(wd[q]));
+#pragma unroll
+   for(int q = 0; q < V; q++)
+      r[q] = make_float2((float)(int)(int16_t)(wd[q] & 0xffffu) * sa, (float)((int)wd[q] >> 16) * sa);
+
+   KeptChain<PL> kc;
+   forward_dif<PL, LD, LANES, 64, KEEP_STORE>(r, A, L, tw, kc);
+   if constexpr(Op::reads_filter) {
+      // slots L*V .. L*V + V - 1, four int16 pairs per 16-byte load
+      const uint32_t fi = modulo_count(t, p.fcount);
+      const float sb = p.sfilt[fi];
+      const Buf fb(p.qfilt, p.fcount * (uint32_t)N * 4u);
+      const uint32_t fo = (fi * N + (uint32_t)L * V) * 4u;
+#pragma unroll
+      for(int m = 0; m < V / 4; m++) {
+         const float4 w4 = fb.ld4(fo, m * 16);
+         const uint32_t w[4] = { __builtin_bit_cast(uint32_t, w4.x), __builtin_bit_cast(uint32_t, w4.y),
+                                 __builtin_bit_cast(uint32_t, w4.z), __builtin_bit_cast(uint32_t, w4.w) };
+#pragma unroll
+         for(int i = 0; i < 4; i++) {
+            const float2 b = make_float2((float)(int)(int16_t)(w[i] & 0xffffu) * sb, (float)((int)w[i] >> 16) * sb);
+            r[4 * m + i] = Op::apply(r[4 * m + i], b);
+         }
+      }
+   } else {
+#pragma unroll
+      for(int k = 0; k < V; k++) r[k] = Op::apply(r[k], make_float2(0.f, 0.f));
+   }
+   inverse_dit<PL, LD, LANES, 64, KEEP_USE>(r, A, L, tw, kc);
+
+   // the transform's abs-max
+   float m = 0.0f;
+#pragma unroll
+   for(int q = 0; q < V; q++) m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fabsf(r[q].x), __builtin_fabsf(r[q].y)));
+   uint32_t x = lanes_max<T>(__builtin_bit_cast(uint32_t, m));
+   if constexpr(T > 64) {
+      if((threadIdx.x & 63) == 0) atomicMax(amax, x);
+      __syncthreads();                            // CPB == 1: every wavefront is this transform's
+      x = amax[0];
+   }
+   const float mx  = __builtin_fmaxf(__builtin_bit_cast(float, x), 1e-30f);
+   const float inv = 32767.0f / mx;
+   // Adding 1.5 * 2^23 to a value of magnitude <= 32767 rounds it to the
+   // nearest integer, ties to even, into the low mantissa bits; the low
+   // halfwords of re and im make the output word
+   const Buf ob(static_cast<char*>(p.qout) + (size_t)t0 * N * 4, TPW * N * 4);
+#pragma unroll
+   for(int q = 0; q < V; q++) {
+      const float yr = __builtin_fminf(__builtin_fmaxf(r[q].x * inv, -32767.0f), 32767.0f) + 12582912.0f;
+      const float yi = __builtin_fminf(__builtin_fmaxf(r[q].y * inv, -32767.0f), 32767.0f) + 12582912.0f;
+      const uint32_t word = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, yi),
+                                                  __builtin_bit_cast(uint32_t, yr), 0x05040100u);
+      ob.stu<POL_NT>(word, lane_pos * 4u, q * T * 4);
+   }
+   if(L == 0) p.sout[t] = mx / 32767.0f;
+}
+
+template<int N, int V, int MID>
+static hipError_t launch_bfp_scaled_one(const BfpScaledParams& p, hipStream_t s)
+{
+   constexpr int T = N / V, CPB = bfp_cpb(T);
+   constexpr int LAYOUT = bfp_lds_layout(N, V);
+   const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2) + (T > 64 ? 4 : 0);
+   const void* k = reinterpret_cast<const void*>(&bfp_scaled_kernel<N, V, LAYOUT, MID>);
+   if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
+   static std::atomic<uint64_t> lds_ok{0};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
+   const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
+   BfpScaledParams arg = p;
+   void* argv[] = { &arg };
+   return hipLaunchKernel(k, grid, block, argv, shm, s);
+}
+
+template<int N, int V>
+static hipError_t launch_bfp_scaled_nv(const BfpScaledParams& p, hipStream_t s)
+{
+   return with_mid(p.mid, [&](auto m) { return launch_bfp_scaled_one<N, V, decltype(m)::value>(p, s); });
+}
+
+bool bfp_scaled_supported(int n, int v)
+{
+   if(v == 8)  return n >= 512 && n <= 8192 && (n & (n - 1)) == 0;
+   if(v == 16) return n >= 256 && n <= 16384 && (n & (n - 1)) == 0;
+   return false;
+}
+
+hipError_t launch_bfp_scaled(int n, int v, const BfpScaledParams& p, hipStream_t s)
+{
+   if(v == 8) {
+      switch(n) {
+         case 512:  return launch_bfp_scaled_nv<512, 8>(p, s);
+         case 1024: return launch_bfp_scaled_nv<1024, 8>(p, s);
+         case 2048: return launch_bfp_scaled_nv<2048, 8>(p, s);
+         case 4096: return launch_bfp_scaled_nv<4096, 8>(p, s);
+         case 8192: return launch_bfp_scaled_nv<8192, 8>(p, s);
+         default:   break;
+      }
+   } else if(v == 16) {
+      switch(n) {
+         case 256:   return launch_bfp_scaled_nv<256, 16>(p, s);
+         case 512:   return launch_bfp_scaled_nv<512, 16>(p, s);
+         case 1024:  return launch_bfp_scaled_nv<1024, 16>(p, s);
+         case 2048:  return launch_bfp_scaled_nv<2048, 16>(p, s);
+         case 4096:  return launch_bfp_scaled_nv<4096, 16>(p, s);
+         case 8192:  return launch_bfp_scaled_nv<8192, 16>(p, s);
+         case 16384: return launch_bfp_scaled_nv<16384, 16>(p, s);
+         default:    break;
+      }
+   }
+   return hipErrorInvalidValue;
 }
 
 bool bfp_supported(int n, int v)

@@ -121,6 +121,23 @@ struct BfpParams {
 bool       bfp_supported(int n, int v);
 hipError_t launch_bfp(int n, int v, int layout, const BfpParams& p, hipStream_t s);
 
+// the reference's own format: one fp32 scale per transform, an int16 filter
+struct BfpScaledParams {
+   const void*   qin;      // int16 pairs
+   const float*  sin;      // one scale per transform
+   const void*   qfilt;    // int16 pairs, digit order
+   const float*  sfilt;    // one scale per filter
+   void*         qout;
+   float*        sout;     // one scale per transform
+   const float2* tw;
+   uint32_t      ntrans;
+   uint32_t      fcount;   // transform t uses filter (t % fcount)
+   int32_t       mid;
+};
+
+bool       bfp_scaled_supported(int n, int v);
+hipError_t launch_bfp_scaled(int n, int v, const BfpScaledParams& p, hipStream_t s);
+
 // ---- four-step outer levels (large.hip) -------------------------------------------
 // one radix-16 level (stride M) over a batch of n-point transforms, in place;
 // dit = false: forward DIF level, dit = true: inverse DIT level

@@ -281,6 +281,31 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
                      int64_t batch, int64_t block, int mid, int variant, int layout,
                      void* stream);
 
+/* ---- int16 BFP in the reference's own format -----------------------------------
+ * fufft_pipeline_v16_bfp(aq, a_scale, bq, b_scale, outq, out_scale)
+ * (fufft.cuh:1614-1701; its CPU transcription kernel_v16_bfp and bfp_quantize,
+ * verify_kernel.cpp:1092-1135): int16 pairs as above with one fp32 scale per
+ * transform, value = q * scale; the filter is int16 pairs in digit order (the
+ * fp32 filter of fufft_plan_filter_f32, FUFFT_LAYOUT_DR, for the same variant,
+ * quantised by fufft_bfp_scaled_quantize) with one fp32 scale per filter.  On
+ * output, per transform: mx = max(abs-max of the fp32 result, 1e-30),
+ * q = rint(clamp(v * (32767 / mx), -32767, 32767)), scale = mx / 32767.
+ * filt_stride 0: one filter (qfilt n points, sfilt one scale) for the batch;
+ * n: one per transform (n*batch points, batch scales).  The fp32 pipeline in
+ * between is fufft_conv_f32's, so with FUFFT_TWIDDLES_REFERENCE and
+ * FUFFT_V16 the words and scales equal the reference transcription's.
+ * FUFFT_V16 256..16384, FUFFT_R8 512..8192 (the reference: FUFFT_V16).
+ * qin == qout and sin == sout are allowed.  qin, qout, sin, sout, sfilt
+ * 4-byte aligned, qfilt 16-byte aligned (FUFFT_ERR_ALIGN). */
+int fufft_conv_bfp16_scaled(const void* qin, const float* sin, const void* qfilt,
+                            const float* sfilt, int64_t filt_stride, void* qout, float* sout,
+                            int64_t n, int64_t batch, int mid, int variant, void* stream);
+/* host codec of that format (bfp_quantize, verify_kernel.cpp:1092-1105):
+ * count transforms of n points, x interleaved re/im, one scale per transform */
+int fufft_bfp_scaled_quantize(const float* x, int64_t n, int64_t count, int16_t* q, float* scale);
+int fufft_bfp_scaled_dequantize(const int16_t* q, const float* scale, int64_t n, int64_t count,
+                                float* x);
+
 /* ---- HBM stream ceiling (measurement) ------------------------------------------------
  * Copies `bytes` (a multiple of 16; 16-byte aligned pointers; in != out) with
  * the buffer instructions the conv kernels use: each 256-lane workgroup moves

@@ -257,6 +257,38 @@ def bfp_conv(q, e, filt, n: int, plan: Plan, filt_stride: int = 0, mid: str = "m
     return qo, eo
 
 
+# The reference's own BFP format: one fp32 scale per transform.  A restatement
+# of bfp_quantize and kernel_v16_bfp (verify_kernel.cpp:1092-1135) in numpy
+# float32 arithmetic (IEEE products and quotients, round to nearest even):
+#   mx = max(abs-max of re and im, 1e-30); inv = 32767 / mx;
+#   q = rint(clamp(x * inv, -32767, 32767)); scale = mx / 32767; x = q * scale.
+# The conv dequantises signal and filter, runs the fp32 pipeline (conv above,
+# whose multiply takes the dequantised filter value) and quantises the result
+# per transform.  Pinned bit for bit to the compiled reference in
+# tests/test_oracle_pins.py and by tests/golden/bfp_scaled_*.npz.
+
+def bfp_scaled_quantize(x, n: int):
+    x = _c64(x).reshape(-1, n)
+    parts = x.view(np.float32).reshape(x.shape[0], 2 * n)
+    mx = np.maximum(np.abs(parts).max(axis=1), np.float32(1e-30)).astype(np.float32)
+    inv = (np.float32(32767.0) / mx).astype(np.float32)
+    y = np.clip(parts * inv[:, None], np.float32(-32767.0), np.float32(32767.0))
+    return np.rint(y).astype(np.int16).reshape(-1), (mx / np.float32(32767.0)).astype(np.float32)
+
+
+def bfp_scaled_dequantize(q, scale, n: int) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int16).reshape(-1, 2 * n).astype(np.float32)
+    s = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1, 1)
+    return np.ascontiguousarray((q * s).astype(np.float32)).view(np.complex64).reshape(-1)
+
+
+def bfp_scaled_conv(q, scale, fq, fscale, n: int, plan: Plan, filt_stride: int = 0, mid: str = "mul",
+                    tw: int = TW_TABLE):
+    a = bfp_scaled_dequantize(q, scale, n)
+    f = bfp_scaled_dequantize(fq, fscale, n) if fq is not None else np.zeros(n, np.complex64)
+    return bfp_scaled_quantize(conv(a, f, n, plan, filt_stride=filt_stride, mid=mid, tw=tw), n)
+
+
 # ---- fp64 ------------------------------------------------------------------------------------
 
 def conv_spec_f64(a, spec_nat, n: int, spec_stride: int = 0, mid: str = "mul") -> np.ndarray:

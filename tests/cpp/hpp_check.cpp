@@ -26,6 +26,8 @@ int main()
    if(!fufft::reads_filter<fufft::MidMultiply>() || !fufft::reads_filter<fufft::MidConjMultiply>() ||
       fufft::reads_filter<fufft::MidNothing>() || fufft::mid_reads_filter(3) != FUFFT_ERR_INVALID) return 15;
    if(fufft::c2c<FUFFT_INVERSE>(nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID) return 8;
+   if(fufft::pipeline_bfp_scaled(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID)
+      return 16;
    if(fufft::plan_filter_device(nullptr, nullptr, n) != FUFFT_ERR_INVALID) return 9;
    if(fufft::pipeline_timed<fufft::MidMultiply>(nullptr, nullptr, nullptr, n, 1, nullptr, 0) != FUFFT_ERR_INVALID) return 10;
    if(fufft::plan_filter_large_device(nullptr, nullptr, 4096) != FUFFT_ERR_UNSUPPORTED) return 11;

@@ -50,6 +50,11 @@ def replay(case: dict) -> dict:
         mid_v = int(case["mid_v"]) if "mid_v" in case else 16
         plan = O.large_plan(lout, mid, mid_v, ref=True)
         return {"out": O.conv(case["a"], case["bdr"], n, plan, filt_stride=n, tw=O.TW_LIBM)}
+    if kind == "bfp_scaled":
+        n = int(case["n"])
+        oq, osc = O.bfp_scaled_conv(case["aq"], case["asc"], case["bq"], case["bsc"], n, O.ref_plan(n, 16),
+                                    tw=O.TW_LIBM)
+        return {"oq": oq, "osc": osc}
     if kind == "c2c_stockham":
         # the reference's Stockham C2C rounds in a different order from this
         # build's DIF + permutation: no bit-exact outputs; test_oracle_c2c

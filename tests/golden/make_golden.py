@@ -3,7 +3,8 @@
 Run in the build container, where /root/reference exists and `make -C oracle
 ref` has built oracle/_ref/libfufft_ref.so:
 
-    python -m tests.golden.make_golden
+    python -m tests.golden.make_golden              # every fixture
+    python -m tests.golden.make_golden bfp_scaled   # only bfp_scaled_n*.npz
 """
 from __future__ import annotations
 
@@ -22,14 +23,41 @@ def _lead_count(n, v):
     return (rads[0] if rads[0] != v else 1), rads.count(v)
 
 
+def _save(name, **kw):
+    np.savez_compressed(HERE / f"{name}.npz", **kw)
+
+
+def bfp_scaled(R) -> None:
+    """The reference's own BFP format (kernel_v16_bfp, verify_kernel.cpp:1107-1135):
+    int16 pairs and one fp32 scale per transform in and out, a shared int16
+    filter with one scale, at the sizes of BASELINE config 3."""
+    rng = np.random.default_rng(20261203)
+    for n in (512, 4096):
+        batch = 4
+        x = (rng.standard_normal((batch, n)) + 1j * rng.standard_normal((batch, n))).astype(np.complex64)
+        x = (x * (10.0 ** rng.uniform(-3, 3, (batch, 1)))).astype(np.complex64)
+        aq, asc = np.empty(2 * n * batch, np.int16), np.empty(batch, np.float32)
+        for t in range(batch):
+            xt = np.ascontiguousarray(x[t])
+            asc[t] = R.ref_vk_bfp_quantize(xt.ctypes.data, n, aq[2 * n * t:].ctypes.data)
+        b = _cu(rng, (1, n))[0] / n
+        bdr = np.ascontiguousarray(b[O.mixedrev(O.kernel_plan(n, 16))])
+        bq = np.empty(2 * n, np.int16)
+        bsc = np.float32(R.ref_vk_bfp_quantize(bdr.ctypes.data, n, bq.ctypes.data))
+        lead, nrv = _lead_count(n, 16)
+        oq, osc = np.empty_like(aq), np.empty(batch, np.float32)
+        R.ref_vk_v16_bfp(n, lead, nrv, aq.ctypes.data, asc.ctypes.data, bq.ctypes.data, float(bsc),
+                         oq.ctypes.data, osc.ctypes.data, batch)
+        _save(f"bfp_scaled_n{n}", kind="bfp_scaled", n=n, aq=aq, asc=asc, bq=bq, bsc=np.array([bsc]),
+              oq=oq, osc=osc)
+
+
 def main() -> None:
     R = O.load_ref()
     if R is None:
         raise SystemExit("oracle/_ref/libfufft_ref.so is not built (needs /root/reference)")
     rng = np.random.default_rng(20261201)
-
-    def save(name, **kw):
-        np.savez_compressed(HERE / f"{name}.npz", **kw)
+    save = _save
 
     for n in (64, 512, 1024):
         batch = 2
@@ -129,6 +157,15 @@ def main() -> None:
     save("fourstep_n8192_mid512_r8", kind="fourstep", n=n, lout=1, mid=mid, mid_v=8, a=a, bdr=bdr,
          out=A.reshape(-1))
 
+    bfp_scaled(R)
+
 
 if __name__ == "__main__":
-    main()
+    import sys
+    if sys.argv[1:] == ["bfp_scaled"]:           # only the reference-format BFP fixtures
+        ref = O.load_ref()
+        if ref is None:
+            raise SystemExit("oracle/_ref/libfufft_ref.so is not built (needs /root/reference)")
+        bfp_scaled(ref)
+    else:
+        main()

@@ -232,3 +232,23 @@ def test_set_twiddles_rejects_bad_source(dev):
     with pytest.raises(ff.FufftError):
         ff.check(ff.lib.fufft_set_twiddles(0, 5), "fufft_set_twiddles")
     assert ff.get_twiddles() == before
+
+
+@pytest.mark.parametrize("name", ["bfp_scaled_n512", "bfp_scaled_n4096"])
+def test_bfp_scaled_equals_reference_on_golden_fixture(ref_tw, name):
+    """The reference's own BFP format at its plan (radix 16): words and scales
+    equal the compiled reference's kernel_v16_bfp (verify_kernel.cpp:1107-1135)
+    on the golden fixtures."""
+    import torch
+    import fufft_amd as ff
+    dev = ref_tw
+    case = _golden()[name]
+    n = int(case["n"])
+    batch = case["asc"].size
+    print(f"case golden {name}", flush=True)
+    dq, ds = to_dev(case["aq"], dev), to_dev(case["asc"], dev)
+    qo, so = torch.empty_like(dq), torch.empty_like(ds)
+    ff.conv_bfp16_scaled(dq, ds, to_dev(case["bq"], dev), to_dev(case["bsc"], dev), qo, so, n=n, batch=batch,
+                         variant="v16")
+    assert np.array_equal(host(qo), case["oq"])
+    assert np.array_equal(host(so).view(np.uint32), case["osc"].view(np.uint32))

@@ -393,3 +393,89 @@ def test_bfp_conv_is_dequantise_conv_quantise(n, block, rng):
     y = O.conv(O.bfp_dequantize(q, e, block=block), filt, n, plan)
     wq, we = O.bfp_quantize(y, block=block)
     assert np.array_equal(oe, we) and np.array_equal(oq, wq)
+
+
+# ---- the reference's own BFP format (one fp32 scale per transform) ----------------------
+
+def _scaled_inputs(rng, n, batch):
+    """Gaussian signals times 10^u per signal, plus edge
+    cases: an all-zero signal (mx = 1e-30) and one whose abs-max sits on the
+    imaginary part of its last point."""
+    x = (crandn(rng, (batch, n)) * (10.0 ** rng.uniform(-3, 3, (batch, 1)))).astype(np.complex64)
+    x[0] = 0
+    if batch > 2:
+        x[1, -1] = x[1, -1].real + 1j * (4.0 * np.abs(x[1]).max())
+    return x.reshape(-1)
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [64, 512, 4096])
+def test_bfp_scaled_quantize_matches_reference(n, rng):
+    """bfp_quantize (verify_kernel.cpp:1092-1105), bit for bit: words and scales;
+    the library's host codec agrees."""
+    import fufft_amd as ff
+    x = _scaled_inputs(rng, n, 4)
+    q, s = O.bfp_scaled_quantize(x, n)
+    hq, hs = ff.bfp_scaled_quantize(x, n)
+    for t in range(4):
+        rq = np.empty(2 * n, np.int16)
+        xt = np.ascontiguousarray(x[t * n:(t + 1) * n])
+        rs = np.float32(REF.ref_vk_bfp_quantize(xt.ctypes.data, n, rq.ctypes.data))
+        assert np.array_equal(q[2 * n * t:2 * n * (t + 1)], rq)
+        assert s[t].view(np.uint32) == rs.view(np.uint32)
+    assert np.array_equal(q, hq) and np.array_equal(s.view(np.uint32), hs.view(np.uint32))
+    assert bits_equal(O.bfp_scaled_dequantize(q, s, n), ff.bfp_scaled_dequantize(q, s, n))
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [256, 512, 1024, 2048, 4096])
+def test_bfp_scaled_libm_matches_reference_bitwise(n, rng):
+    """kernel_v16_bfp (verify_kernel.cpp:1107-1135, the fufft_pipeline_v16_bfp
+    dataflow) against the restatement in LIBM mode, words and scales."""
+    batch = 3
+    x = _scaled_inputs(rng, n, batch)
+    q, s = O.bfp_scaled_quantize(x, n)
+    plan = O.kernel_plan(n, 16)
+    b = crandn(rng, n, scale=1.0 / n)
+    fq, fs = O.bfp_scaled_quantize(b[O.mixedrev(plan)], n)
+    lead, nrv = lead_and_count(n, 16)
+    rq, rs = np.empty_like(q), np.empty(batch, np.float32)
+    REF.ref_vk_v16_bfp(n, lead, nrv, q.ctypes.data, s.ctypes.data, fq.ctypes.data, float(fs[0]),
+                       rq.ctypes.data, rs.ctypes.data, batch)
+    oq, os_ = O.bfp_scaled_conv(q, s, fq, fs, n, plan, tw=O.TW_LIBM)
+    assert np.array_equal(oq, rq)
+    assert np.array_equal(os_.view(np.uint32), rs.view(np.uint32))
+
+
+def test_bfp_scaled_quantize_closed_form(rng):
+    """Without the reference: the largest component maps to +-32767, the
+    round trip is within half a step, and an all-zero transform has scale
+    1e-30 / 32767 and zero words."""
+    n = 256
+    x = _scaled_inputs(rng, n, 5)
+    q, s = O.bfp_scaled_quantize(x, n)
+    parts = x.view(np.float32).reshape(5, 2 * n)
+    qq = q.reshape(5, 2 * n)
+    for t in range(1, 5):
+        i = np.argmax(np.abs(parts[t]))
+        assert abs(int(qq[t, i])) == 32767 and np.sign(qq[t, i]) == np.sign(parts[t, i])
+        err = np.abs(qq[t].astype(np.float64) * np.float64(s[t]) - parts[t])
+        assert err.max() <= 0.5 * np.float64(s[t]) * (1 + 1e-6) + np.abs(parts[t]).max() * 1e-6
+    assert not qq[0].any() and s[0] == np.float32(np.float32(1e-30) / np.float32(32767.0))
+
+
+@pytest.mark.parametrize("n,v", [(512, 16), (4096, 8)])
+def test_bfp_scaled_conv_is_dequantise_conv_quantise(n, v, rng):
+    """The scaled BFP conv is the fp32 conv of the dequantised signal and
+    filter, quantised per transform: a composition of pinned pieces, with
+    per-transform filters too."""
+    batch = 3
+    x = _scaled_inputs(rng, n, batch)
+    q, s = O.bfp_scaled_quantize(x, n)
+    fq, fs = O.bfp_scaled_quantize(crandn(rng, batch * n, scale=1.0 / n), n)
+    plan = O.kernel_plan(n, v)
+    oq, os_ = O.bfp_scaled_conv(q, s, fq, fs, n, plan, filt_stride=n, mid="conj")
+    y = O.conv(O.bfp_scaled_dequantize(q, s, n), O.bfp_scaled_dequantize(fq, fs, n), n, plan, filt_stride=n,
+               mid="conj")
+    wq, ws = O.bfp_scaled_quantize(y, n)
+    assert np.array_equal(oq, wq) and np.array_equal(os_, ws)
