@@ -128,6 +128,164 @@ int col_values_per_lane(int h)
    return (h == 256 || h == 512 || h == 1024 || h == 2048) ? col_v(h) : 0;
 }
 
+// ---- small images: the whole 2D conv in one workgroup ------------------------------------
+// fufft_conv2d<H, W, CPB> (fufft.cuh:1209-1258; its transcription kernel_conv2d,
+// verify_kernel.cpp:700-722) for images of H x W <= 8192 points, H and W powers
+// of two from 8 to 512: rows DIF, columns DIF, mid, columns DIT, rows DIT, every
+// step through LDS, radix 8 both ways (the reference's per-dimension plans), so
+// with the reference's base twiddles the result is its transcription's bit for
+// bit.  An image has I = H*W/8 lanes.  In the row phases lane i runs row i / TW
+// at lane i % TW (TW = W/8), in the column phases column i / TH at lane i % TH
+// (TH = H/8); both are at most 64, so each row or column transform lies inside
+// one wavefront and its exchanges need a wavefront fence only.  Between the
+// phases the image crosses LDS transposed (columns contiguous, one spare slot
+// per column); workgroup barriers order those crossings.  Images past the
+// batch run on empty buffer ranges (loads return zero, stores are dropped), so
+// every lane meets every barrier.
+constexpr int small2d_lanes(int h, int w) { return h * w / 8; }
+constexpr int small2d_images(int h, int w) { return small2d_lanes(h, w) >= 256 ? 1 : 256 / small2d_lanes(h, w); }
+constexpr int small2d_slot(int h, int w)
+{
+   const int rows = h * (w + w / 8), cols = w * (h + h / 8), tr = w * (h + 1);
+   return rows > cols ? (rows > tr ? rows : tr) : (cols > tr ? cols : tr);
+}
+
+template<int H, int W, int MID>
+__global__ void __launch_bounds__(small2d_images(H, W) * small2d_lanes(H, W))
+small2d_kernel(const Small2dParams p)
+{
+   using PW = Plan<W, 8>;
+   using PH = Plan<H, 8>;
+   using LD = Lds<8, LAYOUT_PAD>;
+   using Op = MidOf<MID>;
+   constexpr int TW = W / 8, TH = H / 8, I = small2d_lanes(H, W), IPB = small2d_images(H, W);
+   constexpr int SW = LD::size(W), SH = LD::size(H), CT = H + 1, SLOT = small2d_slot(H, W);
+   constexpr uint32_t BYTES = H * W * 8;
+   static_assert(TW <= 64 && TH <= 64, "a row or column transform inside one wavefront");
+
+   extern __shared__ float2 lds[];
+   const int img = threadIdx.x / I, i = threadIdx.x % I;
+   const uint32_t t = blockIdx.x * IPB + img;
+   const bool live = t < p.nimg;
+   float2* S = lds + img * SLOT;
+   const int rr = i / TW, rl = i % TW;            // row phases: row, lane in the row
+   const int cc = i / TH, cl = i % TH;            // column phases: column, lane in the column
+
+   Twiddles<PW> tww;
+   tww.load(p.tw, rl);
+   Twiddles<PH> twh;
+   twh.load(p.tw, cl);
+
+   // rows DIF: lane (rr, rl) loads row rr's points rl + q*TW; leaves its row's
+   // spectrum slots rl*8 + k in registers
+   float2 r[8];
+   {
+      const Buf ib(static_cast<const char*>(p.in) + (size_t)t * BYTES, live ? BYTES : 0u);
+#pragma unroll
+      for(int q = 0; q < 8; q++) r[q] = ib.ld2((uint32_t)(rr * W + rl) * 8u, q * TW * 8);
+   }
+   forward_dif<PW, LD, 64>(r, S + rr * SW, rl, tww);
+   // transposed: row-spectrum slot s of row rr to S[s*CT + rr]
+   __syncthreads();
+#pragma unroll
+   for(int k = 0; k < 8; k++) S[(rl * 8 + k) * CT + rr] = r[k];
+   __syncthreads();
+   // columns DIF: lane (cc, cl) takes column cc's rows cl + q*TH
+#pragma unroll
+   for(int q = 0; q < 8; q++) r[q] = S[cc * CT + cl + q * TH];
+   __syncthreads();
+   KeptChain<PH> kc;
+   forward_dif<PH, LD, 64, 64, KEEP_STORE>(r, S + cc * SH, cl, twh, kc);
+   // mid: column-spectrum slot cl*8 + k of column cc is 2D slot (cl*8 + k, cc)
+   if constexpr(Op::reads_filter) {
+      const uint32_t fi = modulo_count(t, p.fcount);
+      const Buf fb(static_cast<const char*>(p.filt) + (size_t)fi * BYTES, live ? BYTES : 0u);
+      float2 b[8];
+#pragma unroll
+      for(int k = 0; k < 8; k++) b[k] = fb.ld2((uint32_t)(cl * 8 * W + cc) * 8u, k * W * 8);
+#pragma unroll
+      for(int k = 0; k < 8; k++) r[k] = Op::apply(r[k], b[k]);
+   } else {
+#pragma unroll
+      for(int k = 0; k < 8; k++) r[k] = Op::apply(r[k], make_float2(0.f, 0.f));
+   }
+   inverse_dit<PH, LD, 64, 64, KEEP_USE>(r, S + cc * SH, cl, twh, kc);
+   // transposed back: column cc's rows cl + q*TH to S[cc*CT + row]
+   __syncthreads();
+#pragma unroll
+   for(int q = 0; q < 8; q++) S[cc * CT + cl + q * TH] = r[q];
+   __syncthreads();
+   // rows DIT: lane (rr, rl) takes row rr's spectrum slots rl*8 + k
+#pragma unroll
+   for(int k = 0; k < 8; k++) r[k] = S[(rl * 8 + k) * CT + rr];
+   __syncthreads();
+   inverse_dit<PW, LD, 64>(r, S + rr * SW, rl, tww);
+   {
+      const Buf ob(static_cast<char*>(p.out) + (size_t)t * BYTES, live ? BYTES : 0u);
+#pragma unroll
+      for(int q = 0; q < 8; q++) ob.st2(r[q], (uint32_t)(rr * W + rl) * 8u, q * TW * 8);
+   }
+}
+
+template<int H, int W, int MID>
+static hipError_t launch_small2d_one(const Small2dParams& p, hipStream_t s)
+{
+   constexpr int IPB = small2d_images(H, W);
+   const size_t shm = (size_t)IPB * small2d_slot(H, W) * sizeof(float2);
+   const void* k = reinterpret_cast<const void*>(&small2d_kernel<H, W, MID>);
+   if(!modulo_count_ok(p.fcount, p.nimg)) return hipErrorInvalidValue;
+   static std::atomic<uint64_t> lds_ok{0};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
+   const dim3 grid((p.nimg + IPB - 1) / IPB), block(IPB * small2d_lanes(H, W));
+   Small2dParams arg = p;
+   void* argv[] = { &arg };
+   return hipLaunchKernel(k, grid, block, argv, shm, s);
+}
+
+template<int H, int W>
+static hipError_t launch_small2d_hw(const Small2dParams& p, hipStream_t s)
+{
+   if constexpr(H * W <= 8192)
+      return with_mid(p.mid, [&](auto m) { return launch_small2d_one<H, W, decltype(m)::value>(p, s); });
+   else
+      return hipErrorInvalidValue;
+}
+
+template<int H>
+static hipError_t launch_small2d_h(int w, const Small2dParams& p, hipStream_t s)
+{
+   switch(w) {
+      case 8:   return launch_small2d_hw<H, 8>(p, s);
+      case 16:  return launch_small2d_hw<H, 16>(p, s);
+      case 32:  return launch_small2d_hw<H, 32>(p, s);
+      case 64:  return launch_small2d_hw<H, 64>(p, s);
+      case 128: return launch_small2d_hw<H, 128>(p, s);
+      case 256: return launch_small2d_hw<H, 256>(p, s);
+      case 512: return launch_small2d_hw<H, 512>(p, s);
+      default:  return hipErrorInvalidValue;
+   }
+}
+
+bool small2d_supported(int64_t h, int64_t w)
+{
+   const bool ph = h >= 8 && h <= 512 && (h & (h - 1)) == 0, pw = w >= 8 && w <= 512 && (w & (w - 1)) == 0;
+   return ph && pw && h * w <= 8192;
+}
+
+hipError_t launch_small2d(int h, int w, const Small2dParams& p, hipStream_t s)
+{
+   switch(h) {
+      case 8:   return launch_small2d_h<8>(w, p, s);
+      case 16:  return launch_small2d_h<16>(w, p, s);
+      case 32:  return launch_small2d_h<32>(w, p, s);
+      case 64:  return launch_small2d_h<64>(w, p, s);
+      case 128: return launch_small2d_h<128>(w, p, s);
+      case 256: return launch_small2d_h<256>(w, p, s);
+      case 512: return launch_small2d_h<512>(w, p, s);
+      default:  return hipErrorInvalidValue;
+   }
+}
+
 hipError_t launch_col(int kind, int h, const ColParams& p, hipStream_t s)
 {
    switch(h) {

@@ -178,4 +178,17 @@ enum { COL_CONV = 0, COL_FWD = 1, COL_APPLY = 2 };
 int        col_values_per_lane(int h);      // 0 if h is not a supported column length
 hipError_t launch_col(int kind, int h, const ColParams& p, hipStream_t s);
 
+// ---- small images: the whole 2D conv in one workgroup (conv2d.hip) --------------------
+struct Small2dParams {
+   const void*   in;       // h x w complex images, rows contiguous
+   void*         out;
+   const void*   filt;     // 2D filter, entry (r, c) = bin (rev_h(r), rev_w(c)), radix 8 both ways
+   const float2* tw;
+   uint32_t      nimg;
+   uint32_t      fcount;   // image i uses filter (i % fcount)
+   int32_t       mid;
+};
+bool       small2d_supported(int64_t h, int64_t w);
+hipError_t launch_small2d(int h, int w, const Small2dParams& p, hipStream_t s);
+
 }  // namespace fufft

@@ -58,7 +58,7 @@ def _golden():
 # fixtures whose plan a GPU kernel runs (the GPU's smallest sizes are N = 256
 # radix 16 and N = 512 radix 8; its four-step middle is radix 8 in [512, 4096])
 GPU_FIXTURES = ["v16_n512", "v16_n1024", "v16_n2048", "v16_n4096", "r8_n512", "r8_n1024",
-                "r8_n2048", "r8_n4096", "split_n512", "r2_n512", "fourstep_n8192_mid512_r8"]
+                "r8_n2048", "r8_n4096", "split_n512", "r2_n512", "fourstep_n8192_mid512_r8", "conv2d_64x64"]
 
 
 @pytest.mark.parametrize("name", GPU_FIXTURES)
@@ -104,6 +104,15 @@ def test_gpu_equals_reference_on_golden_fixture(ref_tw, name):
                    variant="r8")
         assert bits_equal(host(du), case["u"])
         assert bits_equal(host(dv), case["v"])
+    elif kind == "conv2d":
+        # the reference's fused small-image 2D conv (fufft_conv2d<64, 64, CPB>)
+        h, w = int(case["h"]), int(case["w"])
+        a = case["a"]
+        da = to_dev(a, dev)
+        out = torch.empty_like(da)
+        ff.conv2d(da, to_dev(case["bdr"], dev), out, h, w, batch=a.size // (h * w), filt_stride=h * w,
+                  layout="dr")
+        assert bits_equal(host(out), case["out"])
     elif kind == "fourstep":
         n = int(case["n"])
         lout, mid = ff.large_plan(n)
