@@ -335,10 +335,17 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
                          int64_t n, int64_t batch, int mid, void* stream);
 
 /* ---- 2D ---------------------------------------------------------------------------
- * h x w images, row-major, h and w single-launch sizes.  Rows DIF, columns
- * DIF, mid, columns DIT, rows DIT (fufft_conv2d, fufft.cuh:1209-1258).
- * Runs as three launches in place on out: row forward, fused column conv,
- * row inverse (7 HBM passes for an image too large for one workgroup).
+ * h x w images, row-major.  Rows DIF, columns DIF, mid, columns DIT, rows DIT
+ * (fufft_conv2d, fufft.cuh:1209-1258).  Two shape ranges:
+ *   small images, h * w <= 8192 with h and w powers of two from 8 to 512 (the
+ *     reference's own fufft_conv2d shapes are powers of 8 up to 4096 points):
+ *     one fused launch per batch, the whole image in one workgroup's LDS,
+ *     radix 8 both ways; fufft_conv2d_f32 and the host planner only (the
+ *     reference has no split or two-for-one path for them; those calls return
+ *     FUFFT_ERR_UNSUPPORTED, as does device planning of taps);
+ *   large images, h in 256 .. 2048, w a single-launch 1D size (256 .. 16384):
+ *     three launches in place on out: row forward, fused column conv, row
+ *     inverse (an image too large for one workgroup).
  * 2D filters: `layout` names the column order of the filter a call reads or
  * a planner writes.
  *   FUFFT_LAYOUT_DR    the reference's order (verify_kernel.cpp:738-748):
@@ -355,9 +362,11 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
  *                      column tile then reads its filter columns as one
  *                      contiguous run per row, which DR order does not give.
  * Both layouts give bit-identical results.  2D spectra (fufft_fwd2d_f32,
- * fufft_apply2d_f32) are always in the FUFFT_LAYOUT_LANE order. */
+ * fufft_apply2d_f32) are always in the FUFFT_LAYOUT_LANE order.  For small
+ * images the column order is the identity: both layouts are the reference's. */
 /* Values per lane of the row plan (the 1D kernel at FUFFT_AUTO for length w)
- * and of the column plan (8 up to h = 512, 16 for h = 1024, 2048); the
+ * and of the column plan (8 up to h = 512, 16 for h = 1024, 2048; 8 and 8 for
+ * small images); the
  * per-dimension digit orders are those of fufft_digit_order with that many
  * values per lane.  No reference counterpart (the reference fixes both
  * dimensions at compile time, fufft.cuh:1209-1214). */
