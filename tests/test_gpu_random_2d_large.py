@@ -16,9 +16,10 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 HEIGHTS = [256, 512, 1024, 2048]                 # the column kernels' lengths
+SMALL = [8, 16, 32, 64, 128, 256, 512]            # fused small images: h * w <= 8192
 WIDTHS = [256, 512, 1024, 2048, 4096, 8192, 16384]
 LARGE = [8192, 16384, 32768, 65536, 131072, 262144]
-OPS = ["conv2d", "r2_2d", "split2d", "large"]
+OPS = ["conv2d", "r2_2d", "split2d", "large", "small2d"]
 MAX_IMAGE = 1 << 22                               # points per image (every width occurs)
 MAX_POINTS = 1 << 21                              # per case beyond one image: the oracle takes a second or two
 
@@ -29,7 +30,11 @@ def draw(seed):
     c = dict(op=op, seed=seed, mid=["mul", "conj", "none"][rng.integers(3)],
              layout=["dr", "lane"][rng.integers(2)], per_item=bool(rng.integers(2)),
              inplace=bool(rng.integers(2)), null_filter=bool(rng.integers(2)))
-    if op == "large":
+    if op == "small2d":
+        h = int(rng.choice(SMALL))
+        w = int(rng.choice([x for x in SMALL if h * x <= 8192]))
+        c.update(h=h, w=w, batch=int(rng.integers(1, 40)))
+    elif op == "large":
         c["n"] = int(rng.choice(LARGE))
         c["batch"] = int(rng.integers(1, max(2, min(5, MAX_POINTS // c["n"] + 1))))
     else:
@@ -84,7 +89,7 @@ def test_random_config(dev, seed):
     ph, pw = plans(h, w)
     np_ = h * w
     stride = np_ if c["per_item"] else 0
-    if c["op"] == "conv2d":
+    if c["op"] in ("conv2d", "small2d"):
         a = crandn(rng, batch * np_)
         filt = np.concatenate([ff.plan_filter2d(cuniform(rng, np_), h, w, kind=ff.FILTER_TAPS, layout=layout)
                                for _ in range(nf)])

@@ -15,14 +15,14 @@ pytestmark = pytest.mark.gpu
 
 SIZES = {"r8": [512, 1024, 2048, 4096, 8192], "v16": [256, 512, 1024, 2048, 4096, 8192, 16384]}
 BFP_SIZES = {"r8": [512, 1024, 2048, 4096, 8192], "v16": [1024, 2048, 4096, 8192, 16384]}
-OPS = ["conv", "split", "r2", "c2c", "bfp"]
+OPS = ["conv", "split", "r2", "c2c", "bfp", "bfp_scaled"]
 
 
 def draw(seed):
     rng = np.random.default_rng(seed)
     op = OPS[seed % len(OPS)]
     variant = ["r8", "v16"][rng.integers(2)]
-    n = int(rng.choice(BFP_SIZES[variant] if op == "bfp" else SIZES[variant]))
+    n = int(rng.choice(BFP_SIZES[variant] if op == "bfp" else SIZES[variant]))   # bfp_scaled: every size
     batch = int(rng.integers(1, max(2, min(37, (1 << 19) // n))))
     return dict(op=op, variant=variant, n=n, batch=batch,
                 mid=["mul", "conj", "none"][rng.integers(3)],
@@ -94,6 +94,20 @@ def test_random_config(dev, seed):
         ff.c2c(da, out, n=n, batch=batch, direction=c["direction"], variant=c["variant"])
         torch.cuda.synchronize()
         assert bits_equal(out.cpu().numpy(), O.c2c(a, n, plan, c["direction"]))
+    elif c["op"] == "bfp_scaled":
+        # the reference's format: fp32 scale per transform, int16 filter in digit order
+        x = crandn(rng, batch * n) * np.repeat(10.0 ** rng.uniform(-3, 3, batch), n).astype(np.float32)
+        q, s = ff.bfp_scaled_quantize(x, n)
+        fq, fs = ff.bfp_scaled_quantize(fdr, n)
+        dq, ds = dt(q), dt(s)
+        qo, so = (dq, ds) if c["inplace"] else (torch.empty_like(dq), torch.empty_like(ds))
+        nofilt = c["mid"] == "none" and c["per_signal"]            # NULL filter where none is read
+        ff.conv_bfp16_scaled(dq, ds, None if nofilt else dt(fq), None if nofilt else dt(fs), qo, so, n=n,
+                             batch=batch, filt_stride=stride, mid=c["mid"], variant=c["variant"])
+        torch.cuda.synchronize()
+        oq, os_ = O.bfp_scaled_conv(q, s, fq, fs, n, plan, filt_stride=stride, mid=c["mid"])
+        assert np.array_equal(so.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+        assert np.array_equal(qo.cpu().numpy(), oq)
     else:
         x = crandn(rng, batch * n) * np.repeat(10.0 ** rng.uniform(-3, 3, batch), n).astype(np.float32)
         q, e = ff.bfp_quantize(x, block=c["block"])
