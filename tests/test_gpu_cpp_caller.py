@@ -4,7 +4,10 @@ tests/cpp/abi_gpu_check.cpp (built by fufft_amd/build.py, linked against
 libfufft_amd.so and the HIP runtime) allocates with hipMalloc, plans the filter
 with include/fufft/fufft.hpp, and checks the template surface against an fp64
 direct cyclic convolution (rel L2 <= 2e-6) and, bit for bit, against the raw C
-entry point, the split forward/apply path and an in-place call.
+entry point, the split forward/apply path and an in-place call; the int16 BFP
+conv in the reference's own format bit for bit against dequantise -> fp32 conv
+-> quantise; and a 64 x 64 image (one fused launch) against an fp64 direct 2D
+cyclic convolution.
 """
 import subprocess
 from pathlib import Path
