@@ -173,31 +173,43 @@ __device__ __forceinline__ void bfp_body(const BfpParams& p)
    }
 
    const Buf qb(static_cast<const char*>(p.qin) + (size_t)tu * N * 4, N * 4);
+   auto exponent = [&](int q) {
+      if constexpr(BIG) {
+         return __builtin_amdgcn_readlane(ein_lane, q);
+      } else {
+         const int byte = block_of(q);
+         return (int)(int8_t)(ew[byte >> 2] >> (8 * (byte & 3)));
+      }
+   };
    float2 r[V];
-   uint32_t wd[V];
-#pragma unroll
-   for(int q = 0; q < V; q++) wd[q] = qb.ldu<POL_NT>((uint32_t)L * 4u, q * T * 4);
    // Radix 16 at N = 2048 and 4096: every signal load goes out before the
    // first dequantisation (the empty asm reads them all).  Left to itself the
    // scheduler interleaves loads and dequantisation, 5-8 waits among the 16
-   // loads; issued together: +3% / +1.7% (396 -> 408, 377 -> 384 Gpt/s, same
-   // box).  At N = 16384 it costs 3.7% and elsewhere it is even.
+   // loads.  The exponents are read first: after the asm the compiler no
+   // longer proves them unchanged and would read them with vector loads.
+   // Same box: N = 2048 399 -> 416 Gpt/s (+4%), N = 4096 397 -> 397 (another
+   // box: 377 -> 384); at N = 16384 it costs 3.7% and elsewhere it is even.
    if constexpr(V == 16 && N >= 2048 && N <= 4096) {
+      int ex[V];
+      uint32_t wd[V];
+#pragma unroll
+      for(int q = 0; q < V; q++) ex[q] = exponent(q);
+#pragma unroll
+      for(int q = 0; q < V; q++) wd[q] = qb.ldu<POL_NT>((uint32_t)L * 4u, q * T * 4);
 #pragma unroll
       for(int q = 0; q < V; q++) asm volatile("" :: "v"(wd[q]));
-   }
 #pragma unroll
-   for(int q = 0; q < V; q++) {
-      const uint32_t word = wd[q];
-      int e;
-      if constexpr(BIG) {
-         e = __builtin_amdgcn_readlane(ein_lane, q);
-      } else {
-         const int byte = block_of(q);
-         e = (int)(int8_t)(ew[byte >> 2] >> (8 * (byte & 3)));
+      for(int q = 0; q < V; q++)
+         r[q] = make_float2(__builtin_amdgcn_ldexpf((float)(int)(int16_t)(wd[q] & 0xffffu), ex[q]),
+                            __builtin_amdgcn_ldexpf((float)((int)wd[q] >> 16), ex[q]));
+   } else {
+#pragma unroll
+      for(int q = 0; q < V; q++) {
+         const uint32_t word = qb.ldu<POL_NT>((uint32_t)L * 4u, q * T * 4);
+         const int e = exponent(q);
+         r[q] = make_float2(__builtin_amdgcn_ldexpf((float)(int)(int16_t)(word & 0xffffu), e),
+                            __builtin_amdgcn_ldexpf((float)((int)word >> 16), e));
       }
-      r[q] = make_float2(__builtin_amdgcn_ldexpf((float)(int)(int16_t)(word & 0xffffu), e),
-                         __builtin_amdgcn_ldexpf((float)((int)word >> 16), e));
    }
 
    KeptChain<PL> kc;
@@ -380,7 +392,11 @@ bfp_scaled_kernel(const BfpScaledParams p)
    Twiddles<PL> tw;
    tw.load(p.tw, L);
 
+   // both scales up front: after the asm below the compiler no longer proves
+   // them unchanged and would read them with vector loads
    const float sa = p.sin[tu];
+   const uint32_t fi = modulo_count(tu, p.fcount);
+   const float sb = Op::reads_filter ? p.sfilt[fi] : 0.0f;
    const Buf qb(static_cast<const char*>(p.qin) + (size_t)t0 * N * 4, TPW * N * 4);
    // every signal load goes out before the first dequantisation (the empty
    // asm reads them all): left to itself the scheduler interleaves loads and
@@ -401,8 +417,6 @@ bfp_scaled_kernel(const BfpScaledParams p)
    forward_dif<PL, LD, LANES, 64, KEEP_STORE>(r, A, L, tw, kc);
    if constexpr(Op::reads_filter) {
       // slots L*V .. L*V + V - 1, four int16 pairs per 16-byte load
-      const uint32_t fi = modulo_count(t, p.fcount);
-      const float sb = p.sfilt[fi];
       const Buf fb(p.qfilt, p.fcount * (uint32_t)N * 4u);
       const uint32_t fo = (fi * N + (uint32_t)L * V) * 4u;
 #pragma unroll
