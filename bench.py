@@ -391,10 +391,11 @@ def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64, var
     return secs / steps, rel_l2(got, want), float(per_sig.max())
 
 
-def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="v16"):
+def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="v16", layout="dr"):
     """int16-BFP conv in the reference's own format (fufft_conv_bfp16_scaled: one
-    fp32 scale per transform, an int16 filter with one scale), on the same
-    Gaussian x 10^u input as bench_bfp, quantised by the reference's rule."""
+    fp32 scale per transform, an int16 filter with one scale, in the given
+    filter layout), on the same Gaussian x 10^u input as bench_bfp, quantised
+    by the reference's rule."""
     batch = pts // n
     rng = np.random.default_rng(seed)
     q = np.empty(2 * pts, dtype=np.int16)
@@ -410,14 +411,15 @@ def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, varian
             x16 = xc[:16].copy()
         q[2 * n * b0: 2 * n * b1], sc[b0:b1] = ff.bfp_scaled_quantize(xc, n)
     taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
-    fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS), n)
+    fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS), n)
     dq, ds = torch.from_numpy(q).to(dev), torch.from_numpy(sc).to(dev)
     dfq, dfs = torch.from_numpy(fq).to(dev), torch.from_numpy(fs).to(dev)
     qo, so = torch.empty_like(dq), torch.empty_like(ds)
     del q
 
     def step():
-        ff.conv_bfp16_scaled(dq, ds, dfq, dfs, qo, so, n=n, batch=batch, variant=variant, stream=stream)
+        ff.conv_bfp16_scaled(dq, ds, dfq, dfs, qo, so, n=n, batch=batch, variant=variant, layout=layout,
+                             stream=stream)
 
     step()
     torch.cuda.synchronize()
@@ -708,16 +710,17 @@ def main():
                     sys.exit(1)
                 bfp[str(s)]["block_n"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
                                           "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst}
-            # the reference's own format (fp32 scale per transform, int16 filter) at its plan
-            a, r = bench_bfp_scaled(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 199 + s)
+            # the reference's own format (fp32 scale per transform, int16 filter), same plan and layout
+            a, r = bench_bfp_scaled(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 199 + s, variant=bv,
+                                    layout=args.layout)
             if not r <= 1e-4:
                 print(json.dumps({"error": f"BFP (reference format) accuracy check failed at N={s}: "
                                            f"rel L2 {r:.3e}"}))
                 sys.exit(1)
             bfp[str(s)]["reference_format"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
                                                "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
-                                               "rel_l2_vs_fp64_unquantised": r, "variant": "v16",
-                                               "filter": "int16, digit order, one scale"}
+                                               "rel_l2_vs_fp64_unquantised": r, "variant": bv,
+                                               "filter_layout": args.layout, "filter": "int16, one scale"}
         line["bfp"] = bfp
 
     large = {}

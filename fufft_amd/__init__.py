@@ -88,7 +88,7 @@ def _load() -> C.CDLL:
         "fufft_bfp_quantize": ([vp, i64, i64, vp, vp], i32),
         "fufft_bfp_dequantize": ([vp, vp, i64, i64, vp], i32),
         "fufft_conv_bfp16": ([vp, vp, vp, i64, vp, vp, i64, i64, i64, i32, i32, i32, vp], i32),
-        "fufft_conv_bfp16_scaled": ([vp, vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_conv_bfp16_scaled": ([vp, vp, vp, vp, i64, vp, vp, i64, i64, i32, i32, i32, vp], i32),
         "fufft_bfp_scaled_quantize": ([vp, i64, i64, vp, vp], i32),
         "fufft_bfp_scaled_dequantize": ([vp, vp, i64, i64, vp], i32),
         "fufft_large_plan": ([i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
@@ -395,10 +395,11 @@ def conv_bfp16(qin, ein, filt, qout, eout, n: int, batch: int, filt_stride: int 
 
 
 def conv_bfp16_scaled(qin, sin, qfilt, sfilt, qout, sout, n: int, batch: int, filt_stride: int = 0,
-                      mid: str = "mul", variant: str = "auto", stream=None) -> None:
+                      mid: str = "mul", variant: str = "auto", layout: str = "dr", stream=None) -> None:
     """int16-BFP fused conv in the reference's own format (fufft_pipeline_v16_bfp):
     one fp32 scale per transform (sin / sout, batch floats), the filter as
-    int16 pairs in digit order with one fp32 scale per filter."""
+    int16 pairs with one fp32 scale per filter, in the slots of the fp32
+    filter's layout ("dr", the reference's digit order; "lane"; "bperm")."""
     qb = 4 * n * batch
     nf = _count(filt_stride, n, batch, "qfilt") if batch else 0
     reads = mid_reads_filter(mid)
@@ -407,7 +408,8 @@ def conv_bfp16_scaled(qin, sin, qfilt, sfilt, qout, sout, n: int, batch: int, fi
     pq, ps, pfq, pfs, pqo, pso = _ptrs((qin, "qin", qb, "bfp"), (sin, "sin", 4 * batch, "scale"), fq, fs,
                                        (qout, "qout", qb, "bfp"), (sout, "sout", 4 * batch, "scale"))
     check(lib.fufft_conv_bfp16_scaled(pq, ps, pfq, pfs, filt_stride, pqo, pso, n, batch, _mid(mid),
-                                      VARIANT[variant], _stream(stream)), "fufft_conv_bfp16_scaled")
+                                      VARIANT[variant], LAYOUT[layout], _stream(stream)),
+          "fufft_conv_bfp16_scaled")
 
 
 def c2c(inp, out, n: int, batch: int, direction: int = FORWARD, variant: str = "auto",

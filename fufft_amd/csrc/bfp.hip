@@ -358,7 +358,48 @@ __device__ __forceinline__ uint32_t lanes_max(uint32_t x)
    return x;
 }
 
-template<int N, int V, int LAYOUT, int MID>
+// The lane's V int16 filter words (re | im << 16, digit-order slots L*V + k)
+// dequantised by sb, then the mid operation.  Word k sits at voff + 4k in
+// digit order (16-byte loads of four words), at voff + (k/2)*8T + 4(k%2)
+// lane-major (8-byte loads of a pair; the slots of the fp32 pair layout) and
+// at voff + 4kT in the reference's bperm (4-byte loads); voff is the lane's
+// first word: 4(f*N + L*V), 4f*N + 8L and 4(f*N + L).  All V words are read
+// before the first product: with each 16-byte load feeding its four products
+// in turn, radix 16 at N = 8192 ran at 0.92 of the block-format conv's rate
+// on the same box, against 1.00 now (the three layouts within 2% of each
+// other at every size).
+template<class PL, int MID, bool BPERM>
+__device__ __forceinline__ void mid_op_i16(float2 (&r)[PL::V], const Buf& fb, uint32_t voff, int fl, float sb)
+{
+   using Op = MidOf<MID>;
+   constexpr int V = PL::V, T = PL::T;
+   uint32_t w[V];
+   if constexpr(BPERM) {
+#pragma unroll
+      for(int k = 0; k < V; k++) w[k] = fb.ldu(voff, k * T * 4);
+   } else if(fl == FLT_DR) {
+#pragma unroll
+      for(int m = 0; m < V / 4; m++) {
+         const float4 q = fb.ld4(voff, m * 16);
+         w[4 * m]     = __builtin_bit_cast(uint32_t, q.x);
+         w[4 * m + 1] = __builtin_bit_cast(uint32_t, q.y);
+         w[4 * m + 2] = __builtin_bit_cast(uint32_t, q.z);
+         w[4 * m + 3] = __builtin_bit_cast(uint32_t, q.w);
+      }
+   } else {
+#pragma unroll
+      for(int m = 0; m < V / 2; m++) {
+         const float2 q = fb.ld2(voff, m * T * 8);
+         w[2 * m]     = __builtin_bit_cast(uint32_t, q.x);
+         w[2 * m + 1] = __builtin_bit_cast(uint32_t, q.y);
+      }
+   }
+#pragma unroll
+   for(int k = 0; k < V; k++)
+      r[k] = Op::apply(r[k], make_float2((float)(int)(int16_t)(w[k] & 0xffffu) * sb, (float)((int)w[k] >> 16) * sb));
+}
+
+template<int N, int V, int LAYOUT, int MID, bool BPERM>
 __global__ void __launch_bounds__(bfp_cpb(N / V) * (N / V), bfp_min_waves(V, LAYOUT))
 bfp_scaled_kernel(const BfpScaledParams p)
 {
@@ -416,20 +457,10 @@ bfp_scaled_kernel(const BfpScaledParams p)
    KeptChain<PL> kc;
    forward_dif<PL, LD, LANES, 64, KEEP_STORE>(r, A, L, tw, kc);
    if constexpr(Op::reads_filter) {
-      // slots L*V .. L*V + V - 1, four int16 pairs per 16-byte load
       const Buf fb(p.qfilt, p.fcount * (uint32_t)N * 4u);
-      const uint32_t fo = (fi * N + (uint32_t)L * V) * 4u;
-#pragma unroll
-      for(int m = 0; m < V / 4; m++) {
-         const float4 w4 = fb.ld4(fo, m * 16);
-         const uint32_t w[4] = { __builtin_bit_cast(uint32_t, w4.x), __builtin_bit_cast(uint32_t, w4.y),
-                                 __builtin_bit_cast(uint32_t, w4.z), __builtin_bit_cast(uint32_t, w4.w) };
-#pragma unroll
-         for(int i = 0; i < 4; i++) {
-            const float2 b = make_float2((float)(int)(int16_t)(w[i] & 0xffffu) * sb, (float)((int)w[i] >> 16) * sb);
-            r[4 * m + i] = Op::apply(r[4 * m + i], b);
-         }
-      }
+      const uint32_t f0 = fi * N * 4u;
+      const uint32_t lo = BPERM ? (uint32_t)L * 4u : p.fl == FLT_DR ? (uint32_t)L * V * 4u : (uint32_t)L * 8u;
+      mid_op_i16<PL, MID, BPERM>(r, fb, f0 + lo, p.fl, sb);
    } else {
 #pragma unroll
       for(int k = 0; k < V; k++) r[k] = Op::apply(r[k], make_float2(0.f, 0.f));
@@ -469,10 +500,16 @@ static hipError_t launch_bfp_scaled_one(const BfpScaledParams& p, hipStream_t s)
    constexpr int T = N / V, CPB = bfp_cpb(T);
    constexpr int LAYOUT = bfp_lds_layout(N, V);
    const size_t shm = (size_t)CPB * Lds<V, LAYOUT>::size(N) * sizeof(float2) + (T > 64 ? 4 : 0);
-   const void* k = reinterpret_cast<const void*>(&bfp_scaled_kernel<N, V, LAYOUT, MID>);
+   if(p.fl != FLT_DR && p.fl != FLT_LANE && p.fl != FLT_BPERM) return hipErrorInvalidValue;
+   // the bperm reads get a kernel of their own (mids that read the filter only)
+   const bool bp = mid_reads_filter<MID> && p.fl == FLT_BPERM;
+   const void* k = reinterpret_cast<const void*>(&bfp_scaled_kernel<N, V, LAYOUT, MID, false>);
+   if constexpr(mid_reads_filter<MID>) {
+      if(bp) k = reinterpret_cast<const void*>(&bfp_scaled_kernel<N, V, LAYOUT, MID, true>);
+   }
    if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
-   static std::atomic<uint64_t> lds_ok{0};
-   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
+   static std::atomic<uint64_t> lds_ok[2]{};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok[bp]); e != hipSuccess) return e;
    const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
    BfpScaledParams arg = p;
    void* argv[] = { &arg };

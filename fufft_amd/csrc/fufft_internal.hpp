@@ -125,7 +125,7 @@ hipError_t launch_bfp(int n, int v, int layout, const BfpParams& p, hipStream_t 
 struct BfpScaledParams {
    const void*   qin;      // int16 pairs
    const float*  sin;      // one scale per transform
-   const void*   qfilt;    // int16 pairs, digit order
+   const void*   qfilt;    // int16 pairs, laid out as fl says
    const float*  sfilt;    // one scale per filter
    void*         qout;
    float*        sout;     // one scale per transform
@@ -133,6 +133,7 @@ struct BfpScaledParams {
    uint32_t      ntrans;
    uint32_t      fcount;   // transform t uses filter (t % fcount)
    int32_t       mid;
+   int32_t       fl;       // FLT_DR / FLT_LANE / FLT_BPERM, slots as in the fp32 filter
 };
 
 bool       bfp_scaled_supported(int n, int v);

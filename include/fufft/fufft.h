@@ -285,9 +285,11 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
  * fufft_pipeline_v16_bfp(aq, a_scale, bq, b_scale, outq, out_scale)
  * (fufft.cuh:1614-1701; its CPU transcription kernel_v16_bfp and bfp_quantize,
  * verify_kernel.cpp:1092-1135): int16 pairs as above with one fp32 scale per
- * transform, value = q * scale; the filter is int16 pairs in digit order (the
- * fp32 filter of fufft_plan_filter_f32, FUFFT_LAYOUT_DR, for the same variant,
- * quantised by fufft_bfp_scaled_quantize) with one fp32 scale per filter.  On
+ * transform, value = q * scale; the filter is int16 pairs (the fp32 filter of
+ * fufft_plan_filter_f32 for the same variant and layout, quantised by
+ * fufft_bfp_scaled_quantize) with one fp32 scale per filter.  layout: the
+ * reference's digit order FUFFT_LAYOUT_DR, or the slots of FUFFT_LAYOUT_LANE /
+ * FUFFT_LAYOUT_BPERM (same values, same result).  On
  * output, per transform: mx = max(abs-max of the fp32 result, 1e-30),
  * q = rint(clamp(v * (32767 / mx), -32767, 32767)), scale = mx / 32767.
  * filt_stride 0: one filter (qfilt n points, sfilt one scale) for the batch;
@@ -299,7 +301,8 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
  * 4-byte aligned, qfilt 16-byte aligned (FUFFT_ERR_ALIGN). */
 int fufft_conv_bfp16_scaled(const void* qin, const float* sin, const void* qfilt,
                             const float* sfilt, int64_t filt_stride, void* qout, float* sout,
-                            int64_t n, int64_t batch, int mid, int variant, void* stream);
+                            int64_t n, int64_t batch, int mid, int variant, int layout,
+                            void* stream);
 /* host codec of that format (bfp_quantize, verify_kernel.cpp:1092-1105):
  * count transforms of n points, x interleaved re/im, one scale per transform */
 int fufft_bfp_scaled_quantize(const float* x, int64_t n, int64_t count, int16_t* q, float* scale);

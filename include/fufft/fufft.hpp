@@ -104,15 +104,16 @@ inline int pipeline_bfp(const void* qin, const int8_t* ein, const void* filt, vo
 }
 
 // fufft_pipeline_v16_bfp<Mid>(aq, a_scale, bq, b_scale, outq, out_scale) (fufft.cuh:1614-1701)
-// in its own format: one fp32 scale per transform, an int16 filter in digit order with one
-// scale per filter (filt_stride 0: one filter; n: one per transform)
+// in its own format: one fp32 scale per transform, an int16 filter (the reference's digit
+// order by default) with one scale per filter (filt_stride 0: one filter; n: one per transform)
 template<class Mid = MidMultiply>
 inline int pipeline_bfp_scaled(const void* aq, const float* a_scale, const void* bq, const float* b_scale,
                                void* outq, float* out_scale, int64_t n, int64_t batch,
-                               void* stream = nullptr, int64_t filt_stride = 0, Variant v = Variant::V16)
+                               void* stream = nullptr, int64_t filt_stride = 0, Variant v = Variant::V16,
+                               int layout = FUFFT_LAYOUT_DR)
 {
    return fufft_conv_bfp16_scaled(aq, a_scale, bq, b_scale, filt_stride, outq, out_scale, n, batch, Mid::id,
-                                  (int)v, stream);
+                                  (int)v, layout, stream);
 }
 
 // fufft_c2c<N, LOG8N, CPB> (fufft.cuh:879-904): natural-order batched C2C; the

@@ -1,6 +1,7 @@
 """GPU parity of the int16 BFP conv in the reference's own format
 (fufft_conv_bfp16_scaled: one fp32 scale per transform, an int16 filter with
-one scale; fufft_pipeline_v16_bfp, fufft.cuh:1614-1701).
+one scale, in digit order or the lane-major / bperm slots;
+fufft_pipeline_v16_bfp, fufft.cuh:1614-1701).
 
 Bar: int16 words and fp32 scales bit-identical to the oracle's restatement of
 kernel_v16_bfp (verify_kernel.cpp:1092-1135) at every size, variant and mid
@@ -12,7 +13,7 @@ the fp64 convolution of the unquantised input on BASELINE config-3 input
 import numpy as np
 import pytest
 
-from conftest import crandn
+from conftest import bperm, crandn, lane_major
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -32,13 +33,13 @@ def config3_signals(rng, batch, n):
     return x.reshape(-1)
 
 
-def run(dev, q, s, fq, fs, n, batch, filt_stride=0, mid="mul", variant="v16", inplace=False):
+def run(dev, q, s, fq, fs, n, batch, filt_stride=0, mid="mul", variant="v16", inplace=False, layout="dr"):
     import torch
     import fufft_amd as ff
     dq, ds = to_dev(q, dev), to_dev(s, dev)
     qo, so = (dq, ds) if inplace else (torch.empty_like(dq), torch.empty_like(ds))
     ff.conv_bfp16_scaled(dq, ds, None if fq is None else to_dev(fq, dev), None if fs is None else to_dev(fs, dev),
-                         qo, so, n=n, batch=batch, filt_stride=filt_stride, mid=mid, variant=variant)
+                         qo, so, n=n, batch=batch, filt_stride=filt_stride, mid=mid, variant=variant, layout=layout)
     torch.cuda.synchronize()
     return qo.cpu().numpy(), so.cpu().numpy()
 
@@ -67,6 +68,36 @@ def test_scaled_bfp_matches_oracle(dev, variant, n, mid, rng):
         got = ff.bfp_scaled_dequantize(qo, so, n)[n:]
         want = O.conv_spec_f64(x[n:], spec, n)
         assert O.rel_l2(got, want) <= TOL_BFP
+
+
+@pytest.mark.parametrize("variant,n", SIZES)
+def test_scaled_bfp_filter_layouts(dev, variant, n, rng):
+    """The int16 filter in the lane-major pair slots and in the reference's
+    bperm slots (the digit-order words moved, the scales unchanged) gives the
+    digit-order call's words and scales bit for bit, which equal the oracle's;
+    a shared filter with the product and per-signal filters with the
+    conjugate product."""
+    import fufft_amd as ff
+    batch = max(3, min(32, 32768 // n)) + 1
+    x = config3_signals(rng, batch, n)
+    q, s = ff.bfp_scaled_quantize(x, n)
+    v = 8 if variant == "r8" else 16
+    taps = crandn(rng, n)
+    fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, kind=ff.FILTER_TAPS), n)
+    lq, ls = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, layout="lane", kind=ff.FILTER_TAPS), n)
+    # quantising the lane-major fp32 filter gives the digit-order words in lane-major slots
+    assert np.array_equal(lq.view(np.uint32), lane_major(fq.view(np.uint32), n, v)) and np.array_equal(ls, fs)
+    pf = (crandn(rng, (batch, n)) / n).astype(np.complex64).reshape(-1)
+    for stride, mid, (fq, fs) in ((0, "mul", (fq, fs)), (n, "conj", ff.bfp_scaled_quantize(pf, n))):
+        print(f"case bfp_scaled layouts n={n} variant={variant} mid={mid} filt_stride={stride}", flush=True)
+        wq, ws = run(dev, q, s, fq, fs, n, batch, filt_stride=stride, mid=mid, variant=variant)
+        oq, os_ = O.bfp_scaled_conv(q, s, fq, fs, n, O.kernel_plan(n, v), filt_stride=stride, mid=mid)
+        assert np.array_equal(wq, oq) and np.array_equal(ws.view(np.uint32), os_.view(np.uint32))
+        for layout, move in (("lane", lane_major), ("bperm", bperm)):
+            mq = move(fq.view(np.uint32), n, v).view(np.int16)
+            gq, gs = run(dev, q, s, mq, fs, n, batch, filt_stride=stride, mid=mid, variant=variant, layout=layout)
+            assert np.array_equal(gq, wq), layout
+            assert np.array_equal(gs.view(np.uint32), ws.view(np.uint32)), layout
 
 
 @pytest.mark.parametrize("variant,n", [("v16", 512), ("r8", 4096), ("v16", 16384)])
@@ -129,9 +160,9 @@ def test_scaled_bfp_rejects_bad_arguments(dev):
         ff.conv_bfp16_scaled(q, s, fq, fs, q, s, n=256, batch=2, variant="r8")
     with pytest.raises(ff.FufftError):                    # a filter stride neither 0 nor n
         ff.check(ff.lib.fufft_conv_bfp16_scaled(q.data_ptr(), s.data_ptr(), fq.data_ptr(), fs.data_ptr(), 7,
-                                                q.data_ptr(), s.data_ptr(), n, 2, 0, 0, None), "stride")
+                                                q.data_ptr(), s.data_ptr(), n, 2, 0, 0, 0, None), "stride")
     with pytest.raises(ff.FufftError):                    # a misaligned filter
         ff.check(ff.lib.fufft_conv_bfp16_scaled(q.data_ptr(), s.data_ptr(), fq.data_ptr() + 4, fs.data_ptr(), 0,
-                                                q.data_ptr(), s.data_ptr(), n, 2, 0, 0, None), "align")
+                                                q.data_ptr(), s.data_ptr(), n, 2, 0, 0, 0, None), "align")
     # an empty batch is a no-op
     ff.conv_bfp16_scaled(q, s, fq, fs, q, s, n=n, batch=0)

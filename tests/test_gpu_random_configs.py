@@ -95,15 +95,19 @@ def test_random_config(dev, seed):
         torch.cuda.synchronize()
         assert bits_equal(out.cpu().numpy(), O.c2c(a, n, plan, c["direction"]))
     elif c["op"] == "bfp_scaled":
-        # the reference's format: fp32 scale per transform, int16 filter in digit order
+        # the reference's format: fp32 scale per transform, int16 filter (its
+        # digit-order words, moved into the drawn layout's slots)
         x = crandn(rng, batch * n) * np.repeat(10.0 ** rng.uniform(-3, 3, batch), n).astype(np.float32)
         q, s = ff.bfp_scaled_quantize(x, n)
         fq, fs = ff.bfp_scaled_quantize(fdr, n)
+        fw = fq.view(np.uint32)
+        fqdev = {"dr": fw, "lane": lane_major(fw, n, v), "bperm": bperm(fw, n, v)}[c["layout"]].view(np.int16)
         dq, ds = dt(q), dt(s)
         qo, so = (dq, ds) if c["inplace"] else (torch.empty_like(dq), torch.empty_like(ds))
         nofilt = c["mid"] == "none" and c["per_signal"]            # NULL filter where none is read
-        ff.conv_bfp16_scaled(dq, ds, None if nofilt else dt(fq), None if nofilt else dt(fs), qo, so, n=n,
-                             batch=batch, filt_stride=stride, mid=c["mid"], variant=c["variant"])
+        ff.conv_bfp16_scaled(dq, ds, None if nofilt else dt(fqdev), None if nofilt else dt(fs), qo, so, n=n,
+                             batch=batch, filt_stride=stride, mid=c["mid"], variant=c["variant"],
+                             layout=c["layout"])
         torch.cuda.synchronize()
         oq, os_ = O.bfp_scaled_conv(q, s, fq, fs, n, plan, filt_stride=stride, mid=c["mid"])
         assert np.array_equal(so.cpu().numpy().view(np.uint32), os_.view(np.uint32))

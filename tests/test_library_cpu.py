@@ -224,14 +224,15 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_plan_filter2d_device_f32(fake, fake + 16, 512, 512, 1, 7, 1, 1, None) == ff.ERR_INVALID
     # the reference-format BFP conv and codec
     S = L.fufft_conv_bfp16_scaled
-    assert S(fake, fake, fake, fake, 0, fake, fake, 128, 1, 0, 0, None) == ff.ERR_UNSUPPORTED   # radix 16 from 256
-    assert S(fake, fake, fake, fake, 0, fake, fake, 256, 1, 0, 1, None) == ff.ERR_UNSUPPORTED   # radix 8 from 512
-    assert S(fake, fake, None, fake, 0, fake, fake, 4096, 1, 0, 0, None) == ff.ERR_INVALID     # mul reads a filter
-    assert S(fake, None, fake, fake, 0, fake, fake, 4096, 1, 0, 0, None) == ff.ERR_INVALID     # no input scales
-    assert S(fake, fake, fake, fake, 5, fake, fake, 4096, 1, 0, 0, None) == ff.ERR_INVALID     # filter stride
-    assert S(fake, fake, fake + 4, fake, 0, fake, fake, 4096, 1, 0, 0, None) == ff.ERR_ALIGN
-    assert S(fake + 2, fake, fake, fake, 0, fake, fake, 4096, 1, 0, 0, None) == ff.ERR_ALIGN
-    assert S(fake, fake, None, None, 0, fake, fake, 4096, 1, 7, 0, None) == ff.ERR_INVALID     # unknown mid
+    assert S(fake, fake, fake, fake, 0, fake, fake, 128, 1, 0, 0, 0, None) == ff.ERR_UNSUPPORTED   # radix 16 from 256
+    assert S(fake, fake, fake, fake, 0, fake, fake, 256, 1, 0, 1, 0, None) == ff.ERR_UNSUPPORTED   # radix 8 from 512
+    assert S(fake, fake, None, fake, 0, fake, fake, 4096, 1, 0, 0, 0, None) == ff.ERR_INVALID     # mul reads a filter
+    assert S(fake, None, fake, fake, 0, fake, fake, 4096, 1, 0, 0, 0, None) == ff.ERR_INVALID     # no input scales
+    assert S(fake, fake, fake, fake, 5, fake, fake, 4096, 1, 0, 0, 0, None) == ff.ERR_INVALID     # filter stride
+    assert S(fake, fake, fake + 4, fake, 0, fake, fake, 4096, 1, 0, 0, 0, None) == ff.ERR_ALIGN
+    assert S(fake + 2, fake, fake, fake, 0, fake, fake, 4096, 1, 0, 0, 0, None) == ff.ERR_ALIGN
+    assert S(fake, fake, None, None, 0, fake, fake, 4096, 1, 7, 0, 0, None) == ff.ERR_INVALID     # unknown mid
+    assert S(fake, fake, fake, fake, 0, fake, fake, 4096, 1, 0, 0, 3, None) == ff.ERR_INVALID  # unknown layout
     assert L.fufft_bfp_scaled_quantize(None, 64, 1, fake, fake) == ff.ERR_INVALID
     assert L.fufft_bfp_scaled_quantize(fake, 0, 1, fake, fake) == ff.ERR_INVALID
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("misaligned pointer")
