@@ -25,6 +25,20 @@ namespace fufft {
 
 constexpr int cpb_for(int T) { return T >= 128 ? 1 : 256 / T; }
 
+// Transform groups one workgroup of the single-launch conv runs in turn.  At
+// N = 16384 the transform fills a CU's LDS, one workgroup per CU, and each
+// new workgroup starts some 1200 cycles after the last left; eight in a row
+// measured 225.3 -> 232.8 and 225.6 -> 230.0 Gpt/s (two boxes, each against
+// one per workgroup), the digit-order filter 218.8 -> 223.4.  Elsewhere the
+// other resident workgroups hide the start, and the loop cost 3-11%
+// (N = 512 .. 8192, 2 to 8 in a row).
+// Iterations need no barrier between them: a lane's last LDS reads (the
+// inverse's pass-0 gather) and its first LDS writes of the next transform
+// (the forward's pass-0 scatter) are the same positions of the same layout,
+// which no other lane touches in between.
+template<int N, int KIND>
+constexpr uint32_t conv_iters() { return (KIND == K_CONV && N == 16384) ? 8u : 1u; }
+
 // A lane's V digit-order values (slots L*V + k of the transform at point
 // offset base) as 16-byte pairs: contiguous in digit order, at 2(L + m*T)
 // lane-major (FLT_LANE).  One uniform branch; each side computes only its own
@@ -40,11 +54,11 @@ __device__ __forceinline__ void store_spectrum(const Buf& ob, const float2 (&r)[
       ob.st4(make_float4(r[2 * m].x, r[2 * m].y, r[2 * m + 1].x, r[2 * m + 1].y), so, m * ms);
 }
 
-// The kernel body.  BPERM: the filter is in the reference's bperm layout
-// (8-byte loads); it gets a kernel of its own so that the digit-order and
-// pair kernels carry no code for it.
+// The kernel body for transform group bid.  BPERM: the filter is in the
+// reference's bperm layout (8-byte loads); it gets a kernel of its own so that
+// the digit-order and pair kernels carry no code for it.
 template<int N, int V, int LAYOUT, int KIND, int MID, bool BPERM>
-__device__ __forceinline__ void conv1d_body(const Conv1dParams& p)
+__device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_t bid)
 {
    using PL = Plan<N, V>;
    using LD = Lds<V, LAYOUT>;
@@ -73,12 +87,12 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p)
    extern __shared__ float2 lds[];
    const int slot = threadIdx.x / T;
    const int L    = threadIdx.x % T;
-   const uint32_t t = blockIdx.x * CPB + slot;
+   const uint32_t t = bid * CPB + slot;
    if(t >= p.ntrans) return;                 // T > 64 => CPB == 1: whole group leaves
 
    // the wavefront's first transform (uniform) and this lane's offset from it
    const uint32_t t0 = (T >= 64) ? (uint32_t)uniform((int)t)
-                                 : blockIdx.x * CPB + (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
+                                 : bid * CPB + (uint32_t)uniform((int)(threadIdx.x / 64)) * TPW;
    const uint32_t lane_pos = (T >= 64) ? (uint32_t)L : (t - t0) * N + L;
 
    float2* A = lds + slot * SLOT;
@@ -232,7 +246,9 @@ template<int N, int V, int LAYOUT, int KIND, int MID>
 __global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
 conv1d_kernel(const Conv1dParams p)
 {
-   conv1d_body<N, V, LAYOUT, KIND, MID, false>(p);
+   constexpr uint32_t IT = conv_iters<N, KIND>();
+#pragma unroll 1
+   for(uint32_t it = 0; it < IT; it++) conv1d_body<N, V, LAYOUT, KIND, MID, false>(p, blockIdx.x * IT + it);
 }
 
 // the calls that read a filter, with a bperm filter
@@ -240,7 +256,9 @@ template<int N, int V, int LAYOUT, int KIND, int MID>
 __global__ void __launch_bounds__(cpb_for(N / V) * (N / V))
 conv1d_bperm_kernel(const Conv1dParams p)
 {
-   conv1d_body<N, V, LAYOUT, KIND, MID, true>(p);
+   constexpr uint32_t IT = conv_iters<N, KIND>();
+#pragma unroll 1
+   for(uint32_t it = 0; it < IT; it++) conv1d_body<N, V, LAYOUT, KIND, MID, true>(p, blockIdx.x * IT + it);
 }
 
 // (the XOR layout is a comparison option and has no bperm kernels)
@@ -269,7 +287,8 @@ static hipError_t launch_one(const Conv1dParams& p, hipStream_t s)
    if(!modulo_count_ok(p.fcount, p.ntrans) || !modulo_count_ok(p.scount, p.ntrans)) return hipErrorInvalidValue;
    static std::atomic<uint64_t> lds_ok[2]{};
    if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok[bp]); e != hipSuccess) return e;
-   const dim3 grid((p.ntrans + CPB - 1) / CPB), block(CPB * T);
+   constexpr uint32_t IT = conv_iters<N, KIND>();
+   const dim3 grid((uint32_t)(((uint64_t)p.ntrans + CPB * IT - 1) / (CPB * IT))), block(CPB * T);
    Conv1dParams arg = p;
    void* argv[] = { &arg };
    return hipLaunchKernel(k, grid, block, argv, shm, s);
