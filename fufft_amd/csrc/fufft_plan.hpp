@@ -605,15 +605,15 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
 
 // The lane's V filter values one at a time, value k at voff + k*kstep (the
 // reference's bperm layout: T values apart; the 2D column kernels: one image
-// row apart).
-template<class PL, int MID>
+// row apart), read with cache policy POL.
+template<class PL, int MID, int POL = POL_DEFAULT>
 __device__ __forceinline__ void mid_op(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t kstep)
 {
    using Op = MidOf<MID>;
    if constexpr(Op::reads_filter) {
       float2 b[PL::V];
 #pragma unroll
-      for(int k = 0; k < PL::V; k++) b[k] = f.ld2(voff, k * kstep);
+      for(int k = 0; k < PL::V; k++) b[k] = f.ld2<POL>(voff, k * kstep);
 #pragma unroll
       for(int k = 0; k < PL::V; k++) r[k] = Op::apply(r[k], b[k]);
    } else {
