@@ -80,6 +80,8 @@ def parse():
     p.add_argument("--no-2d", action="store_true")
     p.add_argument("--no-c2c", action="store_true", help="skip the natural-order C2C line")
     p.add_argument("--no-vendor", action="store_true", help="skip the rocFFT chain comparison")
+    p.add_argument("--no-per-signal", action="store_true",
+                   help="skip the one-filter-per-signal legs (fp32 and reference-format BFP at N)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=20.0,
                    help="wall seconds for all CPU-baseline rows together")
@@ -166,33 +168,46 @@ def pick_variant(ff, n, variant, layout):
 
 
 def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, settle_s=0.0, per_launch=0,
-               layout="dr"):
+               layout="dr", per_signal=False):
     """fp32 fused conv at size n over pts points, the filter planned in
     `layout`: (seconds per launch, rel L2 of a sample), plus the one-by-one
-    launch durations in us when per_launch > 0."""
+    launch durations in us when per_launch > 0.  per_signal: one filter per
+    signal (filt_stride = n, random natural-order spectra planned on the
+    device), the reference bench's own protocol (bench_fufft.cu:160-170),
+    where the filter is a third pass over HBM."""
     batch = pts // n
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
     out = torch.empty_like(x)
     rng = np.random.default_rng(seed)
-    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS)).to(dev)
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
+    if per_signal:
+        spec = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
+        filt = torch.empty_like(spec)
+        ff.plan_filter_device(spec, filt, n, count=batch, variant=variant, layout=layout, stream=stream)
+        spec_s = spec.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
+        del spec
+        stride = n
+    else:
+        taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+        filt = torch.from_numpy(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS)).to(dev)
+        spec_s = np.fft.fft(taps.astype(np.complex128))[None, :]
+        stride = 0
 
     def step():
-        ff.conv(x, filt, out, n=n, batch=batch, variant=variant, layout=layout, stream=stream)
+        ff.conv(x, filt, out, n=n, batch=batch, filt_stride=stride, variant=variant, layout=layout, stream=stream)
 
     # correctness before timing: fp64 numpy on a sample of signals
     step()
     torch.cuda.synchronize()
-    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
     xs = x.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
     ys = out.view(batch, n)[idx].cpu().numpy()
-    want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    want = np.fft.ifft(np.fft.fft(xs, axis=1) * spec_s, axis=1)
     rel = rel_l2(ys, want)
     secs = time_launches(torch, step, steps, warmup, stream, settle_s)
     each = per_launch_us(torch, step, per_launch, stream) if per_launch else []
-    del x, out
+    del x, out, filt
     if per_launch:
         return secs / steps, rel, each
     return secs / steps, rel
@@ -391,11 +406,14 @@ def bench_bfp(torch, ff, dev, n, pts, steps, warmup, stream, seed, block=64, var
     return secs / steps, rel_l2(got, want), float(per_sig.max())
 
 
-def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="v16", layout="dr"):
+def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="v16", layout="dr",
+                     per_signal=False):
     """int16-BFP conv in the reference's own format (fufft_conv_bfp16_scaled: one
     fp32 scale per transform, an int16 filter with one scale, in the given
     filter layout), on the same Gaussian x 10^u input as bench_bfp, quantised
-    by the reference's rule."""
+    by the reference's rule.  per_signal: one int16 filter per signal (random
+    natural-order spectra, planned on the device, quantised per filter), as
+    the reference's bench feeds fufft_pipeline_v16_bfp (bench_fufft.cu:172-178)."""
     batch = pts // n
     rng = np.random.default_rng(seed)
     q = np.empty(2 * pts, dtype=np.int16)
@@ -410,22 +428,39 @@ def bench_bfp_scaled(torch, ff, dev, n, pts, steps, warmup, stream, seed, varian
         if b0 == 0:
             x16 = xc[:16].copy()
         q[2 * n * b0: 2 * n * b1], sc[b0:b1] = ff.bfp_scaled_quantize(xc, n)
-    taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
-    fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS), n)
+    if per_signal:
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        spec = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
+        planned = torch.empty_like(spec)
+        ff.plan_filter_device(spec, planned, n, count=batch, variant=variant, layout=layout, stream=stream)
+        spec16 = spec[: 16 * n].cpu().numpy().astype(np.complex128).reshape(16, n)
+        del spec
+        fq = np.empty(2 * pts, dtype=np.int16)
+        fs = np.empty(batch, dtype=np.float32)
+        for b0 in range(0, batch, chunk):
+            b1 = min(batch, b0 + chunk)
+            fq[2 * n * b0: 2 * n * b1], fs[b0:b1] = ff.bfp_scaled_quantize(planned[n * b0: n * b1].cpu().numpy(), n)
+        del planned
+        stride = n
+    else:
+        taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
+        fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant=variant, layout=layout, kind=ff.FILTER_TAPS), n)
+        spec16 = np.fft.fft(taps.astype(np.complex128))[None, :]
+        stride = 0
     dq, ds = torch.from_numpy(q).to(dev), torch.from_numpy(sc).to(dev)
     dfq, dfs = torch.from_numpy(fq).to(dev), torch.from_numpy(fs).to(dev)
     qo, so = torch.empty_like(dq), torch.empty_like(ds)
     del q
 
     def step():
-        ff.conv_bfp16_scaled(dq, ds, dfq, dfs, qo, so, n=n, batch=batch, variant=variant, layout=layout,
-                             stream=stream)
+        ff.conv_bfp16_scaled(dq, ds, dfq, dfs, qo, so, n=n, batch=batch, filt_stride=stride, variant=variant,
+                             layout=layout, stream=stream)
 
     step()
     torch.cuda.synchronize()
     got = ff.bfp_scaled_dequantize(qo[: 32 * n].cpu().numpy(), so[:16].cpu().numpy(), n).reshape(16, n)
-    want = np.fft.ifft(np.fft.fft(x16.astype(np.complex128), axis=1)
-                       * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    want = np.fft.ifft(np.fft.fft(x16.astype(np.complex128), axis=1) * spec16, axis=1)
     secs = time_launches(torch, step, steps, warmup, stream, SETTLE_S)
     del dq, ds, dfq, dfs, qo, so
     return secs / steps, rel_l2(got, want)
@@ -662,6 +697,20 @@ def main():
     line[f"{other}_layout"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
                                "variant": ovar, "rel_l2": r}
 
+    # the reference bench's protocol: one filter per signal, so the filter is a
+    # third pass over HBM (24 B/pt physical, the model's bytes)
+    if not args.no_per_signal:
+        a, r = bench_fp32(torch, ff, dev, n, pts, var, args.sweep_steps, 3, stream, 4321, SETTLE_S,
+                          layout=args.layout, per_signal=True)
+        if not r <= 2e-6:
+            print(json.dumps({"error": f"fp32 per-signal-filter accuracy check failed at N={n}: rel L2 {r:.3e}"}))
+            sys.exit(1)
+        line["per_signal_filter"] = {
+            "what": "one filter per signal (filt_stride = n), the reference bench's own protocol",
+            "fp32": {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": var,
+                     "filter_layout": args.layout, "achieved_24B_gbs": round(24.0 * pts / a / 1e9, 1),
+                     "frac_24B": round(24.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4), "rel_l2": r}}
+
     if not args.no_vendor:
         vt, vrel = bench_vendor_chain(torch, dev, n, pts, args.sweep_steps, 3, stream, 1234)
         line["vendor_chain"] = {"what": "torch.fft (rocFFT) forward -> multiply -> inverse, same workload",
@@ -721,6 +770,17 @@ def main():
                                                "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
                                                "rel_l2_vs_fp64_unquantised": r, "variant": bv,
                                                "filter_layout": args.layout, "filter": "int16, one scale"}
+            if s == n and not args.no_per_signal:
+                a, r = bench_bfp_scaled(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 299 + s, variant=bv,
+                                        layout=args.layout, per_signal=True)
+                if not r <= 1e-4:
+                    print(json.dumps({"error": f"BFP (reference format, filter per signal) accuracy check failed "
+                                               f"at N={s}: rel L2 {r:.3e}"}))
+                    sys.exit(1)
+                line.setdefault("per_signal_filter", {})["bfp_reference_format"] = {
+                    "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": bv,
+                    "filter_layout": args.layout, "achieved_12B_gbs": round(12.0 * pts / a / 1e9, 1),
+                    "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64_unquantised": r}
         line["bfp"] = bfp
 
     large = {}
