@@ -249,8 +249,41 @@ small2d_kernel(const Small2dParams p)
       const uint32_t fi = modulo_count(t, p.fcount);
       const Buf fb(static_cast<const char*>(p.filt) + (size_t)fi * BYTES, live ? BYTES : 0u);
       float2 b[8];
+      if constexpr(H >= 64 && H * W <= 4096) {
+         // A lane's filter values run down its column, W points apart, and a
+         // wavefront's TH = H/8 lanes per column read TH rows at once, so from
+         // 64 rows on one wavefront instruction touches 8-64 cache lines.  In
+         // these images each wavefront lies in one image and loads 512
+         // consecutive filter points instead (512-byte runs),
+         // after a barrier writes them into their columns' LDS (entry (r, c)
+         // at c*SH + (r + r/8 + c) mod SH: 9 slots per lane's 8 rows and a
+         // turn per column, so both sides stay nearly free of bank conflicts),
+         // and after a second barrier each lane reads its 8 rows.  A column's
+         // LDS is read and then reused by its own lanes only, so the inverse
+         // needs no third barrier.  Same box, Gpt/s before -> after: 512 x 8
+         // 229 -> 274, 64 x 64 281 -> 293, 128 x 32 248 -> 263, 256 x 16 241 ->
+         // 251, 64 x 8 321 -> 335, 64 x 32 291 -> 283; at 8192 points the two
+         // arrays it holds across the barrier cost a workgroup per CU (128 x 64
+         // 224 -> 174, 256 x 32 235 -> 192), and with fewer than 64 rows the
+         // direct reads take 1-4 cache lines per instruction (32 x 32 298 ->
+         // 278, 8 x 512 277 -> 258), so those read in place.
+         const uint32_t pt0 = (wv * 512u) % (H * W);
+         float2 v[8];
 #pragma unroll
-      for(int k = 0; k < 8; k++) b[k] = fb.ld2((uint32_t)(cl * 8 * W + cc) * 8u, k * W * 8);
+         for(int q = 0; q < 8; q++) v[q] = fb.ld2((pt0 + wl) * 8u, q * 512);
+         __syncthreads();                          // every column's forward DIF is done with S
+#pragma unroll
+         for(int q = 0; q < 8; q++) {
+            const uint32_t pt = pt0 + q * 64 + wl, row = pt / W, col = pt % W;
+            S[col * SH + (row + row / 8 + col) % SH] = v[q];
+         }
+         __syncthreads();
+#pragma unroll
+         for(int k = 0; k < 8; k++) b[k] = S[cc * SH + (cl * 9 + k + cc) % SH];
+      } else {
+#pragma unroll
+         for(int k = 0; k < 8; k++) b[k] = fb.ld2((uint32_t)(cl * 8 * W + cc) * 8u, k * W * 8);
+      }
 #pragma unroll
       for(int k = 0; k < 8; k++) r[k] = Op::apply(r[k], b[k]);
    } else {
