@@ -198,7 +198,17 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
          const uint32_t fb0 = modulo_count(t, p.fcount) * N;
          // a uniform branch on the filter layout: each side computes only its own offset
          if constexpr(BPERM)    mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
-         else if(p.fl == FLT_DR) mid_op_pairs<PL, MID>(r, fb, (fb0 + L * V) * 8u, 16u);
+         else if(p.fl == FLT_DR) {
+            // radix 16 from N = 2048 (the reference's own plan and filter
+            // order): through LDS, N = 2048 / 4096 / 8192 334 -> 348, 312 ->
+            // 328, 255 -> 273 Gpt/s (same box); at N = 1024 it cost 2%, at
+            // radix 8 2-5% (33% at N = 8192, where it took the workgroups per
+            // CU down), and in the BFP conv, VALU-bound, 0 to -11%
+            if constexpr(V == 16 && N >= 2048 && mid_reads_filter<MID>)
+               mid_op_dr_staged<PL, typename LD::template at<PL, PL::NP - 2>, MID>(r, fb, fb0, A, L);
+            else
+               mid_op_pairs<PL, MID>(r, fb, (fb0 + L * V) * 8u, 16u);
+         }
          else                    mid_op_pairs<PL, MID>(r, fb, fb0 * 8u + L * 16u, T * 16u);
       }
       stamp(3);

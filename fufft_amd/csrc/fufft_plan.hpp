@@ -603,6 +603,38 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
    }
 }
 
+// The lane's V digit-order filter values, slots L*V .. L*V + V - 1 from
+// fslot0, passed through LDS.  Read in place they are V/2 16-byte loads 16*V
+// bytes apart, so a wavefront instruction touches 64 (V = 16) cache lines.
+// The wavefront's 64*V slots are contiguous: it loads them in 1 KiB runs and
+// writes them to the LDS positions its own lanes hold in the last pass
+// (position L*V + k under that pass's layout LDL), which no other wavefront
+// touches until this one's inverse scatters to them, so a wavefront fence
+// orders the hand-over.  Needs whole wavefronts per transform (T >= 64).
+template<class PL, class LDL, int MID>
+__device__ __forceinline__ void mid_op_dr_staged(float2 (&r)[PL::V], const Buf& f, uint32_t fslot0, float2* A, int L)
+{
+   using Op = MidOf<MID>;
+   constexpr int V = PL::V;
+   static_assert(PL::T >= 64, "whole wavefronts per transform");
+   const int wl = L & 63, w0 = (L & ~63) * V;      // lane in the wavefront, the wavefront's first slot
+   float4 q[V / 2];
+#pragma unroll
+   for(int m = 0; m < V / 2; m++) q[m] = f.ld4((fslot0 + (uint32_t)w0) * 8u + (uint32_t)wl * 16u, m * 1024);
+#pragma unroll
+   for(int m = 0; m < V / 2; m++) {
+      const int s = w0 + m * 128 + 2 * wl;
+      A[LDL::phys(s)]     = make_float2(q[m].x, q[m].y);
+      A[LDL::phys(s + 1)] = make_float2(q[m].z, q[m].w);
+   }
+   pass_barrier<64>();
+   float2 b[V];
+#pragma unroll
+   for(int k = 0; k < V; k++) b[k] = A[LDL::phys(L * V + k)];
+#pragma unroll
+   for(int k = 0; k < V; k++) r[k] = Op::apply(r[k], b[k]);
+}
+
 // The lane's V filter values one at a time, value k at voff + k*kstep (the
 // reference's bperm layout: T values apart; the 2D column kernels: one image
 // row apart), read with cache policy POL.
