@@ -208,6 +208,8 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
     lds = 2 * v * exchanges * (2 if two else 1)
     if kind in ("c2c_fwd", "c2c_inv"):
         lds += 2 * v                     # the digit <-> natural exchange
+    if kind in ("conv", "conv_r2", "conv_timed", "apply", "apply_r2") and mid != "none" and v == 16 and n >= 2048:
+        lds += 2 * v                     # the digit-order filter handed over through LDS (mid_op_dr_staged)
     loads = {"conv": v, "conv_timed": v, "conv_r2": 2 * v, "fwd": v, "fwd_r2": 2 * v, "apply": v // 2,
              "apply_r2": v // 2, "c2c_fwd": v, "c2c_inv": v, "plan_taps": v}[kind]
     loads += twiddle_slots

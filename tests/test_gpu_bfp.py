@@ -127,7 +127,7 @@ def test_bfp_zero_blocks_and_in_place(dev, rng):
     filt = ff.plan_filter(crandn(rng, n), n, variant="auto", kind=ff.FILTER_TAPS)
     print("case bfp zero blocks in place", flush=True)
     qo, eo = run_bfp(dev, q, e, filt, n, batch, inplace=True)
-    oq, oe = O.bfp_conv(q, e, filt, n, O.kernel_plan(n, 8))
+    oq, oe = O.bfp_conv(q, e, filt, n, O.kernel_plan(n, 8 if ff.resolve_variant(n, "auto") == "r8" else 16))
     assert np.array_equal(eo, oe) and np.array_equal(qo, oq)
     assert np.all(eo.reshape(batch, -1)[3] == -128) and np.all(qo.reshape(batch, -1)[3] == 0)
 
