@@ -270,7 +270,7 @@ def bench_c2c(torch, ff, dev, n, pts, steps, warmup, stream, seed):
     t_vendor = time_launches(torch, vendor, steps, warmup, stream, SETTLE_S) / steps
     del x, out, xv
     torch.cuda.empty_cache()
-    return {"n": n, "batch": batch, "direction": "forward", "variant": ff.c2c_variant(n),
+    return {"n": n, "batch": batch, "direction": "forward", "variant": ff.resolve_variant(n, "auto"),
             "gpoints_s": round(pts / t_ours / 1e9, 3), "ms": round(t_ours * 1e3, 5),
             "achieved_16B_gbs": round(16.0 * pts / t_ours / 1e9, 1),
             "frac_16B": round(16.0 * pts / t_ours / 1e9 / HBM_PEAK_GBS, 4), "rel_l2": rel,

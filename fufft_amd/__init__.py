@@ -43,12 +43,6 @@ def resolve_variant(n: int, variant: str) -> str:
     return "r8" if n in (512, 8192) else "v16"
 
 
-def c2c_variant(n: int) -> str:
-    """The variant fufft_c2c_f32 runs for FUFFT_AUTO (natural order in and out,
-    so not tied to the filter rule): "r8" at n = 512, 4096, 8192, else "v16"."""
-    return "r8" if n in (512, 4096, 8192) else "v16"
-
-
 def fastest_variant(n: int, layout: str = "lane") -> str:
     """The faster variant for an n-point conv whose filter is in `layout`
     (fufft_fastest_variant): with "lane", "r8" at n = 512 and "v16" from

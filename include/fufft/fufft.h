@@ -224,8 +224,7 @@ int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
  * workgroup per CPB transforms.  Here the forward DIF of the conv kernels (or
  * their inverse DIT) runs unchanged and one exchange through LDS moves the
  * spectrum between digit order and natural order, for every size and
- * variant fufft_supported accepts.  FUFFT_AUTO here: FUFFT_R8 at n = 512,
- * 4096 and 8192, FUFFT_V16 elsewhere (no filter ties it to the conv's rule). */
+ * variant fufft_supported accepts. */
 #define FUFFT_FORWARD (-1)
 #define FUFFT_INVERSE   1
 int fufft_c2c_f32(const void* in, void* out, int64_t n, int64_t batch,
