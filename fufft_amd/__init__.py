@@ -40,7 +40,7 @@ def resolve_variant(n: int, variant: str) -> str:
     faster one with a digit-order filter, fastest_variant(n, "dr"))."""
     if variant != "auto":
         return variant
-    return "r8" if n in (512, 8192) else "v16"
+    return "r8" if n in (512, 4096, 8192) else "v16"
 
 
 def fastest_variant(n: int, layout: str = "lane") -> str:

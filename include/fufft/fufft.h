@@ -58,8 +58,8 @@ extern "C" {
 #define FUFFT_R8   1   /* 8 values per lane, radix 8 (fufft_pipeline_ip)     */
 #define FUFFT_AUTO 2   /* the faster of the two for this N on MI355X with
                           the digit-order filter (FUFFT_LAYOUT_DR), one rule
-                          for the fp32 and the BFP conv: FUFFT_R8 at N = 512
-                          and 8192, FUFFT_V16 elsewhere.  The filter must
+                          for the fp32 and the BFP conv: FUFFT_R8 at N = 512,
+                          4096 and 8192, FUFFT_V16 elsewhere.  The filter must
                           be planned with the same variant.  For the
                           lane-major filter see fufft_fastest_variant. */
 

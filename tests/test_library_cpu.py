@@ -48,7 +48,7 @@ def test_plan_and_digit_order_match_oracle(variant, v, n):
 def test_auto_variant_rule():
     import fufft_amd as ff
     for n in [256, 512, 1024, 2048, 4096, 8192, 16384]:
-        want = "r8" if n in (512, 8192) else "v16"
+        want = "r8" if n in (512, 4096, 8192) else "v16"
         assert ff.resolve_variant(n, "auto") == want
         assert ff.plan_radices(n, "auto") == ff.plan_radices(n, want)
         # FUFFT_AUTO is the faster variant for the digit-order filter
