@@ -22,17 +22,19 @@ clocks ramp), then W untimed launches, then exactly K launches bracketed by
 torch.cuda.synchronize(), measured with HIP events recorded on the stream the
 kernels are launched on.  Inputs are resident in HBM before the timed region.
 
-roofline.achieved uses the reference's bandwidth model, 3 passes x 8 B = 24
-bytes per point for fp32 (bench_fufft.cu:314-317), over the average launch
-duration; with a shared filter one of those passes is served from cache, so
-the physical minimum is 16 B/pt and `physical` reports that figure too, also
-as a fraction of the measured stream ceiling (fufft_stream_f32, plain and
-non-temporal, over the same bytes).  For int16-BFP the model is 3 x 4 = 12
-B/pt (physical 8 B/pt + 2 B per 64-point block of exponents); at the headline
-N, "bfp" also reports the same conv with one exponent per signal (block = N,
-the reference's per-transform scale).  roofline.traffic is the HBM bytes per
-launch measured by rocprofv3 PMC (FETCH_SIZE + WRITE_SIZE) for this same
-command, read from the committed summary profiles/conv_f32_n4096.md.
+roofline.achieved counts the bytes the workload must move across HBM: the
+signal read and the result written once, 16 bytes per point, plus the shared
+filter once (8N bytes), over the average launch duration; rocprofv3's
+FETCH_SIZE + WRITE_SIZE for this same command (roofline.traffic, read from
+the committed summary profiles/conv_f32_n4096.md) measure 16.003 B/pt, so
+roofline.frac is the fraction of MI355X's 8 TB/s the kernel really moves.
+The reference's own model, 3 passes x 8 B = 24 B/pt (bench_fufft.cu:314-317),
+counts the filter as a third pass; with one shared filter that pass is served
+from cache, so it is reported apart (roofline.model_24B) and can exceed 1.
+Every other leg likewise gives `frac` on the bytes it must move and the
+reference-model figure under a `model_` key.  roofline.stream_ceiling_gbs is
+the best of a sweep of copy shapes of the library's buffer-instruction stream
+copy (fufft_stream_f32) over the same bytes, the measured HBM ceiling.
 
 The cpu_baseline leg times the reference's own CPU conv paths (cpu_mixed.cpp
 fp64, and verify_kernel.cpp's fp32 and int16-BFP transcriptions of the device
@@ -87,6 +89,8 @@ def parse():
                    help="wall seconds for all CPU-baseline rows together")
     p.add_argument("--settle", type=float, default=0.1,
                    help="seconds of untimed launches before each secondary figure (0 under PMC runs)")
+    p.add_argument("--copy-sweep", action="store_true",
+                   help="time every copy shape of the stream-ceiling sweep and print one line per shape")
     p.add_argument("--copy-only", action="store_true",
                    help="time only the stream copy of the workload's bytes (HBM ceiling, and the copy "
                         "of known size that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -105,6 +109,43 @@ def stream_ceiling(torch, ff, dev, pts, steps, warmup, stream, nontemporal):
         raise RuntimeError("stream copy produced a wrong result")
     del x, y
     return 2.0 * pts * 8 * steps / secs / 1e9, secs / steps
+
+
+# The copy shapes of the ceiling sweep (fufft_stream_shape_f32): loads in
+# flight per lane, consecutive tiles per workgroup or a persistent grid of
+# workgroups (0 = one launch-wide grid), and the cache policies of loads and
+# stores (SC0 = 1, NT = 2).
+SWEEP_SHAPES = [(w, loads) for w in (16, 8) for loads in (1, 2, 4, 8, 16, 32)]
+SWEEP_GRID = ((1, 0), (2, 0), (4, 0), (1, 1024), (1, 2048), (1, 4096))
+SWEEP_POLICY = ((0, 0), (2, 2), (2, 0), (0, 2), (3, 3))
+
+
+def stream_sweep(torch, ff, dev, pts, steps, warmup, stream):
+    """Every shape of the sweep over the same 2^k points: a list of
+    (GB/s, shape dict), the whole sweep settled once (the launches run back to
+    back), each shape checked for an exact copy."""
+    x = torch.empty(pts, dtype=torch.complex64, device=dev).fill_(1.0)
+    x.view(torch.float32)[::7].fill_(-3.5)
+    y = torch.empty_like(x)
+    nbytes = pts * 8
+    rows = []
+    time_launches(torch, lambda: ff.stream_copy(x, y, nbytes, True, stream=stream), 1, 1, stream, SETTLE_S)
+    for width, loads in SWEEP_SHAPES:
+        for per, groups in SWEEP_GRID:
+            for pld, pst in SWEEP_POLICY:
+                y.zero_()
+
+                def copy():
+                    ff.stream_copy_shape(x, y, nbytes, loads, per, groups, pld, pst, width=width, stream=stream)
+                secs = time_launches(torch, copy, steps, warmup, stream, 0.0)
+                torch.cuda.synchronize()
+                if not torch.equal(x, y):
+                    raise RuntimeError(f"stream copy shape {(width, loads, per, groups, pld, pst)} copied wrongly")
+                rows.append((2.0 * nbytes * steps / secs / 1e9,
+                             {"load_bytes": width, "loads_per_lane": loads, "tiles_per_group": per,
+                              "groups": groups, "load_policy": pld, "store_policy": pst}))
+    del x, y
+    return rows
 
 
 SETTLE_S = 0.1          # set from --settle in main()
@@ -143,6 +184,11 @@ def measured_traffic(n, pts):
     if not m or int(m.group(2)) != pts:
         return None
     return float(m.group(1))
+
+
+def frac(bytes_per_launch, secs):
+    """Fraction of MI355X's HBM peak: bytes per launch over seconds per launch."""
+    return round(bytes_per_launch / secs / 1e9 / HBM_PEAK_GBS, 4)
 
 
 def rel_l2(got, want):
@@ -272,26 +318,28 @@ def bench_c2c(torch, ff, dev, n, pts, steps, warmup, stream, seed):
     torch.cuda.empty_cache()
     return {"n": n, "batch": batch, "direction": "forward", "variant": ff.resolve_variant(n, "auto"),
             "gpoints_s": round(pts / t_ours / 1e9, 3), "ms": round(t_ours * 1e3, 5),
-            "achieved_16B_gbs": round(16.0 * pts / t_ours / 1e9, 1),
-            "frac_16B": round(16.0 * pts / t_ours / 1e9 / HBM_PEAK_GBS, 4), "rel_l2": rel,
+            "bytes_per_point": 16, "achieved_gbs": round(16.0 * pts / t_ours / 1e9, 1),
+            "frac": frac(16.0 * pts, t_ours), "rel_l2": rel,
             "rocfft": {"what": "torch.fft.fft (rocFFT), same batch", "gpoints_s": round(pts / t_vendor / 1e9, 3),
                        "ms": round(t_vendor * 1e3, 5), "rel_l2": vrel},
             "speedup_vs_rocfft": round(t_vendor / t_ours, 3)}
 
 
-def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed):
+def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="auto"):
     """Four-step conv: batch pts/n of U[-1,1) signals, one
-    shared filter, in place.  Returns (seconds per call, rel L2 of a sample)."""
+    shared filter in the chain order of the middle `variant` ("auto" = "v16",
+    the reference's run_large middle), in place.  Returns (seconds per call,
+    rel L2 of a sample)."""
     batch = pts // n
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     x = (torch.rand(2 * pts, device=dev, generator=gen) * 2 - 1).view(torch.complex64)
     rng = np.random.default_rng(seed)
     taps = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS)).to(dev)
+    filt = torch.from_numpy(ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS, variant=variant)).to(dev)
     idx = torch.from_numpy(np.linspace(0, batch - 1, 8).astype(np.int64)).to(dev)
     xs = x.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
-    ff.conv_large(x, filt, n=n, batch=batch, stream=stream)
+    ff.conv_large(x, filt, n=n, batch=batch, variant=variant, stream=stream)
     torch.cuda.synchronize()
     ys = x.view(batch, n)[idx].cpu().numpy()
     want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
@@ -300,8 +348,8 @@ def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed):
     # they use an all-pass filter (unit-modulus spectrum, random phase) of the
     # same cost, which keeps the data's norm fixed over any number of launches
     phase = np.exp(2j * np.pi * rng.uniform(0, 1, n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter_large(phase, n, kind=ff.FILTER_SPECTRUM)).to(dev)
-    secs = time_launches(torch, lambda: ff.conv_large(x, filt, n=n, batch=batch, stream=stream),
+    filt = torch.from_numpy(ff.plan_filter_large(phase, n, kind=ff.FILTER_SPECTRUM, variant=variant)).to(dev)
+    secs = time_launches(torch, lambda: ff.conv_large(x, filt, n=n, batch=batch, variant=variant, stream=stream),
                          steps, warmup, stream, SETTLE_S)
     del x
     return secs / steps, rel
@@ -359,10 +407,14 @@ def bench_2d(torch, ff, dev, pts, steps, warmup, stream, seed):
         "real_two_for_one_512x512": {
             "gpixels_s": round(2 * nimg * np_img / t_r2 / 1e9, 3), "ms": round(t_r2 * 1e3, 5),
             "images": 2 * nimg, "rel_l2": rel_r2,
-            "bytes_per_pixel": 24, "frac_24B": round(24.0 * 2 * nimg * np_img / t_r2 / 1e9 / HBM_PEAK_GBS, 4)},
+            # three launches, each reading and writing 4 B per real pixel (a complex
+            # point packs two pixels); the filter is cache-resident
+            "bytes_per_pixel": 24, "frac": frac(24.0 * 2 * nimg * np_img, t_r2)},
         "split_apply_512x512_x256": {
             "gpoints_s": round(nf * np_img / t_ap / 1e9, 3), "ms": round(t_ap * 1e3, 5), "rel_l2": rel_ap,
-            "bytes_per_point": 32, "frac_32B": round(32.0 * nf * np_img / t_ap / 1e9 / HBM_PEAK_GBS, 4)},
+            # filter read + result written by the column apply, the row inverse's read
+            # and write; the shared spectrum is cache-resident
+            "bytes_per_point": 32, "frac": frac(32.0 * nf * np_img, t_ap)},
     }
 
 
@@ -637,8 +689,16 @@ def main():
         gbs, t = stream_ceiling(torch, ff, dev, pts, args.steps, args.warmup, stream, False)
         print(json.dumps({"copy_bytes": 2 * pts * 8, "ms": round(t * 1e3, 5), "gb_s": round(gbs, 1)}))
         return
+    if args.copy_sweep:
+        rows = stream_sweep(torch, ff, dev, pts, args.steps, args.warmup, stream)
+        for g, shape in sorted(rows, key=lambda r: -r[0]):
+            print(json.dumps({"gb_s": round(g, 1), **shape}))
+        return
     plain_gbs, _ = stream_ceiling(torch, ff, dev, pts, 20, 3, stream, False)
     nt_gbs, _ = stream_ceiling(torch, ff, dev, pts, 20, 3, stream, True)
+    sweep_rows = stream_sweep(torch, ff, dev, pts, 20, 3, stream)
+    best_gbs, best_shape = max(sweep_rows, key=lambda r: r[0])
+    ceiling = max(best_gbs, plain_gbs, nt_gbs)
 
     # the headline is timed like every other leg: correctness check first, then
     # SETTLE_S of untimed launches, then exactly --warmup and --steps launches
@@ -649,8 +709,11 @@ def main():
         print(json.dumps({"error": f"fp32 accuracy check failed at N={n}: rel L2 {rel:.3e}"}))
         sys.exit(1)
     gpts = pts / avg / 1e9
-    achieved = 24.0 * pts / avg / 1e9
-    physical = 16.0 * pts / avg / 1e9
+    # the bytes the workload must move across HBM: each point read and written
+    # once, the shared filter once
+    alg_bytes = 16.0 * pts + 8.0 * n
+    achieved = alg_bytes / avg / 1e9
+    model24 = 24.0 * pts / avg / 1e9
     traffic = measured_traffic(n, pts)
 
     line = {
@@ -677,25 +740,49 @@ def main():
                    "n": n, "batch": batch, "points": pts, "variant": var, "filter_layout": args.layout},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "model_bytes_per_point": 24,
-                     "physical": {"bytes_per_point": 16, "achieved": round(physical, 1),
-                                  "frac": round(physical / HBM_PEAK_GBS, 4),
-                                  "frac_of_stream": round(physical / max(plain_gbs, nt_gbs), 4)},
-                     # fufft_stream_f32 over the same 2^27 points: the measured HBM ceiling
-                     # of buffer-instruction streaming, plain and non-temporal
-                     "stream_ceiling_gbs": {"plain": round(plain_gbs, 1), "nt": round(nt_gbs, 1)}},
+                     # achieved counts these bytes per launch: 16 B per point plus the filter once
+                     "bytes_per_launch": int(alg_bytes), "bytes_per_point": 16,
+                     "traffic_bytes_per_point": round(traffic / pts, 4) if traffic else None,
+                     "frac_of_stream_ceiling": round(achieved / ceiling, 4),
+                     # the measured HBM ceiling: the best of the sweep of copy shapes of
+                     # fufft_stream_shape_f32 over the same 2^27 points, and the two fixed
+                     # shapes of fufft_stream_f32
+                     "stream_ceiling_gbs": {"best": round(ceiling, 1), "best_shape": best_shape,
+                                            "shapes_timed": len(sweep_rows),
+                                            "fixed_plain": round(plain_gbs, 1), "fixed_nt": round(nt_gbs, 1)},
+                     "model_24B": {"what": "the reference's 3-pass model (bench_fufft.cu:314-317): it counts the "
+                                           "shared filter as a third pass, which the caches serve here, so this "
+                                           "figure can exceed the HBM peak",
+                                   "bytes_per_point": 24, "achieved": round(model24, 1),
+                                   "frac": round(model24 / HBM_PEAK_GBS, 4)}},
         "accuracy": {"rel_l2_vs_fp64_sample": rel},
     }
 
-    # the same workload with the reference's digit-order filter, at its faster variant
+    # the same workload with the other filter layout.  In digit order that is
+    # the reference's own kernel and filter at this N: fufft_pipeline_v16 with
+    # mixedrev_host's radix-16 order (bench_fufft.cu:164-165, 218-219), i.e.
+    # FUFFT_V16 -- and, when it differs, the plan FUFFT_AUTO takes for a
+    # digit-order filter (radix 8 at N = 512, 4096, 8192, the split apply's
+    # faster plan) beside it
     other = "dr" if args.layout == "lane" else "lane"
-    ovar = pick_variant(ff, n, "fastest", other)
+    ovar = "v16" if other == "dr" else pick_variant(ff, n, "fastest", other)
     a, r = bench_fp32(torch, ff, dev, n, pts, ovar, args.sweep_steps, 3, stream, 1234, SETTLE_S, layout=other)
     if not r <= 2e-6:
         print(json.dumps({"error": f"fp32 accuracy check failed at N={n} ({other}): rel L2 {r:.3e}"}))
         sys.exit(1)
     line[f"{other}_layout"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
-                               "variant": ovar, "rel_l2": r}
+                               "variant": ovar, "frac": frac(16.0 * pts + 8.0 * n, a), "rel_l2": r}
+    if other == "dr":
+        line["dr_layout"]["plan"] = "the reference's fufft_pipeline_v16 plan and filter order"
+        avar = ff.resolve_variant(n, "auto")
+        if avar != ovar:
+            a, r = bench_fp32(torch, ff, dev, n, pts, avar, args.sweep_steps, 3, stream, 1234, SETTLE_S,
+                              layout=other)
+            if not r <= 2e-6:
+                print(json.dumps({"error": f"fp32 accuracy check failed at N={n} (dr, auto): rel L2 {r:.3e}"}))
+                sys.exit(1)
+            line["dr_layout"]["auto"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                                         "variant": avar, "rel_l2": r}
 
     # the reference bench's protocol: one filter per signal, so the filter is a
     # third pass over HBM (24 B/pt physical, the model's bytes)
@@ -708,8 +795,8 @@ def main():
         line["per_signal_filter"] = {
             "what": "one filter per signal (filt_stride = n), the reference bench's own protocol",
             "fp32": {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": var,
-                     "filter_layout": args.layout, "achieved_24B_gbs": round(24.0 * pts / a / 1e9, 1),
-                     "frac_24B": round(24.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4), "rel_l2": r}}
+                     "filter_layout": args.layout, "bytes_per_point": 24,
+                     "achieved_gbs": round(24.0 * pts / a / 1e9, 1), "frac": frac(24.0 * pts, a), "rel_l2": r}}
 
     if not args.no_vendor:
         vt, vrel = bench_vendor_chain(torch, dev, n, pts, args.sweep_steps, 3, stream, 1234)
@@ -725,7 +812,8 @@ def main():
         a, r = bench_fp32(torch, ff, dev, s, pts, sv, args.sweep_steps, 3, stream, 77 + s, SETTLE_S,
                           layout=args.layout)
         sweep[str(s)] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
-                         "frac_24B": round(24.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                         "frac": frac(16.0 * pts + 8.0 * s, a),
+                         "model_frac_24B": round(24.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
                          "variant": sv, "filter_layout": args.layout, "rel_l2": r}
         if not r <= 2e-6:
             print(json.dumps({"error": f"fp32 accuracy check failed at N={s}: rel L2 {r:.3e}"}))
@@ -743,9 +831,12 @@ def main():
                 print(json.dumps({"error": f"BFP accuracy check failed at N={s}: rel L2 {r:.3e}"}))
                 sys.exit(1)
             g = pts / a / 1e9
+            # 4 B per point in and out, one exponent byte per 64-point block in and out,
+            # the fp32 filter once
+            bb = 8.0 * pts + 2.0 * pts / 64 + 8.0 * s
             bfp[str(s)] = {"gpoints_s": round(g, 3), "ms": round(a * 1e3, 5),
-                           "achieved_12B_gbs": round(12.0 * pts / a / 1e9, 1),
-                           "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                           "bytes_per_point": round(bb / pts, 4), "achieved_gbs": round(bb / a / 1e9, 1),
+                           "frac": frac(bb, a), "model_frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
                            "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst,
                            "variant": bv, "filter_layout": args.layout}
             if s == n:
@@ -766,8 +857,11 @@ def main():
                 print(json.dumps({"error": f"BFP (reference format) accuracy check failed at N={s}: "
                                            f"rel L2 {r:.3e}"}))
                 sys.exit(1)
+            # 4 B per point in and out, one fp32 scale per transform in and out, the int16 filter once
+            rb = 8.0 * pts + 8.0 * pts / s + 4.0 * s
             bfp[str(s)]["reference_format"] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
-                                               "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                                               "frac": frac(rb, a),
+                                               "model_frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
                                                "rel_l2_vs_fp64_unquantised": r, "variant": bv,
                                                "filter_layout": args.layout, "filter": "int16, one scale"}
             if s == n and not args.no_per_signal:
@@ -779,26 +873,33 @@ def main():
                     sys.exit(1)
                 line.setdefault("per_signal_filter", {})["bfp_reference_format"] = {
                     "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": bv,
-                    "filter_layout": args.layout, "achieved_12B_gbs": round(12.0 * pts / a / 1e9, 1),
-                    "frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4), "rel_l2_vs_fp64_unquantised": r}
+                    "filter_layout": args.layout, "bytes_per_point": 12,
+                    "achieved_gbs": round(12.0 * pts / a / 1e9, 1), "frac": frac(12.0 * pts, a),
+                    "rel_l2_vs_fp64_unquantised": r}
         line["bfp"] = bfp
 
     large = {}
     for s in [int(v) for v in args.large_sizes.split(",") if v.strip()]:
         lout, mid = ff.large_plan(s)
-        a, r = bench_large(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 5 + s)
-        if not r <= 2e-6:
-            print(json.dumps({"error": f"four-step accuracy check failed at N={s}: rel L2 {r:.3e}"}))
-            sys.exit(1)
-        model = (4 * lout + 3) * 8
-        large[str(s)] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
-                         "plan": f"{lout} outer radix-16 level(s) + fused middle N={mid}",
-                         "model_bytes_per_point": model,
-                         "frac_model": round(model * pts / a / 1e9 / HBM_PEAK_GBS, 4),
-                         # three passes of 16 B (the two outer levels of a two-level plan
-                         # run as one pass); the filter is cache-resident
-                         "physical_bytes_per_point": 48,
-                         "rel_l2": r}
+        legs = {}
+        for lv in ("v16", "r8"):
+            a, r = bench_large(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 5 + s, variant=lv)
+            if not r <= 2e-6:
+                print(json.dumps({"error": f"four-step accuracy check failed at N={s} ({lv}): rel L2 {r:.3e}"}))
+                sys.exit(1)
+            model = (4 * lout + 3) * 8
+            legs[lv] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                        "plan": f"{lout} outer radix-16 level(s) + fused middle N={mid} at "
+                                f"{'radix 16 (the reference run_large middle)' if lv == 'v16' else 'radix 8'}",
+                        # three passes of 16 B (the two outer levels of a two-level plan
+                        # run as one pass); the filter is cache-resident
+                        "bytes_per_point": 48, "frac": frac(48.0 * pts, a),
+                        # the reference's (4 lout + 3) x 8 B model (bench_fufft.cu:481)
+                        "model_bytes_per_point": model,
+                        "model_frac": round(model * pts / a / 1e9 / HBM_PEAK_GBS, 4),
+                        "rel_l2": r}
+        # the default middle (the reference's) with the radix-8 one beside it
+        large[str(s)] = {**legs["v16"], "variant": "v16", "r8_middle": legs["r8"]}
     if large:
         line["large"] = large
 

@@ -24,6 +24,7 @@ except ImportError:  # pragma: no cover - torch is part of the image
 
 _LIB_PATH = Path(__file__).resolve().parent / "libfufft_amd.so"
 
+ABI_VERSION = 3                   # FUFFT_ABI_VERSION of the header this binding follows
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
 SCRATCH_BYTES = 64 << 20          # FUFFT_SCRATCH_BYTES
 MID = {"mul": 0, "conj": 1, "none": 2}
@@ -62,11 +63,12 @@ class FufftError(RuntimeError):
 def _load() -> C.CDLL:
     if not _LIB_PATH.exists():
         raise FileNotFoundError(
-            f"{_LIB_PATH} is missing: build it with `python -m fufft_amd.build` "
+            f"{_LIB_PATH} is missing: build it with `python fufft_amd/build.py` "
             "(there is no CPU fallback)")
     L = C.CDLL(str(_LIB_PATH))
     i64, i32, vp, fp = C.c_int64, C.c_int, C.c_void_p, C.POINTER(C.c_float)
     sig = {
+        "fufft_abi_version": ([], i32),
         "fufft_init": ([i32], i32),
         "fufft_status_string": ([i32], C.c_char_p),
         "fufft_supported": ([i64, i32], i32),
@@ -92,9 +94,9 @@ def _load() -> C.CDLL:
         "fufft_bfp_scaled_quantize": ([vp, i64, i64, vp, vp], i32),
         "fufft_bfp_scaled_dequantize": ([vp, vp, i64, i64, vp], i32),
         "fufft_large_plan": ([i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
-        "fufft_large_digit_order": ([i64, C.POINTER(C.c_int32)], i32),
-        "fufft_plan_filter_large_f32": ([i64, i32, i32, vp, vp], i32),
-        "fufft_conv_large_f32": ([vp, vp, i64, i64, i64, i32, vp], i32),
+        "fufft_large_digit_order": ([i64, i32, C.POINTER(C.c_int32)], i32),
+        "fufft_plan_filter_large_f32": ([i64, i32, i32, i32, vp, vp], i32),
+        "fufft_conv_large_f32": ([vp, vp, i64, i64, i64, i32, i32, vp], i32),
         "fufft_plan2d": ([i64, i64, C.POINTER(C.c_int), C.POINTER(C.c_int)], i32),
         "fufft_plan2d_column_order": ([i64, i64, C.POINTER(C.c_int32)], i32),
         "fufft_plan_filter2d_f32": ([i64, i64, i32, i32, i32, vp, vp], i32),
@@ -105,10 +107,11 @@ def _load() -> C.CDLL:
         "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, i32, vp], i32),
         "fufft_c2c_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
         "fufft_stream_f32": ([vp, vp, i64, i32, vp], i32),
+        "fufft_stream_shape_f32": ([vp, vp, i64, i32, i32, i32, i32, i32, i32, vp], i32),
         "fufft_transforms_per_workgroup": ([i64, i32], i32),
         "fufft_conv_timed_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp, i64, vp], i32),
         "fufft_plan_filter_device_f32": ([vp, vp, i64, i64, i32, i32, i32, i32, vp], i32),
-        "fufft_plan_filter_large_device_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
+        "fufft_plan_filter_large_device_f32": ([vp, vp, i64, i64, i32, i32, i32, vp], i32),
         "fufft_plan_filter2d_device_f32": ([vp, vp, i64, i64, i64, i32, i32, i32, vp], i32),
     }
     for name, (args, res) in sig.items():
@@ -116,6 +119,11 @@ def _load() -> C.CDLL:
         if f is None:
             continue
         f.argtypes, f.restype = args, res
+    # a library built from another header would take these arguments wrongly
+    abi = L.fufft_abi_version() if hasattr(L, "fufft_abi_version") else None
+    if abi != ABI_VERSION:
+        raise ImportError(f"{_LIB_PATH} has ABI version {abi}, this binding expects {ABI_VERSION}: "
+                          "rebuild it with `python fufft_amd/build.py`")
     return L
 
 
@@ -431,10 +439,11 @@ def plan_filter_device(inp, out, n: int, count: int = 1, variant: str = "auto", 
 
 
 def plan_filter_large_device(inp, out, n: int, count: int = 1, kind: int = FILTER_SPECTRUM,
-                             fold_inv_n: bool = True, stream=None) -> None:
+                             fold_inv_n: bool = True, variant: str = "auto", stream=None) -> None:
     nb = 8 * n * count
     pi, po = _ptrs((inp, "inp", nb, "complex"), (out, "out", nb, "complex"))
-    check(lib.fufft_plan_filter_large_device_f32(pi, po, n, count, kind, int(fold_inv_n), _stream(stream)),
+    check(lib.fufft_plan_filter_large_device_f32(pi, po, n, count, VARIANT[variant], kind, int(fold_inv_n),
+                                                 _stream(stream)),
           "fufft_plan_filter_large_device_f32")
 
 
@@ -456,29 +465,39 @@ def large_plan(n: int) -> tuple[int, int]:
     return lout.value, mid.value
 
 
-def large_digit_order(n: int) -> np.ndarray:
+def large_middle(variant: str = "auto") -> int:
+    """Values per lane of the four-step middle a variant names: "v16" and
+    "auto" the reference's radix-16 middle, "r8" the radix-8 one."""
+    return 8 if variant == "r8" else 16
+
+
+def large_digit_order(n: int, variant: str = "auto") -> np.ndarray:
+    """Slot -> bin of the chained four-step order: [16]^lout, then the
+    middle's radices ("v16"/"auto": run_large's order, bench_fufft.cu:410-428)."""
     perm = np.empty(n, dtype=np.int32)
-    check(lib.fufft_large_digit_order(n, perm.ctypes.data_as(C.POINTER(C.c_int32))),
+    check(lib.fufft_large_digit_order(n, VARIANT[variant], perm.ctypes.data_as(C.POINTER(C.c_int32))),
           "fufft_large_digit_order")
     return perm
 
 
 def plan_filter_large(x: np.ndarray, n: int, kind: int = FILTER_SPECTRUM,
-                      fold_inv_n: bool = True) -> np.ndarray:
+                      fold_inv_n: bool = True, variant: str = "auto") -> np.ndarray:
     src = np.ascontiguousarray(x, dtype=np.complex64).reshape(-1)
     if src.size != n:
         raise ValueError(f"plan_filter_large: {src.size} points given, n = {n}")
     out = np.empty(n, dtype=np.complex64)
-    check(lib.fufft_plan_filter_large_f32(n, kind, int(fold_inv_n), src.ctypes.data, out.ctypes.data),
+    check(lib.fufft_plan_filter_large_f32(n, VARIANT[variant], kind, int(fold_inv_n), src.ctypes.data,
+                                          out.ctypes.data),
           "fufft_plan_filter_large_f32")
     return out
 
 
 def conv_large(buf, filt, n: int, batch: int, filt_stride: int = 0, mid: str = "mul",
-               stream=None) -> None:
-    """Four-step conv of a batch of n-point signals, in place on buf."""
+               variant: str = "auto", stream=None) -> None:
+    """Four-step conv of a batch of n-point signals, in place on buf; the
+    filter in the chain order of the same variant (large_digit_order)."""
     pb, pf = _ptrs((buf, "buf", 8 * n * batch, "complex"), _filt(filt, "filt", n, batch, filt_stride, mid))
-    check(lib.fufft_conv_large_f32(pb, pf, filt_stride, n, batch, _mid(mid), _stream(stream)),
+    check(lib.fufft_conv_large_f32(pb, pf, filt_stride, n, batch, _mid(mid), VARIANT[variant], _stream(stream)),
           "fufft_conv_large_f32")
 
 
@@ -566,6 +585,17 @@ def stream_copy(inp, out, nbytes: int, nontemporal: bool = False, stream=None) -
     """HBM stream ceiling: copy nbytes with the conv kernels' buffer instructions."""
     pi, po = _ptrs((inp, "inp", nbytes, "complex"), (out, "out", nbytes, "complex"))
     check(lib.fufft_stream_f32(pi, po, nbytes, int(nontemporal), _stream(stream)), "fufft_stream_f32")
+
+
+def stream_copy_shape(inp, out, nbytes: int, loads: int = 8, per: int = 1, groups: int = 0,
+                      load_policy: int = 0, store_policy: int = 0, width: int = 16, stream=None) -> None:
+    """The stream copy in a chosen shape (fufft_stream_shape_f32): `loads`
+    loads of `width` bytes per lane in flight, `per` consecutive tiles per
+    workgroup or a persistent grid of `groups` workgroups, cache policies
+    SC0 = 1, NT = 2."""
+    pi, po = _ptrs((inp, "inp", nbytes, "complex"), (out, "out", nbytes, "complex"))
+    check(lib.fufft_stream_shape_f32(pi, po, nbytes, width, loads, per, groups, load_policy, store_policy,
+                                     _stream(stream)), "fufft_stream_shape_f32")
 
 
 def bfp_exponent(absmax: float) -> int:

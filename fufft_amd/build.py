@@ -3,7 +3,7 @@
 Everything is compiled in-tree so the shared objects travel with the source
 tree to the GPU box.  hipcc cross-compiles for gfx950 without a GPU.
 
-    python -m fufft_amd.build            # library + oracle (+ reference shim)
+    python fufft_amd/build.py            # library + oracle (+ reference shim)
 """
 from __future__ import annotations
 

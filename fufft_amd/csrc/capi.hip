@@ -231,8 +231,15 @@ int resolve_variant(int64_t n, int variant)
    return fastest_variant(n, FUFFT_LAYOUT_DR);
 }
 
-// The four-step middle always runs radix 8 (N = 512 .. 4096 per chunk).
-constexpr int kLargeMiddleV = 8;
+// Values per lane of the four-step middle (N = 512 .. 4096 per chunk):
+// FUFFT_V16 is the reference's own middle (run_large launches
+// fufft_pipeline_v16 on the chunks, bench_fufft.cu:368-386), and FUFFT_AUTO
+// takes it; FUFFT_R8 is the radix-8 middle (conv_foursteps_cfg with the
+// radix-8 middle, verify_kernel.cpp:373-394).
+int large_middle_v(int variant)
+{
+   return variant == FUFFT_R8 ? 8 : (variant == FUFFT_V16 || variant == FUFFT_AUTO) ? 16 : 0;
+}
 
 int values_per_lane(int variant)
 {
@@ -318,6 +325,8 @@ std::vector<double> spectrum_of(int64_t n, int filter_kind, int fold_inv_n, cons
 using namespace fufft;
 
 extern "C" {
+
+int fufft_abi_version(void) { return FUFFT_ABI_VERSION; }
 
 int fufft_init(int device) { return init_device(device); }
 
@@ -758,6 +767,17 @@ int fufft_stream_f32(const void* in, void* out, int64_t bytes, int nontemporal, 
    return status_of(launch_stream(in, out, (uint64_t)bytes, nontemporal != 0, static_cast<hipStream_t>(stream)));
 }
 
+int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int load_bytes, int loads_per_lane,
+                           int tiles_per_group, int groups, int load_policy, int store_policy, void* stream)
+{
+   if(!in || !out || in == out || bytes < 0 || (bytes & 15)) return FUFFT_ERR_INVALID;
+   if(!stream_shape_ok(load_bytes, loads_per_lane, tiles_per_group, groups, load_policy, store_policy))
+      return FUFFT_ERR_INVALID;
+   if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   return status_of(launch_stream_shape(in, out, (uint64_t)bytes, load_bytes, loads_per_lane, tiles_per_group,
+                                        groups, load_policy, store_policy, static_cast<hipStream_t>(stream)));
+}
+
 // ---- BFP host codec -----------------------------------------------------------------
 
 int fufft_bfp_exponent(float absmax)
@@ -831,8 +851,8 @@ int fufft_large_plan(int64_t n, int* lout, int* mid)
    if(!lout || !mid) return FUFFT_ERR_INVALID;
    if(!pow2(n) || n < 8192 || n > ((int64_t)1 << FUFFT_TW_LOG_MAX)) return FUFFT_ERR_UNSUPPORTED;
    // fewest outer levels that bring the middle to a single-workgroup size
-   // <= 4096; the middle then lies in [512, 4096], where the radix-8 kernel
-   // is the fastest
+   // <= 4096; the middle then lies in [512, 4096], which both middles (radix
+   // 16 and radix 8) cover
    int lo = 1;
    while((n >> (4 * lo)) > 4096) lo++;
    *lout = lo;
@@ -840,32 +860,34 @@ int fufft_large_plan(int64_t n, int* lout, int* mid)
    return FUFFT_OK;
 }
 
-// chain radices: lout radix-16 outer levels, then the middle's own plan
-static int large_radices(int64_t n, int* lout, int* mid, int* r)
+// chain radices: lout radix-16 outer levels, then the middle's own plan at
+// v values per lane -- the order of bench_fufft.cu:410-428
+static int large_radices(int64_t n, int v, int* lout, int* mid, int* r)
 {
+   if(!v) return FUFFT_ERR_INVALID;
    const int st = fufft_large_plan(n, lout, mid);
    if(st != FUFFT_OK) return st;
    int np = 0;
    for(int i = 0; i < *lout; i++) r[np++] = 16;
-   np += factor(*mid, kLargeMiddleV, r + np);
+   np += factor(*mid, v, r + np);
    return np;
 }
 
-int fufft_large_digit_order(int64_t n, int32_t* perm)
+int fufft_large_digit_order(int64_t n, int variant, int32_t* perm)
 {
    int r[64], lout = 0, mid = 0;
-   const int np = large_radices(n, &lout, &mid, r);
+   const int np = large_radices(n, large_middle_v(variant), &lout, &mid, r);
    if(np < 0) return np;
    if(!perm) return FUFFT_ERR_INVALID;
    for(int64_t i = 0; i < n; i++) perm[i] = group_reverse((int32_t)i, r, np);
    return FUFFT_OK;
 }
 
-int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n, const float* in,
+int fufft_plan_filter_large_f32(int64_t n, int variant, int filter_kind, int fold_inv_n, const float* in,
                                 float* out)
 {
    int r[64], lout = 0, mid = 0;
-   const int np = large_radices(n, &lout, &mid, r);
+   const int np = large_radices(n, large_middle_v(variant), &lout, &mid, r);
    if(np < 0) return np;
    if(!in || !out) return FUFFT_ERR_INVALID;
    if(filter_kind != FUFFT_FILTER_SPECTRUM && filter_kind != FUFFT_FILTER_TAPS) return FUFFT_ERR_INVALID;
@@ -893,10 +915,11 @@ static hipError_t outer_levels(float2* a, int64_t n, int64_t batch, int lout, bo
 }
 
 int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int64_t count,
-                                       int filter_kind, int fold_inv_n, void* stream)
+                                       int variant, int filter_kind, int fold_inv_n, void* stream)
 {
    int r[64], lout = 0, mn = 0;
-   const int np = large_radices(n, &lout, &mn, r);
+   const int v = large_middle_v(variant);
+   const int np = large_radices(n, v, &lout, &mn, r);
    if(np < 0) return np;
    int st = check_plan_kind(filter_kind);
    if(st != FUFFT_OK) return st;
@@ -925,21 +948,21 @@ int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int
    p.tw = tw; p.in0 = out; p.out0 = out;
    p.ntrans = (uint32_t)(count * (n / mn));
    p.fcount = 1; p.scount = 1; p.mid = FUFFT_MID_NONE; p.fl = FUFFT_LAYOUT_DR; p.scale = scale;
-   return run_conv1d(K_PLAN_TAPS, mn, kLargeMiddleV, p, stream);
+   return run_conv1d(K_PLAN_TAPS, mn, v, p, stream);
 }
 
 int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64_t n,
-                         int64_t batch, int mid, void* stream)
+                         int64_t batch, int mid, int variant, void* stream)
 {
    int lout = 0, mn = 0;
    int st = fufft_large_plan(n, &lout, &mn);
    if(st != FUFFT_OK) return st;
-   if(!mid_known(mid)) return FUFFT_ERR_INVALID;
+   const int v = large_middle_v(variant);
+   if(!mid_known(mid) || !v) return FUFFT_ERR_INVALID;
    if(batch < 0 || batch * (n / 16) > 0xffffffffll) return FUFFT_ERR_INVALID;
    if(!buf || (mid_needs_filter(mid) && !filt)) return FUFFT_ERR_INVALID;
    if(!aligned16(buf) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
    if(filt_stride != 0 && filt_stride != n) return FUFFT_ERR_INVALID;
-   const int v = kLargeMiddleV;
    if(!conv1d_supported(mn, v)) return FUFFT_ERR_UNSUPPORTED;
    Conv1dParams p{};
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;

@@ -316,9 +316,10 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
    switch(kind) {
       case K_CONV:    return launch_mid<N, V, LAYOUT, K_CONV>(p, s);
       case K_CONV_MID:
-         // the four-step middle runs radix 8 at N = 512 .. 4096 only
-         if constexpr(V == 8 && N <= 4096) return launch_mid<N, V, LAYOUT, K_CONV_MID>(p, s);
-         else                              return hipErrorInvalidValue;
+         // the four-step middle: N = 512 .. 4096, radix 16 (the reference's
+         // middle) or radix 8
+         if constexpr(N >= 512 && N <= 4096) return launch_mid<N, V, LAYOUT, K_CONV_MID>(p, s);
+         else                                return hipErrorInvalidValue;
       case K_CONV_R2: return launch_one<N, V, LAYOUT, K_CONV_R2, MID_MUL>(p, s);
       case K_FWD:     return launch_one<N, V, LAYOUT, K_FWD, MID_NONE>(p, s);
       case K_APPLY:   return launch_mid<N, V, LAYOUT, K_APPLY>(p, s);

@@ -33,6 +33,20 @@
 extern "C" {
 #endif
 
+/* ---- ABI version ----------------------------------------------------------
+ * Bumped whenever an entry point's arguments or the meaning of an id change,
+ * so that a caller built against one header can refuse a library built from
+ * another (compare fufft_abi_version() with FUFFT_ABI_VERSION):
+ *   2  FUFFT_LAYOUT_LANE (1) became the lane-major pair layout (the one-value
+ *      lane-major layout moved to FUFFT_LAYOUT_BPERM, 2); the 2D calls and
+ *      fufft_conv_r2_f32 gained `layout`;
+ *   3  the four-step calls (fufft_large_digit_order, fufft_plan_filter_large_
+ *      f32 and _device_f32, fufft_conv_large_f32) gained `variant`, and the
+ *      default four-step middle is the reference's radix-16 one.
+ * No reference counterpart (the reference ships no library). */
+#define FUFFT_ABI_VERSION 3
+int fufft_abi_version(void);
+
 /* ---- status -------------------------------------------------------------- */
 #define FUFFT_OK                0
 #define FUFFT_ERR_INVALID      -1   /* null pointer, bad count, stride or enum */
@@ -246,7 +260,7 @@ int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t c
                                  int variant, int layout, int filter_kind,
                                  int fold_inv_n, void* stream);
 int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n,
-                                       int64_t count, int filter_kind,
+                                       int64_t count, int variant, int filter_kind,
                                        int fold_inv_n, void* stream);
 int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t w,
                                    int64_t count, int layout, int filter_kind,
@@ -319,23 +333,50 @@ int fufft_bfp_scaled_dequantize(const int16_t* q, const float* scale, int64_t n,
  * ceiling beside MI355X's 8 TB/s, and this copy of known size scales the
  * rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes. */
 int fufft_stream_f32(const void* in, void* out, int64_t bytes, int nontemporal, void* stream);
+/* The same copy in a chosen shape, so that the ceiling is the best of a sweep
+ * of shapes rather than one configuration (same argument rules as above):
+ *   load_bytes       8 or 16 bytes per load and store (16: the stream copy
+ *                    above; 8: the float2 width of the conv kernels' I/O);
+ *   loads_per_lane   1, 2, 4, 8, 16 or 32 loads per lane in flight before
+ *                    the stores (a workgroup tile of 256 lanes x that many);
+ *   tiles_per_group  1..4096 consecutive tiles per workgroup, in a loop;
+ *   groups           0, or a persistent grid of that many workgroups that
+ *                    stride over the tiles (tiles_per_group is then ignored);
+ *   load_policy,     cache-policy bits of the loads and of the stores, 0..3:
+ *   store_policy     SC0 = 1, NT = 2 (streaming), as the gfx950 buffer
+ *                    instructions take them.
+ * fufft_stream_f32 is (16, 8, 1, 0, p, p) with p = 0 or NT.  No reference
+ * counterpart (measurement only). */
+int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int load_bytes,
+                           int loads_per_lane, int tiles_per_group, int groups,
+                           int load_policy, int store_policy, void* stream);
 
 /* ---- four-step large N -------------------------------------------------------------
  * N = 16^lout * mid with mid a single-launch size: lout radix-16 DIF levels
  * over HBM, the fused conv on contiguous mid-point chunks in place, lout DIT
  * levels (run_large / MidLaunch, bench_fufft.cu:357-492;
  * fufft_outer_pass_r, fufft.cuh:1113-1140).  buf is transformed in place.
- * filt is in the chained digit order (fufft_large_digit_order).
+ * fufft_large_plan gives lout and mid (the fewest outer levels that leave
+ * mid <= 4096: 32768 = 16 x 2048, 65536 = 16 x 4096, 262144 = 16^2 x 1024,
+ * as run_large's instantiations, bench_fufft.cu:519-520).
+ * `variant` names the middle's plan and so the filter's chain order,
+ * [16]^lout followed by the middle's radices:
+ *   FUFFT_V16 (and FUFFT_AUTO): the reference's middle, fufft_pipeline_v16 on
+ *     the chunks, so a filter permuted as run_large permutes it
+ *     (bench_fufft.cu:410-428, [16]^lout ++ [lead] ++ [16]^k) passes as it is;
+ *   FUFFT_R8: a radix-8 middle ([16]^lout ++ [lead] ++ [8]^k), the chain of
+ *     the reference's radix-8 conv_foursteps_cfg (verify_kernel.cpp:373-394).
+ * Plan the filter (fufft_large_digit_order, fufft_plan_filter_large_f32 or
+ * its device form) and run the conv with the same variant.
  * The reference makes 4*lout + 3 HBM passes; here the two outer levels of a
  * two-level plan (n >= 2^17) run as one pass through LDS, bit-identical, so
- * every plan reads and writes the data three times.  The middle runs radix 8
- * (FUFFT_R8) at every mid. */
+ * every plan reads and writes the data three times. */
 int fufft_large_plan(int64_t n, int* lout, int* mid);
-int fufft_large_digit_order(int64_t n, int32_t* perm);
-int fufft_plan_filter_large_f32(int64_t n, int filter_kind, int fold_inv_n,
+int fufft_large_digit_order(int64_t n, int variant, int32_t* perm);
+int fufft_plan_filter_large_f32(int64_t n, int variant, int filter_kind, int fold_inv_n,
                                 const float* in, float* out);
 int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride,
-                         int64_t n, int64_t batch, int mid, void* stream);
+                         int64_t n, int64_t batch, int mid, int variant, void* stream);
 
 /* ---- 2D ---------------------------------------------------------------------------
  * h x w images, row-major.  Rows DIF, columns DIF, mid, columns DIT, rows DIT

@@ -147,10 +147,13 @@ inline int pipeline_timed(const void* in, const void* filt, void* out, int64_t n
                                timing_groups, stream);
 }
 
+// the four-step chain order of the reference's V=16 middle by default (bench_fufft.cu:410-428)
 inline int plan_filter_large_device(const void* natural, void* planned, int64_t n, int64_t count = 1,
-                                    void* stream = nullptr, int kind = FUFFT_FILTER_TAPS, bool fold_inv_n = true)
+                                    void* stream = nullptr, int kind = FUFFT_FILTER_TAPS, bool fold_inv_n = true,
+                                    Variant middle = Variant::V16)
 {
-   return fufft_plan_filter_large_device_f32(natural, planned, n, count, kind, fold_inv_n ? 1 : 0, stream);
+   return fufft_plan_filter_large_device_f32(natural, planned, n, count, (int)middle, kind, fold_inv_n ? 1 : 0,
+                                             stream);
 }
 
 // 2D filters default to the reference's column order (verify_kernel.cpp:738-748);
@@ -165,11 +168,12 @@ inline int plan_filter2d_device(const void* natural, void* planned, int64_t h, i
 
 // ---- four-step (run_large, bench_fufft.cu:357-492) ----------------------------------------
 
+// run_large<N, LOUT, 16, MID, lead, nrv>: the middle is fufft_pipeline_v16 (Variant::V16)
 template<class Mid = MidMultiply>
 inline int conv_large(void* buf, const void* filt, int64_t n, int64_t batch, void* stream = nullptr,
-                      int64_t filt_stride = 0)
+                      int64_t filt_stride = 0, Variant middle = Variant::V16)
 {
-   return fufft_conv_large_f32(buf, filt, filt_stride, n, batch, Mid::id, stream);
+   return fufft_conv_large_f32(buf, filt, filt_stride, n, batch, Mid::id, (int)middle, stream);
 }
 
 // ---- 2D (fufft_conv2d, fufft.cuh:1209-1258) -------------------------------------------------

@@ -5,6 +5,7 @@ ref` has built oracle/_ref/libfufft_ref.so:
 
     python -m tests.golden.make_golden              # every fixture
     python -m tests.golden.make_golden bfp_scaled   # only bfp_scaled_n*.npz
+    python -m tests.golden.make_golden fourstep_v16 # only fourstep_n32768_mid2048_v16.npz
 """
 from __future__ import annotations
 
@@ -50,6 +51,23 @@ def bfp_scaled(R) -> None:
                          oq.ctypes.data, osc.ctypes.data, batch)
         _save(f"bfp_scaled_n{n}", kind="bfp_scaled", n=n, aq=aq, asc=asc, bq=bq, bsc=np.array([bsc]),
               oq=oq, osc=osc)
+
+
+def fourstep_v16(R) -> None:
+    """The reference bench's own four-step configuration,
+    run_large<32768, 1, 16, 2048, 8, 2> (bench_fufft.cu:519): one radix-16
+    outer level around the V=16 middle (lead 8, two radix-16 passes), the
+    filter in run_large's chain order (bench_fufft.cu:410-428), computed by
+    the reference's transcription conv_foursteps_cfg with the V=16 middle
+    (verify_kernel.cpp:373-394)."""
+    rng = np.random.default_rng(20261204)
+    n, mid = 32768, 2048
+    a, b = _cu(rng, (1, n)), _cu(rng, (1, n)) / n
+    bdr = np.ascontiguousarray(b[:, O.mixedrev(O.large_plan(1, mid, 16, ref=True))])
+    A = a.copy()
+    R.ref_vk_conv_foursteps_cfg(A.ctypes.data, bdr.ctypes.data, n, 1, 16, mid, 1)
+    _save("fourstep_n32768_mid2048_v16", kind="fourstep", n=n, lout=1, mid=mid, mid_v=16, a=a, bdr=bdr,
+          out=A.reshape(-1))
 
 
 def main() -> None:
@@ -158,14 +176,16 @@ def main() -> None:
          out=A.reshape(-1))
 
     bfp_scaled(R)
+    fourstep_v16(R)
 
 
 if __name__ == "__main__":
     import sys
-    if sys.argv[1:] == ["bfp_scaled"]:           # only the reference-format BFP fixtures
+    parts = {"bfp_scaled": bfp_scaled, "fourstep_v16": fourstep_v16}
+    if sys.argv[1:] and sys.argv[1] in parts:    # only one group of fixtures
         ref = O.load_ref()
         if ref is None:
             raise SystemExit("oracle/_ref/libfufft_ref.so is not built (needs /root/reference)")
-        bfp_scaled(ref)
+        parts[sys.argv[1]](ref)
     else:
         main()

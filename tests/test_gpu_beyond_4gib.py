@@ -98,7 +98,7 @@ def test_conv_large_per_signal_filters_beyond_4gib(dev):
     ff.conv_large(x, f, n=n, batch=batch, filt_stride=n)
     torch.cuda.synchronize()
     lout, mid = ff.large_plan(n)
-    want = O.conv(a_s, f_s, n, O.large_plan(lout, mid, 8), filt_stride=n).reshape(len(idx), n)
+    want = O.conv(a_s, f_s, n, O.large_plan(lout, mid, ff.large_middle("auto")), filt_stride=n).reshape(len(idx), n)
     assert bits_equal(x.view(batch, n)[ti].cpu().numpy(), want)
     del x, f
 

@@ -156,24 +156,27 @@ def test_plan_device_taps_in_place_then_conv(dev, rng):
 
 
 @pytest.mark.parametrize("n", [8192, 32768, 131072])
-def test_plan_device_large(dev, n, rng):
+@pytest.mark.parametrize("variant", ["v16", "r8"])
+def test_plan_device_large(dev, n, variant, rng):
     import torch
     import fufft_amd as ff
     count = 2
     taps = cuniform(rng, (count, n))
     spec = np.fft.fft(taps.astype(np.complex128), axis=1).astype(np.complex64)
-    print(f"case plan large n={n}", flush=True)
+    print(f"case plan large n={n} variant={variant}", flush=True)
     dt, ds = to_dev(taps, dev), to_dev(spec, dev)
     out_t, out_s = torch.empty_like(dt), torch.empty_like(ds)
-    ff.plan_filter_large_device(dt, out_t, n, count, kind=ff.FILTER_TAPS)
-    ff.plan_filter_large_device(ds, out_s, n, count, kind=ff.FILTER_SPECTRUM)
+    ff.plan_filter_large_device(dt, out_t, n, count, kind=ff.FILTER_TAPS, variant=variant)
+    ff.plan_filter_large_device(ds, out_s, n, count, kind=ff.FILTER_SPECTRUM, variant=variant)
     got_t, got_s = from_dev(out_t), from_dev(out_s)
-    host_s = np.stack([ff.plan_filter_large(spec[i], n, kind=ff.FILTER_SPECTRUM) for i in range(count)])
+    host_s = np.stack([ff.plan_filter_large(spec[i], n, kind=ff.FILTER_SPECTRUM, variant=variant)
+                       for i in range(count)])
     assert bits_equal(got_s, host_s)
     lout, mid = ff.large_plan(n)
-    want_t = O.fwd(taps, n, O.large_plan(lout, mid, mid_v=8))          # the middle runs radix 8
+    want_t = O.fwd(taps, n, O.large_plan(lout, mid, mid_v=ff.large_middle(variant)))
     assert bits_equal(got_t.reshape(-1), scaled(want_t, 1.0 / n))
-    host_t = np.stack([ff.plan_filter_large(taps[i], n, kind=ff.FILTER_TAPS) for i in range(count)])
+    host_t = np.stack([ff.plan_filter_large(taps[i], n, kind=ff.FILTER_TAPS, variant=variant)
+                       for i in range(count)])
     assert O.rel_l2(got_t, host_t) <= 1e-6
 
 

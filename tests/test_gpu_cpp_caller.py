@@ -20,7 +20,7 @@ EXE = Path(__file__).resolve().parent / "cpp" / "_build" / "abi_gpu_check"
 
 
 def test_cpp_caller_through_the_c_abi(dev):
-    assert EXE.exists(), f"{EXE} is missing: run python -m fufft_amd.build"
+    assert EXE.exists(), f"{EXE} is missing: run python fufft_amd/build.py"
     print("case C++ caller n=4096 batch=16", flush=True)
     out = subprocess.run([str(EXE)], capture_output=True, text=True, timeout=120)
     print(out.stdout.strip(), out.stderr.strip(), flush=True)

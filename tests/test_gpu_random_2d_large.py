@@ -73,7 +73,8 @@ def test_random_config(dev, seed):
     if c["op"] == "large":
         n = c["n"]
         lout, mid_n = ff.large_plan(n)
-        plan = O.large_plan(lout, mid_n, 8)
+        # the default middle, the reference's radix-16 one
+        plan = O.large_plan(lout, mid_n, ff.large_middle("auto"))
         a = cuniform(rng, batch * n)
         filt = np.concatenate([ff.plan_filter_large(cuniform(rng, n), n, kind=ff.FILTER_TAPS)
                                for _ in range(nf)])

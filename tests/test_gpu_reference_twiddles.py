@@ -56,9 +56,12 @@ def _golden():
 
 
 # fixtures whose plan a GPU kernel runs (the GPU's smallest sizes are N = 256
-# radix 16 and N = 512 radix 8; its four-step middle is radix 8 in [512, 4096])
+# radix 16 and N = 512 radix 8; its four-step middle is radix 16 or radix 8 in
+# [512, 4096]; fourstep_n32768_mid2048_v16 is the reference bench's own
+# run_large<32768, 1, 16, 2048, 8, 2>)
 GPU_FIXTURES = ["v16_n512", "v16_n1024", "v16_n2048", "v16_n4096", "r8_n512", "r8_n1024",
-                "r8_n2048", "r8_n4096", "split_n512", "r2_n512", "fourstep_n8192_mid512_r8", "conv2d_64x64"]
+                "r8_n2048", "r8_n4096", "split_n512", "r2_n512", "fourstep_n8192_mid512_r8",
+                "fourstep_n32768_mid2048_v16", "conv2d_64x64"]
 
 
 @pytest.mark.parametrize("name", GPU_FIXTURES)
@@ -117,8 +120,12 @@ def test_gpu_equals_reference_on_golden_fixture(ref_tw, name):
         n = int(case["n"])
         lout, mid = ff.large_plan(n)
         assert (lout, mid) == (int(case["lout"]), int(case["mid"]))
+        # the middle the fixture was made with: the reference's V=16 run_large
+        # middle by default, radix 8 where the fixture says so
+        variant = "r8" if "mid_v" in case and int(case["mid_v"]) == 8 else "v16"
         buf = to_dev(case["a"], dev)
-        ff.conv_large(buf, to_dev(case["bdr"], dev), n=n, batch=case["a"].size // n, filt_stride=n)
+        ff.conv_large(buf, to_dev(case["bdr"], dev), n=n, batch=case["a"].size // n, filt_stride=n,
+                      variant=variant)
         assert bits_equal(host(buf), case["out"])
     else:
         raise AssertionError(kind)
@@ -150,17 +157,18 @@ def test_conv_equals_libm_oracle(ref_tw, variant, n, mid, rng):
 
 
 @pytest.mark.parametrize("n", [32768, 65536])
-def test_fourstep_equals_libm_oracle(ref_tw, n, rng):
+@pytest.mark.parametrize("variant", ["v16", "r8"])
+def test_fourstep_equals_libm_oracle(ref_tw, n, variant, rng):
     import fufft_amd as ff
     dev = ref_tw
     lout, mid = ff.large_plan(n)
-    plan = O.large_plan(lout, mid, 8)
+    plan = O.large_plan(lout, mid, ff.large_middle(variant))
     a = cuniform(rng, (2, n))
     spec = cuniform(rng, n) / n
     fdr = spec[O.mixedrev(plan)]
-    print(f"case reftw fourstep n={n}", flush=True)
+    print(f"case reftw fourstep n={n} variant={variant}", flush=True)
     buf = to_dev(a, dev)
-    ff.conv_large(buf, to_dev(fdr, dev), n=n, batch=2)
+    ff.conv_large(buf, to_dev(fdr, dev), n=n, batch=2, variant=variant)
     got = host(buf)
     assert bits_equal(got, O.conv(a, fdr, n, plan, tw=O.TW_LIBM))
     assert O.rel_l2(got, O.conv_spec_f64(a, spec, n)) <= TOL_F32

@@ -35,6 +35,13 @@ def test_every_declared_symbol_is_exported():
     assert not missing, missing
 
 
+def test_abi_version_matches_header():
+    import fufft_amd as ff
+    text = (ROOT / "include" / "fufft" / "fufft.h").read_text()
+    declared = int(re.search(r"#define FUFFT_ABI_VERSION\s+(\d+)", text).group(1))
+    assert ff.lib.fufft_abi_version() == declared == ff.ABI_VERSION
+
+
 @pytest.mark.parametrize("variant,v", [("v16", 16), ("r8", 8)])
 @pytest.mark.parametrize("n", [256, 512, 1024, 2048, 4096, 8192, 16384])
 def test_plan_and_digit_order_match_oracle(variant, v, n):
@@ -61,12 +68,47 @@ def test_auto_variant_rule():
             ff.fastest_variant(bad, "lane")
 
 
+def run_large_chain_order(n, lout, mid):
+    """The filter permutation run_large builds (bench_fufft.cu:410-428), restated
+    from its loop: digit widths [4]*lout ++ [log2 lead] ++ [4]*nrv of the V=16
+    middle, each index's digits read from the top, reassembled reversed."""
+    lead_bits = int(np.log2(mid)) % 4
+    wid = [4] * lout + ([lead_bits] if lead_bits else []) + [4] * (int(np.log2(mid)) // 4)
+    mb = sum(wid)
+    out = np.empty(n, dtype=np.int64)
+    for i in range(n):
+        pos, dg = mb, []
+        for w in wid:
+            pos -= w
+            dg.append((i >> pos) & ((1 << w) - 1))
+        r, op = 0, mb
+        for k in range(len(wid) - 1, -1, -1):
+            op -= wid[k]
+            r |= dg[k] << op
+        out[i] = r
+    return out
+
+
 @pytest.mark.parametrize("n", [8192, 32768, 65536, 131072])
-def test_large_plan_matches_oracle(n):
+@pytest.mark.parametrize("variant,v", [("v16", 16), ("r8", 8), ("auto", 16)])
+def test_large_plan_matches_oracle(n, variant, v):
     import fufft_amd as ff
     lout, mid = ff.large_plan(n)
     assert 16 ** lout * mid == n and 512 <= mid <= 4096
-    assert np.array_equal(ff.large_digit_order(n), O.mixedrev(O.large_plan(lout, mid, 8)))
+    assert np.array_equal(ff.large_digit_order(n, variant), O.mixedrev(O.large_plan(lout, mid, v)))
+
+
+@pytest.mark.parametrize("n,lout,mid", [(32768, 1, 2048), (65536, 1, 4096), (8192, 1, 512)])
+def test_large_v16_chain_is_run_large_order(n, lout, mid):
+    """The default four-step chain is the reference's: a filter permuted as
+    run_large<32768, 1, 16, 2048, 8, 2> permutes it passes unchanged."""
+    import fufft_amd as ff
+    assert ff.large_plan(n) == (lout, mid)
+    want = run_large_chain_order(n, lout, mid)
+    assert np.array_equal(ff.large_digit_order(n), want)
+    assert np.array_equal(ff.large_digit_order(n, "v16"), want)
+    # the radix-8 middle is a different order (it is not the reference's GPU chain)
+    assert not np.array_equal(ff.large_digit_order(n, "r8"), want)
 
 
 def test_filter_planning_1d_layouts(rng):
@@ -103,8 +145,9 @@ def test_filter_planning_large_and_2d(rng):
     n = 32768
     taps = crandn(rng, n)
     want = np.fft.fft(taps.astype(np.complex128)) / n
-    got = ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS)
-    assert np.max(np.abs(got - want[ff.large_digit_order(n)])) <= 2e-7 * np.max(np.abs(want))
+    for variant in ("auto", "v16", "r8"):
+        got = ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS, variant=variant)
+        assert np.max(np.abs(got - want[ff.large_digit_order(n, variant)])) <= 2e-7 * np.max(np.abs(want))
     h, w = 256, 1024
     taps2 = crandn(rng, h * w)
     vr, vc = ff.plan2d(h, w)
@@ -196,8 +239,11 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 256, 1, 64, 0, 1, 0, None) == ff.ERR_UNSUPPORTED
     for block in (32, 96, 8192):                # below 64, not a power of two, longer than n
         assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 4096, 1, block, 0, 1, 0, None) == ff.ERR_INVALID
-    assert L.fufft_conv_large_f32(fake, fake, 0, 4096, 1, 0, None) == ff.ERR_UNSUPPORTED
-    assert L.fufft_conv_large_f32(fake, fake, 3, 32768, 1, 0, None) == ff.ERR_INVALID
+    assert L.fufft_conv_large_f32(fake, fake, 0, 4096, 1, 0, 2, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_large_f32(fake, fake, 3, 32768, 1, 0, 2, None) == ff.ERR_INVALID
+    assert L.fufft_conv_large_f32(fake, fake, 0, 32768, 1, 0, 7, None) == ff.ERR_INVALID   # variant
+    assert L.fufft_large_digit_order(32768, 7, (C.c_int32 * 32768)()) == ff.ERR_INVALID
+    assert L.fufft_plan_filter_large_f32(32768, 7, 1, 1, fake, fake) == ff.ERR_INVALID
     assert L.fufft_conv2d_f32(fake, fake, 0, fake, 128, 512, 1, 0, 0, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 100, 1, 0, 0, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_conv2d_f32(fake, fake, 5, fake, 512, 512, 1, 0, 0, None) == ff.ERR_INVALID
@@ -219,7 +265,8 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_c2c_f32(fake + 8, fake, 4096, 1, -1, 2, None) == ff.ERR_ALIGN
     assert L.fufft_plan_filter_device_f32(fake, fake, 4096, 1, 2, 0, 0, 1, None) == ff.ERR_INVALID
     assert L.fufft_plan_filter_device_f32(fake, fake + 16, 4096, 1, 2, 0, 5, 1, None) == ff.ERR_INVALID
-    assert L.fufft_plan_filter_large_device_f32(fake, fake, 4096, 1, 1, 1, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter_large_device_f32(fake, fake, 4096, 1, 2, 1, 1, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter_large_device_f32(fake, fake + 16, 32768, 1, 7, 1, 1, None) == ff.ERR_INVALID
     assert L.fufft_plan_filter2d_device_f32(fake, fake, 512, 100, 1, 0, 1, 1, None) == ff.ERR_UNSUPPORTED
     assert L.fufft_plan_filter2d_device_f32(fake, fake + 16, 512, 512, 1, 7, 1, 1, None) == ff.ERR_INVALID
     # the reference-format BFP conv and codec
@@ -235,6 +282,18 @@ def test_status_codes_without_gpu_calls():
     assert S(fake, fake, fake, fake, 0, fake, fake, 4096, 1, 0, 0, 3, None) == ff.ERR_INVALID  # unknown layout
     assert L.fufft_bfp_scaled_quantize(None, 64, 1, fake, fake) == ff.ERR_INVALID
     assert L.fufft_bfp_scaled_quantize(fake, 0, 1, fake, fake) == ff.ERR_INVALID
+    # the stream copy's shape is checked before any launch
+    SS = L.fufft_stream_shape_f32
+    assert SS(fake, fake + 1024, 4096, 16, 6, 1, 0, 0, 0, None) == ff.ERR_INVALID      # loads per lane
+    assert SS(fake, fake + 1024, 4096, 16, 64, 1, 0, 0, 0, None) == ff.ERR_INVALID
+    assert SS(fake, fake + 1024, 4096, 4, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID       # load width
+    assert SS(fake, fake + 1024, 4096, 16, 8, 0, 0, 0, 0, None) == ff.ERR_INVALID      # tiles per group
+    assert SS(fake, fake + 1024, 4096, 16, 8, 1, -1, 0, 0, None) == ff.ERR_INVALID     # groups
+    assert SS(fake, fake + 1024, 4096, 16, 8, 1, 0, 4, 0, None) == ff.ERR_INVALID      # load policy
+    assert SS(fake, fake + 1024, 4096, 16, 8, 1, 0, 0, 4, None) == ff.ERR_INVALID      # store policy
+    assert SS(fake, fake + 1024, 4100, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID      # not 16-byte granular
+    assert SS(fake, fake, 4096, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID             # in == out
+    assert SS(fake + 8, fake + 1024, 4096, 16, 8, 1, 0, 0, 0, None) == ff.ERR_ALIGN
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("misaligned pointer")
     assert "scratch" in L.fufft_status_string(ff.ERR_SCRATCH).decode()
 
@@ -263,7 +322,7 @@ def test_mid_policy_registry():
         assert L.fufft_conv_f32(fake, fake, 0, fake, 4096, 1, mid, 2, 0, None) == ff.ERR_INVALID
         assert L.fufft_apply_f32(fake, 4096, fake, 0, fake + 16, 4096, 1, mid, 2, 0, None) == ff.ERR_INVALID
         assert L.fufft_conv_bfp16(fake, fake, fake, 0, fake, fake, 4096, 1, 64, mid, 1, 0, None) == ff.ERR_INVALID
-        assert L.fufft_conv_large_f32(fake, fake, 0, 32768, 1, mid, None) == ff.ERR_INVALID
+        assert L.fufft_conv_large_f32(fake, fake, 0, 32768, 1, mid, 2, None) == ff.ERR_INVALID
         assert L.fufft_conv2d_f32(fake, fake, 0, fake, 512, 512, 1, mid, 0, None) == ff.ERR_INVALID
         assert L.fufft_apply2d_f32(fake, 0, fake, 0, fake + 16, 512, 512, 1, mid, 0, None) == ff.ERR_INVALID
 
