@@ -624,19 +624,41 @@ def bfp_scaled_quantize(x: np.ndarray, n: int) -> tuple[np.ndarray, np.ndarray]:
     return q, sc[: src.size // n]
 
 
+def _int16_words(q) -> np.ndarray:
+    """BFP words as a contiguous int16 array; any other dtype is refused (an
+    int32 array would otherwise be read as pairs of int16)."""
+    q = np.asarray(q)
+    if q.dtype != np.int16:
+        raise TypeError(f"BFP words must be int16, got {q.dtype}")
+    return np.ascontiguousarray(q).reshape(-1)
+
+
 def bfp_scaled_dequantize(q: np.ndarray, scale: np.ndarray, n: int) -> np.ndarray:
+    q = _int16_words(q)
+    if n < 1 or q.size % (2 * n):
+        raise ValueError(f"{q.size} int16 words are not whole transforms of {n} points")
     count = q.size // (2 * n)
+    sc = np.ascontiguousarray(scale, dtype=np.float32).reshape(-1)
+    if sc.size < count:
+        raise ValueError(f"{count} transforms need {count} scales, {sc.size} given")
     x = np.empty(count * n, dtype=np.complex64)
-    check(lib.fufft_bfp_scaled_dequantize(np.ascontiguousarray(q).ctypes.data,
-                                          np.ascontiguousarray(scale, dtype=np.float32).ctypes.data, n, count,
-                                          x.ctypes.data), "fufft_bfp_scaled_dequantize")
+    check(lib.fufft_bfp_scaled_dequantize(q.ctypes.data, sc.ctypes.data, n, count, x.ctypes.data),
+          "fufft_bfp_scaled_dequantize")
     return x
 
 
 def bfp_dequantize(q: np.ndarray, e: np.ndarray, block: int = BFP_BLOCK) -> np.ndarray:
+    q = _int16_words(q)
     npts = q.size // 2
+    if q.size % 2 or block < 1 or npts % block:
+        raise ValueError(f"{q.size} int16 words are not whole blocks of {block} points")
+    ex = np.asarray(e)
+    if ex.dtype != np.int8:
+        raise TypeError(f"BFP exponents must be int8, got {ex.dtype}")
+    ex = np.ascontiguousarray(ex).reshape(-1)
+    if ex.size < npts // block:
+        raise ValueError(f"{npts // block} blocks need {npts // block} exponents, {ex.size} given")
     x = np.empty(npts, dtype=np.complex64)
-    check(lib.fufft_bfp_dequantize(np.ascontiguousarray(q).ctypes.data,
-                                   np.ascontiguousarray(e).ctypes.data, npts, block, x.ctypes.data),
+    check(lib.fufft_bfp_dequantize(q.ctypes.data, ex.ctypes.data, npts, block, x.ctypes.data),
           "fufft_bfp_dequantize")
     return x

@@ -30,12 +30,19 @@ template<class Mid> inline bool reads_filter() { return fufft_mid_reads_filter(M
 enum class Variant : int { V16 = FUFFT_V16, R8 = FUFFT_R8, Auto = FUFFT_AUTO };
 
 inline const char* status_string(int status) { return fufft_status_string(status); }
+// true when the loaded library was built from this header (FUFFT_ABI_VERSION)
+inline bool abi_matches() { return fufft_abi_version() == FUFFT_ABI_VERSION; }
 inline int init(int device = 0) { return fufft_init(device); }
 inline bool supported(int64_t n, Variant v = Variant::Auto) { return fufft_supported(n, (int)v) != 0; }
-// the faster variant for a filter layout (FUFFT_LAYOUT_LANE: radix 16 from n = 1024 on)
-inline Variant fastest_variant(int64_t n, int layout = FUFFT_LAYOUT_LANE)
+// the faster variant for a filter layout (FUFFT_LAYOUT_LANE: radix 16 from n = 1024 on);
+// returns FUFFT_OK, or the library's negative status (an unsupported n or an
+// unknown layout) with *out left unchanged
+inline int fastest_variant(int64_t n, Variant* out, int layout = FUFFT_LAYOUT_LANE)
 {
-   return fufft_fastest_variant(n, layout) == FUFFT_R8 ? Variant::R8 : Variant::V16;
+   const int v = fufft_fastest_variant(n, layout);
+   if(v < 0) return v;
+   if(out) *out = v == FUFFT_R8 ? Variant::R8 : Variant::V16;
+   return FUFFT_OK;
 }
 
 // ---- host planning (bench_fufft.cu:63-82, 156-170) ---------------------------------------

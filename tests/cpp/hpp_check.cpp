@@ -21,8 +21,17 @@ int main()
    if(fufft::pipeline<fufft::MidMultiply>(nullptr, nullptr, nullptr, 1000, 1) != FUFFT_ERR_UNSUPPORTED) return 5;
    if(fufft::conv_large<fufft::MidNothing>(nullptr, nullptr, 1024, 1) != FUFFT_ERR_UNSUPPORTED) return 6;
    if(!fufft::supported(n) || fufft::supported(100)) return 7;
-   if(fufft::fastest_variant(4096) != fufft::Variant::V16 || fufft::fastest_variant(512) != fufft::Variant::R8 ||
-      fufft::fastest_variant(4096, FUFFT_LAYOUT_DR) != fufft::Variant::R8) return 14;
+   if(!fufft::abi_matches()) return 18;
+   {
+      fufft::Variant a = fufft::Variant::Auto, b = fufft::Variant::Auto, c = fufft::Variant::Auto;
+      if(fufft::fastest_variant(4096, &a) != FUFFT_OK || a != fufft::Variant::V16 ||
+         fufft::fastest_variant(512, &b) != FUFFT_OK || b != fufft::Variant::R8 ||
+         fufft::fastest_variant(4096, &c, FUFFT_LAYOUT_DR) != FUFFT_OK || c != fufft::Variant::R8) return 14;
+      // an unsupported size or an unknown layout comes back as a status, the output untouched
+      fufft::Variant d = fufft::Variant::Auto;
+      if(fufft::fastest_variant(1000, &d) != FUFFT_ERR_UNSUPPORTED || d != fufft::Variant::Auto ||
+         fufft::fastest_variant(4096, &d, 9) != FUFFT_ERR_INVALID || d != fufft::Variant::Auto) return 17;
+   }
    if(!fufft::reads_filter<fufft::MidMultiply>() || !fufft::reads_filter<fufft::MidConjMultiply>() ||
       fufft::reads_filter<fufft::MidNothing>() || fufft::mid_reads_filter(3) != FUFFT_ERR_INVALID) return 15;
    if(fufft::c2c<FUFFT_INVERSE>(nullptr, nullptr, n, 1) != FUFFT_ERR_INVALID) return 8;

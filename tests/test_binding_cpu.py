@@ -134,3 +134,25 @@ def test_variant_defaults_are_auto():
     # 2D planners and launches share one default column order
     for name in ("plan_filter2d", "plan_filter2d_device", "conv2d", "conv2d_r2", "apply2d"):
         assert inspect.signature(getattr(fufft_amd, name)).parameters["layout"].default == "dr", name
+
+
+def test_host_bfp_codecs_check_their_arrays(ff):
+    """The host dequantisers refuse words that are not int16, exponents that
+    are not int8, and too few exponents or scales, before the library reads
+    past a host array."""
+    n = 64
+    q = np.zeros(2 * n * 2, dtype=np.int16)
+    with pytest.raises(TypeError, match="int16"):
+        ff.bfp_dequantize(q.astype(np.int32), np.zeros(2, dtype=np.int8), block=64)
+    with pytest.raises(TypeError, match="int8"):
+        ff.bfp_dequantize(q, np.zeros(2, dtype=np.int32), block=64)
+    with pytest.raises(ValueError, match="exponents"):
+        ff.bfp_dequantize(q, np.zeros(1, dtype=np.int8), block=64)
+    with pytest.raises(ValueError, match="whole blocks"):
+        ff.bfp_dequantize(q[:-2], np.zeros(2, dtype=np.int8), block=64)
+    with pytest.raises(TypeError, match="int16"):
+        ff.bfp_scaled_dequantize(q.astype(np.int32), np.ones(2, dtype=np.float32), n)
+    with pytest.raises(ValueError, match="scales"):
+        ff.bfp_scaled_dequantize(q, np.ones(1, dtype=np.float32), n)
+    with pytest.raises(ValueError, match="whole transforms"):
+        ff.bfp_scaled_dequantize(q[:-2], np.ones(2, dtype=np.float32), n)

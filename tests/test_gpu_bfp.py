@@ -213,3 +213,52 @@ def test_bfp_full_batch_lane_layout_fastest_variant(dev, n):
     assert np.array_equal(eo.view(batch, nb)[idx].cpu().numpy(), oe.reshape(16, -1))
     assert np.array_equal(qo.view(batch, 2 * n)[idx].cpu().numpy(), oq.reshape(16, -1))
     del dq, de, qo, eo
+
+
+@pytest.mark.parametrize("n,variant,layout", [(512, "auto", "dr"), (4096, "auto", "dr"),
+                                              (512, "fastest", "lane"), (4096, "fastest", "lane")])
+def test_bfp_config3_full_size(dev, n, variant, layout):
+    """BASELINE config 3 as written: 2^27 points of per-signal Gaussian x 10^u
+    (u ~ U[-3, 3]) signals, quantised by the library's host codec (64-point
+    blocks), one shared fp32 filter, at N = 512 and 4096 with the default
+    plan and with the bench's (lane-major filter at the fastest variant).
+    16 signals spread over the batch: words and exponents bit-identical to
+    the oracle, and rel L2 <= 1e-4 against the fp64 convolution of the
+    unquantised signals (input quantisation included)."""
+    import torch
+    import fufft_amd as ff
+    batch = (1 << 27) // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(31 * n + len(layout))
+    scale = torch.pow(10.0, torch.rand(batch, 1, device=dev, generator=gen) * 6 - 3)
+    x = (torch.randn(batch, n, dtype=torch.complex64, device=dev, generator=gen) * scale).cpu().numpy()
+    del scale
+    q, e = ff.bfp_quantize(x)
+    rng = np.random.default_rng(n)
+    taps = crandn(rng, n)
+    var = ff.fastest_variant(n, layout) if variant == "fastest" else variant
+    v = 8 if ff.resolve_variant(n, var) == "r8" else 16
+    filt = ff.plan_filter(taps, n, variant=var, layout=layout, kind=ff.FILTER_TAPS)
+    fdr = ff.plan_filter(taps, n, variant=var, layout="dr", kind=ff.FILTER_TAPS)
+    dq, de = to_dev(q, dev), to_dev(e, dev)
+    qo, eo = torch.empty_like(dq), torch.empty_like(de)
+    print(f"case bfp config 3 full size n={n} variant={var} layout={layout} batch={batch}", flush=True)
+    ff.conv_bfp16(dq, de, to_dev(filt, dev), qo, eo, n=n, batch=batch, variant=var, layout=layout)
+    idx = np.linspace(0, batch - 1, 16).astype(np.int64)
+    tidx = torch.from_numpy(idx).to(dev)
+    nb = n // 64
+    q_s = q.reshape(batch, 2 * n)[idx]
+    e_s = e.reshape(batch, nb)[idx]
+    oq, oe = O.bfp_conv(q_s, e_s, fdr, n, O.kernel_plan(n, v))
+    torch.cuda.synchronize()
+    got_q = qo.view(batch, 2 * n)[tidx].cpu().numpy()
+    got_e = eo.view(batch, nb)[tidx].cpu().numpy()
+    assert np.array_equal(got_e, oe.reshape(16, -1))
+    assert np.array_equal(got_q, oq.reshape(16, -1))
+    spec = np.fft.fft(taps.astype(np.complex128)) / n
+    want = np.fft.ifft(np.fft.fft(x[idx].astype(np.complex128), axis=1) * spec[None, :] * n, axis=1)
+    got = O.bfp_dequantize(got_q, got_e).reshape(16, n)
+    rel = np.sqrt(np.sum(np.abs(got - want) ** 2) / np.sum(np.abs(want) ** 2))
+    print(f"   rel L2 {rel:.3e}", flush=True)
+    assert rel <= TOL_BFP
+    del dq, de, qo, eo
