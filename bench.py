@@ -89,6 +89,8 @@ def parse():
                    help="wall seconds for all CPU-baseline rows together")
     p.add_argument("--settle", type=float, default=0.1,
                    help="seconds of untimed launches before each secondary figure (0 under PMC runs)")
+    p.add_argument("--no-stream-sweep", action="store_true",
+                   help="skip the sweep of copy shapes (the ceiling is then the best fixed shape; for PMC runs)")
     p.add_argument("--copy-sweep", action="store_true",
                    help="time every copy shape of the stream-ceiling sweep and print one line per shape")
     p.add_argument("--copy-only", action="store_true",
@@ -696,8 +698,8 @@ def main():
         return
     plain_gbs, _ = stream_ceiling(torch, ff, dev, pts, 20, 3, stream, False)
     nt_gbs, _ = stream_ceiling(torch, ff, dev, pts, 20, 3, stream, True)
-    sweep_rows = stream_sweep(torch, ff, dev, pts, 20, 3, stream)
-    best_gbs, best_shape = max(sweep_rows, key=lambda r: r[0])
+    sweep_rows = [] if args.no_stream_sweep else stream_sweep(torch, ff, dev, pts, 20, 3, stream)
+    best_gbs, best_shape = max(sweep_rows, key=lambda r: r[0]) if sweep_rows else (0.0, None)
     ceiling = max(best_gbs, plain_gbs, nt_gbs)
 
     # the headline is timed like every other leg: correctness check first, then
