@@ -11,10 +11,16 @@
 //     definition: dequantise on the host, the fp32 conv on the GPU, quantise
 //     on the host with the same codec (fufft_bfp_scaled_*);
 //   - a small 2D image (64 x 64, one fused launch) against an fp64 direct 2D
-//     cyclic convolution, rel L2 <= 2e-6.
+//     cyclic convolution, rel L2 <= 2e-6;
+//   - the plan objects of include/fufft/plan.hpp (Conv1d with the lane-major
+//     filter at the fastest variant and with the reference's digit order,
+//     Conv1d::from_device, the BFP conv through a Conv1d, ConvLarge with the
+//     reference's V=16 middle, Conv2d) bit for bit against the C calls with
+//     filters planned by hand, and their argument errors as fufft::Error.
 // Built by fufft_amd/build.py into tests/cpp/_build/abi_gpu_check and run by
 // tests/test_gpu_cpp_caller.py.  Prints "ok ..." and returns 0 on success.
 #include "fufft/fufft.hpp"
+#include "fufft/plan.hpp"
 
 #include <hip/hip_runtime.h>
 
@@ -199,11 +205,147 @@ int main()
       if(!(rel2 <= 2e-6)) { std::fprintf(stderr, "2D rel L2 vs fp64 direct %.3e > 2e-6\n", rel2); return 7; }
    }
 
+   // 8. plan objects against the C calls they make, on fresh input
+   int plans = 0;
+   try {
+      std::vector<float> x(2 * pts), want(2 * pts), got(2 * pts), fl(2 * n);
+      for(auto& v : x) v = rng.next();
+      CHECK_HIP(hipMemcpy(d_a, x.data(), pts * 8, hipMemcpyHostToDevice));
+      // (a) the fastest plan: lane-major filter at fufft_fastest_variant's variant
+      fufft::Conv1d<fufft::MidMultiply> fast(n, taps.data());
+      fufft::Variant fv = fufft::Variant::Auto;
+      CHECK_FU(fufft::fastest_variant(n, &fv, FUFFT_LAYOUT_LANE));
+      if(fast.variant() != fv || fast.layout() != FUFFT_LAYOUT_LANE) { std::fprintf(stderr, "Conv1d plan\n"); return 20; }
+      CHECK_FU(fufft::plan_filter(taps.data(), fl.data(), n, fv, FUFFT_FILTER_TAPS, FUFFT_LAYOUT_LANE));
+      CHECK_HIP(hipMemcpy(d_f, fl.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+      CHECK_FU(fufft::pipeline<fufft::MidMultiply>(d_a, d_f, d_o, n, batch, s, 0, fv, FUFFT_LAYOUT_LANE));
+      fast(d_a, d_o2, batch, s);
+      CHECK_HIP(hipStreamSynchronize(s));
+      CHECK_HIP(hipMemcpy(want.data(), d_o, pts * 8, hipMemcpyDeviceToHost));
+      CHECK_HIP(hipMemcpy(got.data(), d_o2, pts * 8, hipMemcpyDeviceToHost));
+      if(!same_bits(want, got)) { std::fprintf(stderr, "Conv1d (lane) differs from the C call\n"); return 21; }
+      plans++;
+      // (b) the reference's own plan and filter order
+      fufft::Conv1d<fufft::MidMultiply> ref(n, taps.data(), 1, FUFFT_FILTER_TAPS, FUFFT_LAYOUT_DR, fufft::Variant::V16);
+      CHECK_FU(fufft::plan_filter(taps.data(), fl.data(), n, fufft::Variant::V16));
+      CHECK_HIP(hipMemcpy(d_f, fl.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+      CHECK_FU(fufft::pipeline<fufft::MidMultiply>(d_a, d_f, d_o, n, batch, s, 0, fufft::Variant::V16));
+      ref(d_a, d_o2, batch, s);
+      CHECK_HIP(hipStreamSynchronize(s));
+      CHECK_HIP(hipMemcpy(want.data(), d_o, pts * 8, hipMemcpyDeviceToHost));
+      CHECK_HIP(hipMemcpy(got.data(), d_o2, pts * 8, hipMemcpyDeviceToHost));
+      if(!same_bits(want, got)) { std::fprintf(stderr, "Conv1d (digit order, V16) differs\n"); return 22; }
+      plans++;
+      // (c) one filter per signal, planned on the device from natural-order
+      //     spectra, against the same spectra planned on the host
+      {
+         const int64_t cnt = batch;
+         std::vector<float> specs(2 * pts);
+         for(auto& v : specs) v = rng.next();
+         fufft::Conv1d<fufft::MidConjMultiply> host(n, specs.data(), cnt, FUFFT_FILTER_SPECTRUM);
+         CHECK_HIP(hipMemcpy(d_spec, specs.data(), pts * 8, hipMemcpyHostToDevice));
+         auto dev = fufft::Conv1d<fufft::MidConjMultiply>::from_device(n, d_spec, cnt, FUFFT_FILTER_SPECTRUM,
+                                                                      FUFFT_LAYOUT_LANE, fufft::Variant::Auto, s);
+         host(d_a, d_o, batch, s);
+         dev(d_a, d_o2, batch, s);
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(want.data(), d_o, pts * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(got.data(), d_o2, pts * 8, hipMemcpyDeviceToHost));
+         if(!same_bits(want, got)) { std::fprintf(stderr, "Conv1d::from_device differs from the host plan\n"); return 23; }
+         // a per-signal plan refuses a batch of another size
+         bool threw = false;
+         try {
+            host(d_a, d_o, batch - 1, s);
+         } catch(const fufft::Error& e) {
+            threw = e.status() == FUFFT_ERR_INVALID;
+         }
+         if(!threw) { std::fprintf(stderr, "per-signal plan accepted a mismatched batch\n"); return 24; }
+         plans++;
+      }
+      // (d) the BFP conv through the same plan as the fp32 conv
+      {
+         std::vector<int16_t> q(2 * pts), qa(2 * pts), qb(2 * pts);
+         std::vector<int8_t> e(pts / 64), ea(pts / 64), eb(pts / 64);
+         CHECK_FU(fufft_bfp_quantize(x.data(), (int64_t)pts, 64, q.data(), e.data()));
+         void *d_q = nullptr, *d_qo = nullptr, *d_e = nullptr, *d_eo = nullptr;
+         CHECK_HIP(hipMalloc(&d_q, pts * 4)); CHECK_HIP(hipMalloc(&d_qo, pts * 4));
+         CHECK_HIP(hipMalloc(&d_e, pts / 64)); CHECK_HIP(hipMalloc(&d_eo, pts / 64));
+         CHECK_HIP(hipMemcpy(d_q, q.data(), pts * 4, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_e, e.data(), pts / 64, hipMemcpyHostToDevice));
+         CHECK_FU(fufft::plan_filter(taps.data(), fl.data(), n, fv, FUFFT_FILTER_TAPS, FUFFT_LAYOUT_LANE));
+         CHECK_HIP(hipMemcpy(d_f, fl.data(), (size_t)n * 8, hipMemcpyHostToDevice));
+         CHECK_FU(fufft::pipeline_bfp<fufft::MidMultiply>(d_q, static_cast<int8_t*>(d_e), d_f, d_qo,
+                                                         static_cast<int8_t*>(d_eo), n, batch, s, 0, fv,
+                                                         FUFFT_LAYOUT_LANE));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(qa.data(), d_qo, pts * 4, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(ea.data(), d_eo, pts / 64, hipMemcpyDeviceToHost));
+         fast.bfp(d_q, static_cast<int8_t*>(d_e), d_qo, static_cast<int8_t*>(d_eo), batch, 64, s);
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(qb.data(), d_qo, pts * 4, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(eb.data(), d_eo, pts / 64, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipFree(d_q)); CHECK_HIP(hipFree(d_qo)); CHECK_HIP(hipFree(d_e)); CHECK_HIP(hipFree(d_eo));
+         if(std::memcmp(qa.data(), qb.data(), qa.size() * 2) != 0 || std::memcmp(ea.data(), eb.data(), ea.size()) != 0) {
+            std::fprintf(stderr, "Conv1d::bfp differs from the C call\n");
+            return 25;
+         }
+         plans++;
+      }
+      // (e) four-step with the reference's V=16 middle, in place
+      {
+         const int64_t nl = 32768, bl = 2;
+         std::vector<float> tl(2 * nl), fl2(2 * nl), xl(2 * nl * bl), a1(2 * nl * bl), a2(2 * nl * bl);
+         for(auto& v : tl) v = rng.next();
+         for(auto& v : xl) v = rng.next();
+         fufft::ConvLarge<fufft::MidMultiply> large(nl, tl.data());
+         if(large.variant() != fufft::Variant::V16 || large.outer_levels() != 1 || large.middle() != 2048) {
+            std::fprintf(stderr, "ConvLarge plan\n");
+            return 26;
+         }
+         CHECK_FU(fufft_plan_filter_large_f32(nl, FUFFT_V16, FUFFT_FILTER_TAPS, 1, tl.data(), fl2.data()));
+         void* d_l = nullptr; void* d_lf = nullptr;
+         CHECK_HIP(hipMalloc(&d_l, (size_t)nl * bl * 8)); CHECK_HIP(hipMalloc(&d_lf, (size_t)nl * 8));
+         CHECK_HIP(hipMemcpy(d_lf, fl2.data(), (size_t)nl * 8, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_l, xl.data(), (size_t)nl * bl * 8, hipMemcpyHostToDevice));
+         CHECK_FU(fufft_conv_large_f32(d_l, d_lf, 0, nl, bl, FUFFT_MID_MUL, FUFFT_V16, s));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(a1.data(), d_l, (size_t)nl * bl * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(d_l, xl.data(), (size_t)nl * bl * 8, hipMemcpyHostToDevice));
+         large(d_l, bl, s);
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(a2.data(), d_l, (size_t)nl * bl * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipFree(d_l)); CHECK_HIP(hipFree(d_lf));
+         if(!same_bits(a1, a2)) { std::fprintf(stderr, "ConvLarge differs from the C call\n"); return 27; }
+         plans++;
+      }
+      // (f) 2D, 64 x 64 (its column order is the identity: both layouts give the same filter)
+      {
+         const int64_t h = 64, w = 64, np = h * w, nimg = 3;
+         std::vector<float> img(2 * np * nimg), t2(2 * np), f2(2 * np), b1(2 * np * nimg), b2(2 * np * nimg);
+         for(auto& v : img) v = rng.next();
+         for(auto& v : t2) v = rng.next();
+         fufft::Conv2d<fufft::MidMultiply> c2(h, w, t2.data());
+         CHECK_FU(fufft_plan_filter2d_f32(h, w, FUFFT_LAYOUT_LANE, FUFFT_FILTER_TAPS, 1, t2.data(), f2.data()));
+         CHECK_HIP(hipMemcpy(d_a, img.data(), np * nimg * 8, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_f, f2.data(), np * 8, hipMemcpyHostToDevice));
+         CHECK_FU(fufft_conv2d_f32(d_a, d_f, 0, d_o, h, w, nimg, FUFFT_MID_MUL, FUFFT_LAYOUT_LANE, s));
+         c2(d_a, d_o2, nimg, s);
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(b1.data(), d_o, np * nimg * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(b2.data(), d_o2, np * nimg * 8, hipMemcpyDeviceToHost));
+         if(!same_bits(b1, b2)) { std::fprintf(stderr, "Conv2d differs from the C call\n"); return 28; }
+         plans++;
+      }
+   } catch(const fufft::Error& e) {
+      std::fprintf(stderr, "plan object: %s\n", e.what());
+      return 29;
+   }
+
    CHECK_HIP(hipFree(d_a)); CHECK_HIP(hipFree(d_f)); CHECK_HIP(hipFree(d_o));
    CHECK_HIP(hipFree(d_o2)); CHECK_HIP(hipFree(d_spec));
    CHECK_HIP(hipStreamDestroy(s));
    std::printf("ok C++ caller: n=%lld batch=%lld, template == C entry == split == in place, rel L2 vs fp64 direct %.2e; "
-               "reference-format BFP == its definition; 64x64 2D rel L2 %.2e\n",
-               (long long)n, (long long)batch, rel, rel2);
+               "reference-format BFP == its definition; 64x64 2D rel L2 %.2e; %d plan objects == their C calls\n",
+               (long long)n, (long long)batch, rel, rel2, plans);
    return 0;
 }

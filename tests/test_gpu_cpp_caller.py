@@ -6,8 +6,11 @@ with include/fufft/fufft.hpp, and checks the template surface against an fp64
 direct cyclic convolution (rel L2 <= 2e-6) and, bit for bit, against the raw C
 entry point, the split forward/apply path and an in-place call; the int16 BFP
 conv in the reference's own format bit for bit against dequantise -> fp32 conv
--> quantise; and a 64 x 64 image (one fused launch) against an fp64 direct 2D
-cyclic convolution.
+-> quantise; a 64 x 64 image (one fused launch) against an fp64 direct 2D
+cyclic convolution; and the plan objects of include/fufft/plan.hpp (Conv1d
+lane-major / digit order / planned on the device / BFP, ConvLarge with the
+reference's V=16 middle, Conv2d) bit for bit against the C calls with filters
+planned by hand, a per-signal plan refusing a mismatched batch.
 """
 import subprocess
 from pathlib import Path

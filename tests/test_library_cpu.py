@@ -341,3 +341,25 @@ def test_cpp_mirror_header_builds_and_runs(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
     assert out.returncode == 0, (out.returncode, out.stderr)
     assert out.stdout.startswith("ok")
+
+
+def test_cpp_plan_objects_build_and_reject_bad_arguments(tmp_path):
+    """include/fufft/plan.hpp (plan objects that own their device filter)
+    compiles with g++ against the HIP headers, and each plan object throws
+    fufft::Error with the C ABI status before any allocation or device call
+    (tests/cpp/plan_check.cpp)."""
+    import shutil
+    import subprocess
+    rocm = Path("/opt/rocm")
+    if shutil.which("g++") is None or not (rocm / "include" / "hip" / "hip_runtime_api.h").exists():
+        pytest.skip("g++ or the HIP headers are not available")
+    lib_dir = ROOT / "fufft_amd"
+    exe = tmp_path / "plan_check"
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+                    f"-I{ROOT / 'include'}", f"-I{rocm / 'include'}",
+                    str(ROOT / "tests" / "cpp" / "plan_check.cpp"), f"-L{lib_dir}", "-lfufft_amd",
+                    f"-L{rocm / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{lib_dir}", f"-Wl,-rpath,{rocm / 'lib'}",
+                    "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, (out.returncode, out.stdout, out.stderr)
+    assert out.stdout.startswith("ok")
