@@ -1,6 +1,6 @@
 """Seeded random configurations of the 2D and four-step entry points against
 the oracle, bit for bit: shape, batch (ragged), mid operation, filter order,
-per-item filters, broadcast spectra and aliasing are drawn per case, so
+per-item filters, broadcast spectra, aliasing and the four-step middle are drawn per case, so
 combinations the targeted tests do not list still run.  Every case prints its
 parameters first.  FUFFT_RANDOM_SEEDS=a:b runs seeds a .. b-1 instead of the
 default 30 (the same variable as the 1D sweep).
@@ -37,6 +37,7 @@ def draw(seed):
     elif op == "large":
         c["n"] = int(rng.choice(LARGE))
         c["batch"] = int(rng.integers(1, max(2, min(5, MAX_POINTS // c["n"] + 1))))
+        c["middle"] = ["v16", "r8"][rng.integers(2)]
     else:
         h = int(rng.choice(HEIGHTS))
         w = int(rng.choice([x for x in WIDTHS if h * x <= MAX_IMAGE]))
@@ -73,15 +74,15 @@ def test_random_config(dev, seed):
     if c["op"] == "large":
         n = c["n"]
         lout, mid_n = ff.large_plan(n)
-        # the default middle, the reference's radix-16 one
-        plan = O.large_plan(lout, mid_n, ff.large_middle("auto"))
+        # the middle drawn for the case: the reference's radix-16 one or radix 8
+        plan = O.large_plan(lout, mid_n, ff.large_middle(c["middle"]))
         a = cuniform(rng, batch * n)
-        filt = np.concatenate([ff.plan_filter_large(cuniform(rng, n), n, kind=ff.FILTER_TAPS)
+        filt = np.concatenate([ff.plan_filter_large(cuniform(rng, n), n, kind=ff.FILTER_TAPS, variant=c["middle"])
                                for _ in range(nf)])
         stride = n if c["per_item"] else 0
         buf = dt(a)
         gfilt = None if (mid == "none" and c["null_filter"]) else dt(filt)
-        ff.conv_large(buf, gfilt, n=n, batch=batch, filt_stride=stride, mid=mid)
+        ff.conv_large(buf, gfilt, n=n, batch=batch, filt_stride=stride, mid=mid, variant=c["middle"])
         torch.cuda.synchronize()
         assert bits_equal(buf.cpu().numpy(), O.conv(a, filt, n, plan, filt_stride=stride, mid=mid))
         return
