@@ -211,9 +211,13 @@ int fastest_variant(int64_t n, int layout)
    if(layout == FUFFT_LAYOUT_LANE || layout == FUFFT_LAYOUT_BPERM) return n == 512 ? FUFFT_R8 : FUFFT_V16;
    // digit order: one rule for every call a digit-order filter or spectrum
    // ties together.  At N = 4096 the fp32 conv alone runs radix 16 faster
-   // (331 / 320 Gpt/s, its filter read staged through LDS), the BFP conv is
-   // even (370 / 367) and the split apply, reading a digit-order spectrum,
-   // runs radix 8 9% faster (371 / 340), so radix 8 stays
+   // (335 / 327 Gpt/s, its filter read staged through LDS), the BFP conv is
+   // even (374 / 371) and the split apply runs radix 8 9% faster (367 / 338,
+   // both with the spectrum read staged through LDS at radix 16), so radix 8
+   // stays.  At N = 8192 radix 16 wins the fp32 conv (275 / 258), the split
+   // apply (342 / 334) and the C2C (358 / 345), radix 8 the BFP conv (310 /
+   // 297); the rule keeps radix 8 there, as filters planned at FUFFT_AUTO by
+   // earlier builds expect
    return (n == 512 || n == 4096 || n == 8192) ? FUFFT_R8 : FUFFT_V16;
 }
 

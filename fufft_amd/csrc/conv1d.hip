@@ -129,6 +129,16 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
             r[2 * m] = make_float2(q.x, q.y);
             r[2 * m + 1] = make_float2(q.z, q.w);
          }
+      } else if constexpr(V == 16 && N >= 2048) {
+         // digit order at radix 16: each wavefront's 64 * 16 slots are
+         // contiguous, loaded in 1 KiB runs and handed to its lanes through
+         // LDS (as the filter read below); read in place every 16-byte load
+         // of a wavefront touches 64 cache lines.  Same box, 2^27 points,
+         // bit-identical: N = 2048 336 -> 369, 8192 312 -> 342 Gpt/s, 4096
+         // even (339).  The LDS reads complete before the filter read reuses
+         // the same positions (wavefront fence)
+         load_dr_staged<PL, typename LD::template at<PL, PL::NP - 2>>(r, sb, modulo_count(t, p.scount) * N, A, L);
+         pass_barrier<64>();
       } else {
          // digit order: slots L*V .. L*V+V-1, two complex per 16-byte load
          const uint32_t so = (modulo_count(t, p.scount) * N + L * V) * 8u;

@@ -611,10 +611,9 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
 // (position L*V + k under that pass's layout LDL), which no other wavefront
 // touches until this one's inverse scatters to them, so a wavefront fence
 // orders the hand-over.  Needs whole wavefronts per transform (T >= 64).
-template<class PL, class LDL, int MID>
-__device__ __forceinline__ void mid_op_dr_staged(float2 (&r)[PL::V], const Buf& f, uint32_t fslot0, float2* A, int L)
+template<class PL, class LDL>
+__device__ __forceinline__ void load_dr_staged(float2 (&b)[PL::V], const Buf& f, uint32_t fslot0, float2* A, int L)
 {
-   using Op = MidOf<MID>;
    constexpr int V = PL::V;
    static_assert(PL::T >= 64, "whole wavefronts per transform");
    const int wl = L & 63, w0 = (L & ~63) * V;      // lane in the wavefront, the wavefront's first slot
@@ -628,11 +627,18 @@ __device__ __forceinline__ void mid_op_dr_staged(float2 (&r)[PL::V], const Buf& 
       A[LDL::phys(s + 1)] = make_float2(q[m].z, q[m].w);
    }
    pass_barrier<64>();
-   float2 b[V];
 #pragma unroll
    for(int k = 0; k < V; k++) b[k] = A[LDL::phys(L * V + k)];
+}
+
+template<class PL, class LDL, int MID>
+__device__ __forceinline__ void mid_op_dr_staged(float2 (&r)[PL::V], const Buf& f, uint32_t fslot0, float2* A, int L)
+{
+   using Op = MidOf<MID>;
+   float2 b[PL::V];
+   load_dr_staged<PL, LDL>(b, f, fslot0, A, L);
 #pragma unroll
-   for(int k = 0; k < V; k++) r[k] = Op::apply(r[k], b[k]);
+   for(int k = 0; k < PL::V; k++) r[k] = Op::apply(r[k], b[k]);
 }
 
 // The lane's V filter values one at a time, value k at voff + k*kstep (the
