@@ -516,7 +516,11 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.filt = filt; p.out0 = out;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
-   return run_conv1d(K_CONV, (int)n, v, p, stream);
+   // one lane-major filter per signal at radix 16, N = 4096: the kernel that
+   // loads each signal's filter with the signal (K_CONV_PSF)
+   const bool psf = conv_psf_plan((int)n, v) && layout == FUFFT_LAYOUT_LANE && filt_stride == n &&
+                    mid_needs_filter(mid);
+   return run_conv1d(psf ? K_CONV_PSF : K_CONV, (int)n, v, p, stream);
 }
 
 static_assert(TIMER_STRIDE == FUFFT_TIMER_STRIDE, "timer record layout");

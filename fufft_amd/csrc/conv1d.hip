@@ -77,10 +77,13 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
    constexpr bool C2C_INV   = KIND == K_C2C_INV;
    constexpr bool PLAN      = KIND == K_PLAN_TAPS;
    constexpr bool TIMED     = KIND == K_CONV_TIMED;
+   // one lane-major filter per signal: its loads go out with the signal's
+   constexpr bool PSF       = KIND == K_CONV_PSF && mid_reads_filter<MID>;
    // the signal read and the result written once per launch stream past the
    // caches in the single-launch conv and C2C; the four-step middle, the split
    // and 2D row kernels keep the default policy
-   constexpr int  IO_POL    = (KIND == K_CONV || TIMED || C2C_FWD || C2C_INV) ? POL_NT : POL_DEFAULT;
+   constexpr int  IO_POL    = (KIND == K_CONV || KIND == K_CONV_PSF || TIMED || C2C_FWD || C2C_INV) ? POL_NT
+                                                                                              : POL_DEFAULT;
    constexpr int  EL_IN     = REAL_IN ? 4 : 8;
    constexpr int  EL_OUT    = REAL_OUT ? 4 : 8;
 
@@ -116,6 +119,7 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
    constexpr int KEEP_I = KEEP_F == KEEP_STORE ? KEEP_USE : KEEP_NONE;
    KeptChain<PL> kc;
    float2 r[V];
+   float4 pf[PSF ? V / 2 : 1];
 
    if constexpr(FROM_SPEC) {
       const Buf sb(p.spec, p.scount * (uint32_t)N * 8u);
@@ -172,6 +176,18 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
 #pragma unroll
          for(int q = 0; q < V; q++) r[q] = xb.ld2<IO_POL>(lane_pos * 8u, q * T * 8);
       }
+      if constexpr(PSF) {
+         // each signal's own filter is a third stream from HBM: issued here,
+         // its latency hides behind the forward DIF instead of the mid phase.
+         // N = 4096, one filter per signal, same box: 234.0 / 234.5 -> 243.4 /
+         // 243.7 Gpt/s (+4%, bit-identical); at N = 1024 / 2048 +0.7% / even,
+         // and with a shared (cache-resident) filter -0.4% for the kept chain
+         // it gives up, so it is this plan's per-signal kernel only
+         const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
+         const uint32_t so = modulo_count(t, p.fcount) * N * 8u + L * 16u;
+#pragma unroll
+         for(int m = 0; m < V / 2; m++) pf[m] = fb.ld4(so, m * T * 16);
+      }
       stamp(1);
       if constexpr(C2C_INV) natural_to_digit<PL, LD, LANES, true>(r, A, L);
       else                  forward_dif<PL, LD, LANES, 64, KEEP_F>(r, A, L, tw, kc);
@@ -207,7 +223,15 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
          const uint32_t fb0 = modulo_count(t, p.fcount) * N;
          // a uniform branch on the filter layout: each side computes only its own offset
-         if constexpr(BPERM)    mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
+         if constexpr(PSF) {
+            using Op = MidOf<MID>;
+#pragma unroll
+            for(int m = 0; m < V / 2; m++) {
+               r[2 * m]     = Op::apply(r[2 * m], make_float2(pf[m].x, pf[m].y));
+               r[2 * m + 1] = Op::apply(r[2 * m + 1], make_float2(pf[m].z, pf[m].w));
+            }
+         }
+         else if constexpr(BPERM) mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
          else if(p.fl == FLT_DR) {
             // radix 16 from N = 2048 (the reference's own plan and filter
             // order): through LDS, N = 2048 / 4096 / 8192 334 -> 348, 312 ->
@@ -325,6 +349,13 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
 {
    switch(kind) {
       case K_CONV:    return launch_mid<N, V, LAYOUT, K_CONV>(p, s);
+      case K_CONV_PSF:
+         // lane-major filters only (the launcher's choice)
+         if constexpr(conv_psf_plan(N, V)) {
+            return p.fl == FLT_LANE ? launch_mid<N, V, LAYOUT, K_CONV_PSF>(p, s) : hipErrorInvalidValue;
+         } else {
+            return hipErrorInvalidValue;
+         }
       case K_CONV_MID:
          // the four-step middle: N = 512 .. 4096, radix 16 (the reference's
          // middle) or radix 8

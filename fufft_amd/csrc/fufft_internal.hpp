@@ -51,11 +51,18 @@ __host__ __device__ constexpr uint32_t lane_position(uint32_t slot, uint32_t tlo
 // layout fl (digit order or lane-major).
 // K_CONV_TIMED: K_CONV with the phase timer (a timestamp after the load, the
 // forward DIF, the mid operation, the inverse DIT and the store).
-// K_CONV_MID: K_CONV as the four-step middle (radix 8, N <= 4096), whose
+// K_CONV_MID: K_CONV as the four-step middle (N = 512 .. 4096), whose
 // chunks the next launch reads again: default cache policy, where K_CONV
 // streams its signal and result past the caches (POL_NT).
+// K_CONV_PSF: K_CONV for one lane-major filter per signal at radix 16,
+// N = 4096: the filter loads go out with the signal loads (without the kept
+// twiddle chain, for the registers they hold through the forward DIF).
 enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5,
-       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9, K_CONV_MID = 10 };
+       K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9, K_CONV_MID = 10,
+       K_CONV_PSF = 11 };
+
+// the plans K_CONV_PSF is built for
+constexpr bool conv_psf_plan(int n, int v) { return n == 4096 && v == 16; }
 
 // phase timer record of one workgroup (K_CONV_TIMED), TIMER_STRIDE words:
 // [0] HW_ID, [1] XCC_ID, [2] marks, [3] s_memrealtime ticks (100 MHz) from

@@ -41,7 +41,8 @@ LLVM = Path("/opt/rocm/llvm/bin")
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 
 KINDS = {0: "conv", 1: "conv_r2", 2: "fwd", 3: "apply", 4: "fwd_r2", 5: "apply_r2",
-         6: "c2c_fwd", 7: "c2c_inv", 8: "plan_taps", 9: "conv_timed", 10: "conv_mid"}
+         6: "c2c_fwd", 7: "c2c_inv", 8: "plan_taps", 9: "conv_timed", 10: "conv_mid",
+         11: "conv_psf"}
 MIDS = {0: "mul", 1: "conj", 2: "none"}
 LAYOUTS = {0: "xor", 1: "pad", 2: "xchg"}
 
