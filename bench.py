@@ -113,11 +113,12 @@ def stream_ceiling(torch, ff, dev, pts, steps, warmup, stream, nontemporal):
     return 2.0 * pts * 8 * steps / secs / 1e9, secs / steps
 
 
-# The copy shapes of the ceiling sweep (fufft_stream_shape_f32): loads in
-# flight per lane, consecutive tiles per workgroup or a persistent grid of
-# workgroups (0 = one launch-wide grid), and the cache policies of loads and
-# stores (SC0 = 1, NT = 2).
-SWEEP_SHAPES = [(w, loads) for w in (16, 8) for loads in (1, 2, 4, 8, 16, 32)]
+# The copy shapes of the ceiling sweep (fufft_stream_shape_f32): lanes per
+# workgroup, bytes per load and loads in flight per lane, consecutive tiles per
+# workgroup or a persistent grid of workgroups (0 = one launch-wide grid), and
+# the cache policies of loads and stores (SC0 = 1, NT = 2).
+SWEEP_SHAPES = [(lanes, w, loads) for lanes in (256, 64, 1024) for w in (16, 8) for loads in (1, 2, 4, 8, 16, 32)
+                if lanes * w * loads <= 256 * 1024]
 SWEEP_GRID = ((1, 0), (2, 0), (4, 0), (1, 1024), (1, 2048), (1, 4096))
 SWEEP_POLICY = ((0, 0), (2, 2), (2, 0), (0, 2), (3, 3))
 
@@ -132,19 +133,21 @@ def stream_sweep(torch, ff, dev, pts, steps, warmup, stream):
     nbytes = pts * 8
     rows = []
     time_launches(torch, lambda: ff.stream_copy(x, y, nbytes, True, stream=stream), 1, 1, stream, SETTLE_S)
-    for width, loads in SWEEP_SHAPES:
+    for lanes, width, loads in SWEEP_SHAPES:
         for per, groups in SWEEP_GRID:
             for pld, pst in SWEEP_POLICY:
                 y.zero_()
 
                 def copy():
-                    ff.stream_copy_shape(x, y, nbytes, loads, per, groups, pld, pst, width=width, stream=stream)
+                    ff.stream_copy_shape(x, y, nbytes, loads, per, groups, pld, pst, width=width, lanes=lanes,
+                                         stream=stream)
                 secs = time_launches(torch, copy, steps, warmup, stream, 0.0)
                 torch.cuda.synchronize()
                 if not torch.equal(x, y):
-                    raise RuntimeError(f"stream copy shape {(width, loads, per, groups, pld, pst)} copied wrongly")
+                    raise RuntimeError(f"stream copy shape {(lanes, width, loads, per, groups, pld, pst)} "
+                                       "copied wrongly")
                 rows.append((2.0 * nbytes * steps / secs / 1e9,
-                             {"load_bytes": width, "loads_per_lane": loads, "tiles_per_group": per,
+                             {"lanes": lanes, "load_bytes": width, "loads_per_lane": loads, "tiles_per_group": per,
                               "groups": groups, "load_policy": pld, "store_policy": pst}))
     del x, y
     return rows

@@ -24,7 +24,7 @@ except ImportError:  # pragma: no cover - torch is part of the image
 
 _LIB_PATH = Path(__file__).resolve().parent / "libfufft_amd.so"
 
-ABI_VERSION = 3                   # FUFFT_ABI_VERSION of the header this binding follows
+ABI_VERSION = 4                   # FUFFT_ABI_VERSION of the header this binding follows
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_ALIGN, ERR_SCRATCH = 0, -1, -2, -3, -4, -5
 SCRATCH_BYTES = 64 << 20          # FUFFT_SCRATCH_BYTES
 MID = {"mul": 0, "conj": 1, "none": 2}
@@ -107,7 +107,7 @@ def _load() -> C.CDLL:
         "fufft_apply2d_f32": ([vp, i64, vp, i64, vp, i64, i64, i64, i32, i32, vp], i32),
         "fufft_c2c_f32": ([vp, vp, i64, i64, i32, i32, vp], i32),
         "fufft_stream_f32": ([vp, vp, i64, i32, vp], i32),
-        "fufft_stream_shape_f32": ([vp, vp, i64, i32, i32, i32, i32, i32, i32, vp], i32),
+        "fufft_stream_shape_f32": ([vp, vp, i64, i32, i32, i32, i32, i32, i32, i32, vp], i32),
         "fufft_transforms_per_workgroup": ([i64, i32], i32),
         "fufft_conv_timed_f32": ([vp, vp, i64, vp, i64, i64, i32, i32, i32, vp, i64, vp], i32),
         "fufft_plan_filter_device_f32": ([vp, vp, i64, i64, i32, i32, i32, i32, vp], i32),
@@ -588,13 +588,14 @@ def stream_copy(inp, out, nbytes: int, nontemporal: bool = False, stream=None) -
 
 
 def stream_copy_shape(inp, out, nbytes: int, loads: int = 8, per: int = 1, groups: int = 0,
-                      load_policy: int = 0, store_policy: int = 0, width: int = 16, stream=None) -> None:
-    """The stream copy in a chosen shape (fufft_stream_shape_f32): `loads`
-    loads of `width` bytes per lane in flight, `per` consecutive tiles per
-    workgroup or a persistent grid of `groups` workgroups, cache policies
-    SC0 = 1, NT = 2."""
+                      load_policy: int = 0, store_policy: int = 0, width: int = 16, lanes: int = 256,
+                      stream=None) -> None:
+    """The stream copy in a chosen shape (fufft_stream_shape_f32): workgroups
+    of `lanes` lanes, `loads` loads of `width` bytes per lane in flight, `per`
+    consecutive tiles per workgroup or a persistent grid of `groups`
+    workgroups, cache policies SC0 = 1, NT = 2."""
     pi, po = _ptrs((inp, "inp", nbytes, "complex"), (out, "out", nbytes, "complex"))
-    check(lib.fufft_stream_shape_f32(pi, po, nbytes, width, loads, per, groups, load_policy, store_policy,
+    check(lib.fufft_stream_shape_f32(pi, po, nbytes, lanes, width, loads, per, groups, load_policy, store_policy,
                                      _stream(stream)), "fufft_stream_shape_f32")
 
 

@@ -775,15 +775,17 @@ int fufft_stream_f32(const void* in, void* out, int64_t bytes, int nontemporal, 
    return status_of(launch_stream(in, out, (uint64_t)bytes, nontemporal != 0, static_cast<hipStream_t>(stream)));
 }
 
-int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int load_bytes, int loads_per_lane,
-                           int tiles_per_group, int groups, int load_policy, int store_policy, void* stream)
+int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int lanes, int load_bytes,
+                           int loads_per_lane, int tiles_per_group, int groups, int load_policy,
+                           int store_policy, void* stream)
 {
    if(!in || !out || in == out || bytes < 0 || (bytes & 15)) return FUFFT_ERR_INVALID;
-   if(!stream_shape_ok(load_bytes, loads_per_lane, tiles_per_group, groups, load_policy, store_policy))
+   if(!stream_shape_ok(lanes, load_bytes, loads_per_lane, tiles_per_group, groups, load_policy, store_policy))
       return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
-   return status_of(launch_stream_shape(in, out, (uint64_t)bytes, load_bytes, loads_per_lane, tiles_per_group,
-                                        groups, load_policy, store_policy, static_cast<hipStream_t>(stream)));
+   return status_of(launch_stream_shape(in, out, (uint64_t)bytes, lanes, load_bytes, loads_per_lane,
+                                        tiles_per_group, groups, load_policy, store_policy,
+                                        static_cast<hipStream_t>(stream)));
 }
 
 // ---- BFP host codec -----------------------------------------------------------------

@@ -160,13 +160,13 @@ hipError_t launch_outer_pass(float2* buf, int64_t n, int64_t batch, int64_t M, b
 // copy of bytes (a multiple of 16) with 16-byte buffer loads and stores;
 // nontemporal adds the NT cache policy
 hipError_t launch_stream(const void* in, void* out, uint64_t bytes, bool nontemporal, hipStream_t s);
-// the same copy in a given shape: loads (1 .. 32, a power of two) loads of
-// width (8 or 16) bytes per lane in flight, per consecutive tiles per
-// workgroup or (groups > 0) a persistent grid of that many workgroups, cache
-// policies pld / pst (SC0 = 1, NT = 2)
-bool stream_shape_ok(int width, int loads, int per, int groups, int pld, int pst);
-hipError_t launch_stream_shape(const void* in, void* out, uint64_t bytes, int width, int loads, int per,
-                               int groups, int pld, int pst, hipStream_t s);
+// the same copy in a given shape: workgroups of lanes (64, 256, 1024) lanes,
+// loads (1 .. 32, a power of two) loads of width (8 or 16) bytes per lane in
+// flight, per consecutive tiles per workgroup or (groups > 0) a persistent
+// grid of that many workgroups, cache policies pld / pst (SC0 = 1, NT = 2)
+bool stream_shape_ok(int lanes, int width, int loads, int per, int groups, int pld, int pst);
+hipError_t launch_stream_shape(const void* in, void* out, uint64_t bytes, int lanes, int width, int loads,
+                               int per, int groups, int pld, int pst, hipStream_t s);
 
 // ---- 2D column kernels (conv2d.hip) -------------------------------------------------
 struct ColParams {

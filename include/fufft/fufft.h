@@ -42,9 +42,10 @@ extern "C" {
  *      fufft_conv_r2_f32 gained `layout`;
  *   3  the four-step calls (fufft_large_digit_order, fufft_plan_filter_large_
  *      f32 and _device_f32, fufft_conv_large_f32) gained `variant`, and the
- *      default four-step middle is the reference's radix-16 one.
+ *      default four-step middle is the reference's radix-16 one;
+ *   4  fufft_stream_shape_f32 gained `lanes` (workgroup size).
  * No reference counterpart (the reference ships no library). */
-#define FUFFT_ABI_VERSION 3
+#define FUFFT_ABI_VERSION 4
 int fufft_abi_version(void);
 
 /* ---- status -------------------------------------------------------------- */
@@ -335,19 +336,21 @@ int fufft_bfp_scaled_dequantize(const int16_t* q, const float* scale, int64_t n,
 int fufft_stream_f32(const void* in, void* out, int64_t bytes, int nontemporal, void* stream);
 /* The same copy in a chosen shape, so that the ceiling is the best of a sweep
  * of shapes rather than one configuration (same argument rules as above):
+ *   lanes            64, 256 or 1024 lanes per workgroup;
  *   load_bytes       8 or 16 bytes per load and store (16: the stream copy
  *                    above; 8: the float2 width of the conv kernels' I/O);
  *   loads_per_lane   1, 2, 4, 8, 16 or 32 loads per lane in flight before
- *                    the stores (a workgroup tile of 256 lanes x that many);
+ *                    the stores (a workgroup tile of lanes x that many, at
+ *                    most 256 KiB);
  *   tiles_per_group  1..4096 consecutive tiles per workgroup, in a loop;
  *   groups           0, or a persistent grid of that many workgroups that
  *                    stride over the tiles (tiles_per_group is then ignored);
  *   load_policy,     cache-policy bits of the loads and of the stores, 0..3:
  *   store_policy     SC0 = 1, NT = 2 (streaming), as the gfx950 buffer
  *                    instructions take them.
- * fufft_stream_f32 is (16, 8, 1, 0, p, p) with p = 0 or NT.  No reference
- * counterpart (measurement only). */
-int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int load_bytes,
+ * fufft_stream_f32 is (256, 16, 8, 1, 0, p, p) with p = 0 or NT.  No
+ * reference counterpart (measurement only). */
+int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int lanes, int load_bytes,
                            int loads_per_lane, int tiles_per_group, int groups,
                            int load_policy, int store_policy, void* stream);
 

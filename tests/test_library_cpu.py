@@ -284,16 +284,18 @@ def test_status_codes_without_gpu_calls():
     assert L.fufft_bfp_scaled_quantize(fake, 0, 1, fake, fake) == ff.ERR_INVALID
     # the stream copy's shape is checked before any launch
     SS = L.fufft_stream_shape_f32
-    assert SS(fake, fake + 1024, 4096, 16, 6, 1, 0, 0, 0, None) == ff.ERR_INVALID      # loads per lane
-    assert SS(fake, fake + 1024, 4096, 16, 64, 1, 0, 0, 0, None) == ff.ERR_INVALID
-    assert SS(fake, fake + 1024, 4096, 4, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID       # load width
-    assert SS(fake, fake + 1024, 4096, 16, 8, 0, 0, 0, 0, None) == ff.ERR_INVALID      # tiles per group
-    assert SS(fake, fake + 1024, 4096, 16, 8, 1, -1, 0, 0, None) == ff.ERR_INVALID     # groups
-    assert SS(fake, fake + 1024, 4096, 16, 8, 1, 0, 4, 0, None) == ff.ERR_INVALID      # load policy
-    assert SS(fake, fake + 1024, 4096, 16, 8, 1, 0, 0, 4, None) == ff.ERR_INVALID      # store policy
-    assert SS(fake, fake + 1024, 4100, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID      # not 16-byte granular
-    assert SS(fake, fake, 4096, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID             # in == out
-    assert SS(fake + 8, fake + 1024, 4096, 16, 8, 1, 0, 0, 0, None) == ff.ERR_ALIGN
+    assert SS(fake, fake + 1024, 4096, 128, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID     # lanes
+    assert SS(fake, fake + 1024, 4096, 256, 16, 6, 1, 0, 0, 0, None) == ff.ERR_INVALID     # loads per lane
+    assert SS(fake, fake + 1024, 4096, 1024, 16, 32, 1, 0, 0, 0, None) == ff.ERR_INVALID   # 512 KiB tile
+    assert SS(fake, fake + 1024, 4096, 256, 16, 64, 1, 0, 0, 0, None) == ff.ERR_INVALID
+    assert SS(fake, fake + 1024, 4096, 256, 4, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID      # load width
+    assert SS(fake, fake + 1024, 4096, 256, 16, 8, 0, 0, 0, 0, None) == ff.ERR_INVALID     # tiles per group
+    assert SS(fake, fake + 1024, 4096, 256, 16, 8, 1, -1, 0, 0, None) == ff.ERR_INVALID    # groups
+    assert SS(fake, fake + 1024, 4096, 256, 16, 8, 1, 0, 4, 0, None) == ff.ERR_INVALID     # load policy
+    assert SS(fake, fake + 1024, 4096, 256, 16, 8, 1, 0, 0, 4, None) == ff.ERR_INVALID     # store policy
+    assert SS(fake, fake + 1024, 4100, 256, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID     # not 16-byte granular
+    assert SS(fake, fake, 4096, 256, 16, 8, 1, 0, 0, 0, None) == ff.ERR_INVALID            # in == out
+    assert SS(fake + 8, fake + 1024, 4096, 256, 16, 8, 1, 0, 0, 0, None) == ff.ERR_ALIGN
     assert L.fufft_status_string(ff.ERR_ALIGN).decode().startswith("misaligned pointer")
     assert "scratch" in L.fufft_status_string(ff.ERR_SCRATCH).decode()
 
