@@ -192,6 +192,45 @@ bool pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
+// The device buffers of one call either coincide, where the call works in
+// place, or share no byte.  A partial overlap would let one workgroup's (or
+// one sub-batch's) stores land in data that another still has to read, so
+// the entry points return FUFFT_ERR_INVALID for it.
+struct Span {
+   const void* p;
+   uint64_t    bytes;
+};
+
+static bool disjoint(Span a, Span b)
+{
+   if(!a.p || !b.p || a.bytes == 0 || b.bytes == 0) return true;
+   const uintptr_t x = reinterpret_cast<uintptr_t>(a.p), y = reinterpret_cast<uintptr_t>(b.p);
+   return x + a.bytes <= y || y + b.bytes <= x;
+}
+
+// in place (the same bytes) or apart
+static bool same_or_disjoint(Span a, Span b) { return (a.p == b.p && a.bytes == b.bytes) || disjoint(a, b); }
+
+// bytes of a filter or spectrum argument: one (stride 0) or one per item
+static uint64_t per_item_bytes(int64_t stride, int64_t batch, int64_t item_bytes)
+{
+   return (uint64_t)(stride == 0 ? 1 : batch) * (uint64_t)item_bytes;
+}
+
+// the real two-for-one conv's buffers (1D or 2D, items of `pts` points):
+// u and v each in place of x or y or apart from both, u and v apart, the
+// filter and a caller workspace apart from every other argument
+static bool r2_buffers_ok(const float* x, const float* y, const void* filt, int64_t filt_stride, const float* u,
+                          const float* v, const void* work, uint64_t work_bytes, int64_t pts, int64_t batch)
+{
+   const uint64_t b = (uint64_t)(pts * batch * 4);
+   const Span sx{x, b}, sy{y, b}, su{u, b}, sv{v, b}, sf{filt, per_item_bytes(filt_stride, batch, pts * 8)};
+   const Span sw{work, work_bytes};
+   return same_or_disjoint(sx, su) && same_or_disjoint(sx, sv) && same_or_disjoint(sy, su) &&
+          same_or_disjoint(sy, sv) && disjoint(su, sv) && disjoint(su, sf) && disjoint(sv, sf) &&
+          disjoint(sw, sx) && disjoint(sw, sy) && disjoint(sw, su) && disjoint(sw, sv) && disjoint(sw, sf);
+}
+
 // The faster variant for an N and a filter layout, one rule for the fp32 and
 // the BFP conv (a filter planned for one serves both).  Same box, 2^27
 // points, Gpt/s radix 8 / radix 16:
@@ -513,6 +552,9 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
    Conv1dParams p{};
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   const Span si{in, (uint64_t)(n * batch * 8)}, so{out, si.bytes};
+   const Span sf{mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, n * 8)};
+   if(!same_or_disjoint(si, so) || !disjoint(so, sf)) return FUFFT_ERR_INVALID;
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.filt = filt; p.out0 = out;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
@@ -550,6 +592,12 @@ int fufft_conv_timed_f32(const void* in, const void* filt, int64_t filt_stride, 
    Conv1dParams p{};
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
    if((uint64_t)p.fcount * (uint64_t)n * 8 > 0xffffffffull) return FUFFT_ERR_UNSUPPORTED;
+   const Span si{in, (uint64_t)(n * batch * 8)}, so{out, si.bytes};
+   const Span sf{mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, n * 8)};
+   const Span st_{timing, (uint64_t)timing_groups * TIMER_STRIDE * 4};
+   if(!same_or_disjoint(si, so) || !disjoint(so, sf) || !disjoint(st_, si) || !disjoint(st_, so) ||
+      !disjoint(st_, sf))
+      return FUFFT_ERR_INVALID;
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.filt = filt; p.out0 = out;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
@@ -565,6 +613,8 @@ int fufft_fwd_f32(const void* in, void* spec, int64_t n, int64_t batch,
    if(st != FUFFT_OK) return st;
    if(!in || !spec) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(spec)) return FUFFT_ERR_ALIGN;
+   if(!same_or_disjoint({in, (uint64_t)(n * batch * 8)}, {spec, (uint64_t)(n * batch * 8)}))
+      return FUFFT_ERR_INVALID;
    Conv1dParams p{};
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.out0 = spec; p.ntrans = (uint32_t)batch;
@@ -584,9 +634,12 @@ int fufft_apply_f32(const void* spec, int64_t spec_stride, const void* filt,
    Conv1dParams p{};
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
    if((st = filter_count(spec_stride, n, batch, &p.scount)) != FUFFT_OK) return st;
-   // a spectrum shared by the batch must not be overwritten by the first
-   // transform while the others still read it
-   if(spec_stride == 0 && batch > 1 && spec == out) return FUFFT_ERR_INVALID;
+   // in place only with one spectrum per transform: a spectrum shared by the
+   // batch would be overwritten by the first transform while the others
+   // still read it
+   const Span ss{spec, per_item_bytes(spec_stride, batch, n * 8)}, so{out, (uint64_t)(n * batch * 8)};
+   const Span sf{mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, n * 8)};
+   if(!same_or_disjoint(ss, so) || !disjoint(so, sf)) return FUFFT_ERR_INVALID;
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.spec = spec; p.filt = filt; p.out0 = out;
    p.ntrans = (uint32_t)batch; p.mid = mid; p.fl = layout;
@@ -605,6 +658,7 @@ int fufft_conv_r2_f32(const float* x, const float* y, const void* filt,
       return FUFFT_ERR_ALIGN;
    Conv1dParams p{};
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   if(!r2_buffers_ok(x, y, filt, filt_stride, u, v, nullptr, 0, n, batch)) return FUFFT_ERR_INVALID;
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = x; p.in1 = y; p.filt = filt; p.out0 = u; p.out1 = v;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = FUFFT_MID_MUL; p.fl = layout;
@@ -622,6 +676,8 @@ int fufft_c2c_f32(const void* in, void* out, int64_t n, int64_t batch, int direc
    if(direction != FUFFT_FORWARD && direction != FUFFT_INVERSE) return FUFFT_ERR_INVALID;
    if(!in || !out) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   if(!same_or_disjoint({in, (uint64_t)(n * batch * 8)}, {out, (uint64_t)(n * batch * 8)}))
+      return FUFFT_ERR_INVALID;
    Conv1dParams p{};
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.out0 = out; p.ntrans = (uint32_t)batch;
@@ -659,6 +715,8 @@ int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t c
    if((st = check_plan_kind(filter_kind)) != FUFFT_OK) return st;
    if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   if(!same_or_disjoint({in, (uint64_t)(n * count * 8)}, {out, (uint64_t)(n * count * 8)}))
+      return FUFFT_ERR_INVALID;
    const float scale = fold_inv_n ? 1.0f / (float)n : 1.0f;   // a power of two: exact
    if(filter_kind == FUFFT_FILTER_SPECTRUM) {
       int r[64];
@@ -699,6 +757,14 @@ int fufft_conv_bfp16(const void* qin, const int8_t* ein, const void* filt,
    BfpParams p{};
    int st;
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   {
+      const uint64_t qb = (uint64_t)(n * batch * 4), eb = (uint64_t)(batch * (n / block));
+      const Span sq{qin, qb}, sqo{qout, qb}, se{ein, eb}, seo{eout, eb};
+      const Span sf{mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, n * 8)};
+      if(!same_or_disjoint(sq, sqo) || !same_or_disjoint(se, seo) || !disjoint(sq, seo) || !disjoint(se, sqo) ||
+         !disjoint(sqo, seo) || !disjoint(sf, sqo) || !disjoint(sf, seo))
+         return FUFFT_ERR_INVALID;
+   }
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
    p.qin = qin; p.ein = ein; p.filt = filt; p.qout = qout; p.eout = eout;
@@ -740,6 +806,17 @@ int fufft_conv_bfp16_scaled(const void* qin, const float* sin, const void* qfilt
    BfpScaledParams p{};
    int st;
    if((st = filter_count(filt_stride, n, batch, &p.fcount)) != FUFFT_OK) return st;
+   {
+      const uint64_t qb = (uint64_t)(n * batch * 4), sb = (uint64_t)(batch * 4);
+      const Span sq{qin, qb}, sqo{qout, qb}, ss{sin, sb}, sso{sout, sb};
+      const bool f = mid_needs_filter(mid);
+      const Span sqf{f ? qfilt : nullptr, per_item_bytes(filt_stride, batch, n * 4)};
+      const Span ssf{f ? sfilt : nullptr, per_item_bytes(filt_stride, batch, 4)};
+      if(!same_or_disjoint(sq, sqo) || !same_or_disjoint(ss, sso) || !disjoint(sq, sso) || !disjoint(ss, sqo) ||
+         !disjoint(sqo, sso) || !disjoint(sqf, sqo) || !disjoint(sqf, sso) || !disjoint(ssf, sqo) ||
+         !disjoint(ssf, sso))
+         return FUFFT_ERR_INVALID;
+   }
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
    p.qin = qin; p.sin = sin; p.qfilt = qfilt; p.sfilt = sfilt; p.qout = qout; p.sout = sout;
@@ -772,6 +849,7 @@ int fufft_stream_f32(const void* in, void* out, int64_t bytes, int nontemporal, 
    if(!in || !out || in == out || bytes < 0 || (bytes & 15) || (nontemporal != 0 && nontemporal != 1))
       return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   if(!disjoint({in, (uint64_t)bytes}, {out, (uint64_t)bytes})) return FUFFT_ERR_INVALID;
    return status_of(launch_stream(in, out, (uint64_t)bytes, nontemporal != 0, static_cast<hipStream_t>(stream)));
 }
 
@@ -783,6 +861,7 @@ int fufft_stream_shape_f32(const void* in, void* out, int64_t bytes, int lanes, 
    if(!stream_shape_ok(lanes, load_bytes, loads_per_lane, tiles_per_group, groups, load_policy, store_policy))
       return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   if(!disjoint({in, (uint64_t)bytes}, {out, (uint64_t)bytes})) return FUFFT_ERR_INVALID;
    return status_of(launch_stream_shape(in, out, (uint64_t)bytes, lanes, load_bytes, loads_per_lane,
                                         tiles_per_group, groups, load_policy, store_policy,
                                         static_cast<hipStream_t>(stream)));
@@ -936,6 +1015,8 @@ int fufft_plan_filter_large_device_f32(const void* in, void* out, int64_t n, int
    if(count < 0 || count * (n / 16) > 0xffffffffll) return FUFFT_ERR_INVALID;
    if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   if(!same_or_disjoint({in, (uint64_t)(n * count * 8)}, {out, (uint64_t)(n * count * 8)}))
+      return FUFFT_ERR_INVALID;
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(count == 0) return FUFFT_OK;
@@ -974,6 +1055,9 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
    if(!aligned16(buf) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
    if(filt_stride != 0 && filt_stride != n) return FUFFT_ERR_INVALID;
    if(!conv1d_supported(mn, v)) return FUFFT_ERR_UNSUPPORTED;
+   if(!disjoint({buf, (uint64_t)(n * batch * 8)},
+                {mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, n * 8)}))
+      return FUFFT_ERR_INVALID;
    Conv1dParams p{};
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
@@ -1203,6 +1287,8 @@ int fufft_plan_filter2d_device_f32(const void* in, void* out, int64_t h, int64_t
    if(!layout_ok(layout)) return FUFFT_ERR_INVALID;
    if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out)) return FUFFT_ERR_ALIGN;
+   if(!same_or_disjoint({in, (uint64_t)(h * w * count * 8)}, {out, (uint64_t)(h * w * count * 8)}))
+      return FUFFT_ERR_INVALID;
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(count == 0) return FUFFT_OK;
@@ -1240,6 +1326,11 @@ int fufft_conv2d_f32(const void* in, const void* filt, int64_t filt_stride, void
    if(!in || !out || (mid_needs_filter(mid) && !filt)) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
    if(filt_stride != 0 && filt_stride != h * w) return FUFFT_ERR_INVALID;
+   {
+      const Span si{in, (uint64_t)(h * w * batch * 8)}, so{out, si.bytes};
+      const Span sf{mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, h * w * 8)};
+      if(!same_or_disjoint(si, so) || !disjoint(so, sf)) return FUFFT_ERR_INVALID;
+   }
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
@@ -1288,6 +1379,8 @@ int fufft_conv2d_r2_f32(const float* x, const float* y, const void* filt, int64_
       !aligned16(work))
       return FUFFT_ERR_ALIGN;
    if(filt_stride != 0 && filt_stride != h * w) return FUFFT_ERR_INVALID;
+   if(!r2_buffers_ok(x, y, filt, filt_stride, u, v, work, (uint64_t)(h * w * batch * 8), h * w, batch))
+      return FUFFT_ERR_INVALID;
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    const int64_t sub = subbatch_items(h * w * 8, batch, SUBBATCH_2D_MB);
@@ -1308,6 +1401,7 @@ int fufft_conv2d_r2_noalloc_f32(const float* x, const float* y, const void* filt
    if(filt_stride != 0 && filt_stride != h * w) return FUFFT_ERR_INVALID;
    const int64_t img_bytes = h * w * 8;
    if(img_bytes > FUFFT_SCRATCH_BYTES) return FUFFT_ERR_SCRATCH;
+   if(!r2_buffers_ok(x, y, filt, filt_stride, u, v, nullptr, 0, h * w, batch)) return FUFFT_ERR_INVALID;
    const float2* tw = nullptr;
    float2* scr = nullptr;
    if((st = current_table(&tw, &scr)) != FUFFT_OK) return st;
@@ -1329,6 +1423,8 @@ int fufft_fwd2d_f32(const void* in, void* spec, int64_t h, int64_t w, int64_t ba
    if(pl.small) return FUFFT_ERR_UNSUPPORTED;      // the fused conv only, as in the reference
    if(!in || !spec) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(spec)) return FUFFT_ERR_ALIGN;
+   if(!same_or_disjoint({in, (uint64_t)(h * w * batch * 8)}, {spec, (uint64_t)(h * w * batch * 8)}))
+      return FUFFT_ERR_INVALID;
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;
@@ -1361,8 +1457,13 @@ int fufft_apply2d_f32(const void* spec, int64_t spec_stride, const void* filt, i
    const int64_t np = h * w;
    if((filt_stride != 0 && filt_stride != np) || (spec_stride != 0 && spec_stride != np))
       return FUFFT_ERR_INVALID;
-   // a spectrum shared by the batch must not be overwritten by the first image
-   if(spec_stride == 0 && batch > 1 && spec == out) return FUFFT_ERR_INVALID;
+   // in place only with one spectrum per image: a spectrum shared by the
+   // batch would be overwritten by the first image while the others read it
+   {
+      const Span ss{spec, per_item_bytes(spec_stride, batch, np * 8)}, so{out, (uint64_t)(np * batch * 8)};
+      const Span sf{mid_needs_filter(mid) ? filt : nullptr, per_item_bytes(filt_stride, batch, np * 8)};
+      if(!same_or_disjoint(ss, so) || !disjoint(so, sf)) return FUFFT_ERR_INVALID;
+   }
    const float2* tw = nullptr;
    if((st = current_table(&tw)) != FUFFT_OK) return st;
    if(batch == 0) return FUFFT_OK;

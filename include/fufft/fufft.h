@@ -16,6 +16,10 @@
  *     asynchronous, stateless and thread-safe across streams.
  *   - Every function returns FUFFT_OK (0) or a negative status; none exits.
  *     HIP launch errors are reported as FUFFT_ERR_HIP.
+ *   - The device buffers of one call either coincide, where the call says
+ *     it works in place (in == out and the like), or share no byte.  Any
+ *     other overlap (an output reaching into an input, the filter or another
+ *     output) returns FUFFT_ERR_INVALID before anything is launched.
  *   - Filters are spectra with 1/N already folded in, in the digit order the
  *     forward DIF leaves behind (see fufft_plan_filter_f32).  filt_stride is 0
  *     (one filter shared by the batch) or n (one filter per signal).
