@@ -905,6 +905,24 @@ def main():
                         "rel_l2": r}
         # the default middle (the reference's) with the radix-8 one beside it
         large[str(s)] = {**legs["v16"], "variant": "v16", "r8_middle": legs["r8"]}
+        if ff.supported(s, "v16"):
+            # the same size as one fused conv (N = 32768: a workgroup per
+            # transform, 32 values per lane), 16 B/pt, both filter layouts
+            single = {}
+            for lay in ("lane", "dr"):
+                a, r = bench_fp32(torch, ff, dev, s, pts, "v16", args.sweep_steps, 3, stream, 6 + s, SETTLE_S,
+                                  layout=lay)
+                if not r <= 2e-6:
+                    print(json.dumps({"error": f"fused conv accuracy check failed at N={s} ({lay}): "
+                                               f"rel L2 {r:.3e}"}))
+                    sys.exit(1)
+                single[lay] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5),
+                               "bytes_per_point": 16, "frac": frac(16.0 * pts + 8.0 * s, a), "rel_l2": r}
+            large[str(s)]["single_launch"] = {
+                "what": "fufft_conv_f32 at this N: one launch, the radix-16 plan with 32 values per lane "
+                        "(not the reference's four-step chain); N(0,1) signals, one shared filter",
+                **single["lane"], "filter_layout": "lane", "dr_filter": single["dr"],
+                "speedup_vs_fourstep": round(legs["v16"]["ms"] / single["lane"]["ms"], 3)}
     if large:
         line["large"] = large
 

@@ -189,6 +189,9 @@ int current_table(const float2** tw, float2** scr = nullptr)
 int status_of(hipError_t e) { return e == hipSuccess ? FUFFT_OK : FUFFT_ERR_HIP; }
 
 bool pow2(int64_t n) { return n > 0 && (n & (n - 1)) == 0; }
+
+// the single-launch kernels' sizes (conv1d.hip): every 1D call
+static bool single_supported(int64_t n, int v) { return pow2(n) && n <= 16384 && conv1d_supported((int)n, v); }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
@@ -400,13 +403,13 @@ const char* fufft_status_string(int status)
 int fufft_supported(int64_t n, int variant)
 {
    const int v = values_per_lane(resolve_variant(n, variant));
-   return (v && pow2(n) && n <= 16384 && conv1d_supported((int)n, v)) ? 1 : 0;
+   return (v && (single_supported(n, v) || conv_wide_plan(n, v))) ? 1 : 0;
 }
 
 int fufft_fastest_variant(int64_t n, int layout)
 {
    if(!layout1d_ok(layout)) return FUFFT_ERR_INVALID;
-   if(!pow2(n) || n < 256 || n > 16384) return FUFFT_ERR_UNSUPPORTED;
+   if(!pow2(n) || n < 256 || n > CONV_WIDE_N) return FUFFT_ERR_UNSUPPORTED;
    return fastest_variant(n, layout);
 }
 
@@ -491,14 +494,16 @@ static_assert(mid_needs_filter(FUFFT_MID_MUL) && !mid_needs_filter(FUFFT_MID_NON
 static_assert(FUFFT_LAYOUT_DR == FLT_DR && FUFFT_LAYOUT_LANE == FLT_LANE && FUFFT_LAYOUT_BPERM == FLT_BPERM,
               "filter layout ids");
 
-static int check_1d(int64_t n, int64_t batch, int variant, int mid, int layout, int* v)
+// wide: the call is the fused conv, which also runs N = 32768 (wide.hip);
+// every other 1D call stops at the single-launch kernels' sizes
+static int check_1d(int64_t n, int64_t batch, int variant, int mid, int layout, int* v, bool wide = false)
 {
    *v = values_per_lane(resolve_variant(n, variant));
    if(!*v) return FUFFT_ERR_INVALID;
    if(!mid_known(mid)) return FUFFT_ERR_INVALID;
    if(!layout1d_ok(layout)) return FUFFT_ERR_INVALID;
    if(batch < 0 || batch > 0xffffffffll) return FUFFT_ERR_INVALID;
-   if(!pow2(n) || !fufft_supported(n, variant)) return FUFFT_ERR_UNSUPPORTED;
+   if(!single_supported(n, *v) && !(wide && conv_wide_plan(n, *v))) return FUFFT_ERR_UNSUPPORTED;
    return FUFFT_OK;
 }
 
@@ -546,7 +551,7 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
                    int layout, void* stream)
 {
    int v = 0;
-   int st = check_1d(n, batch, variant, mid, layout, &v);
+   int st = check_1d(n, batch, variant, mid, layout, &v, true);
    if(st != FUFFT_OK) return st;
    if(!in || !out || (mid_needs_filter(mid) && !filt)) return FUFFT_ERR_INVALID;
    if(!aligned16(in) || !aligned16(out) || (filt && !aligned16(filt))) return FUFFT_ERR_ALIGN;
@@ -558,6 +563,8 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.filt = filt; p.out0 = out;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
+   // N = 32768: one workgroup per transform, 32 values per lane
+   if(conv_wide_plan(n, v)) return status_of(launch_conv_wide(p, static_cast<hipStream_t>(stream)));
    // one lane-major filter per signal at radix 16, N = 4096: the kernel that
    // loads each signal's filter with the signal (K_CONV_PSF)
    const bool psf = conv_psf_plan((int)n, v) && layout == FUFFT_LAYOUT_LANE && filt_stride == n &&

@@ -93,6 +93,14 @@ struct Conv1dParams {
 bool       conv1d_supported(int n, int v);
 hipError_t launch_conv1d(int kind, int n, int v, int layout, const Conv1dParams& p, hipStream_t s);
 
+// ---- fused conv at N = 32768, 32 values per lane (wide.hip) --------------------------
+// The radix-16 plan (LEAD 8, three radix-16 passes) with each lane running two
+// radix-16 lanes' groups; fufft_conv_f32 only (mid, filter layout and stride
+// as there), results bit for bit the radix-16 plan's.
+constexpr int CONV_WIDE_N = 32768;
+constexpr bool conv_wide_plan(int64_t n, int v) { return n == CONV_WIDE_N && v == 16; }
+hipError_t launch_conv_wide(const Conv1dParams& p, hipStream_t s);
+
 // ---- filter planning on the device (plan.hip) ----------------------------------------
 struct GatherDigits {
    int32_t np;             // digit groups (passes)

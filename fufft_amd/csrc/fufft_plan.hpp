@@ -1,16 +1,19 @@
 // Compile-time pass plan and LDS layouts shared by the 1D, BFP and 2D kernels.
 //
-// A transform of N = LEAD * V^NR points is held by T = N/V lanes, V values per
-// lane.  DIF pass p has radix R_p (LEAD first when LEAD > 1, then V) and stride
-// M_p = N / (R_0 ... R_p); DIT runs the same passes in reverse.  In pass p lane
-// L owns the G = V/R groups gidx = L + g*T, j = gidx % M, b = gidx / M, whose
-// taps sit at b*R*M + j + k*M (fufft.cuh:722-756); tap k of group g lives in
-// register g + k*G.  With that convention:
+// A transform of N = LEAD * RM^NR points is held by T = N/V lanes, V values
+// per lane, main radix RM = V (or V/2: the 32-values-per-lane conv, whose lanes
+// each run two radix-16 groups).  DIF pass p has radix R_p (LEAD first when
+// LEAD > 1, then RM) and stride M_p = N / (R_0 ... R_p); DIT runs the same
+// passes in reverse.  In pass p lane L owns the G = V/R groups gidx = L + g*T,
+// j = gidx % M, b = gidx / M, whose taps sit at b*R*M + j + k*M
+// (fufft.cuh:722-756); tap k of group g lives in register g + k*G.  With that
+// convention:
 //   - pass 0 reads position L + q*T into register q, so the first DIF pass
 //     loads straight from HBM and the last DIT pass stores straight to HBM
 //     (coalesced across lanes for every q);
 //   - the last DIF pass and the first DIT pass run at M = 1 with lane L owning
-//     positions L*V .. L*V + V-1 in registers, so the pointwise mid operation
+//     positions L*V .. L*V + V-1 in registers (with two groups per lane,
+//     (L + g*T)*RM + k in register g + 2k), so the pointwise mid operation
 //     happens in registers between them (fufft.cuh:1435-1443);
 //   - every other pass boundary is one exchange through LDS.
 #pragma once
@@ -26,18 +29,21 @@ namespace fufft {
 
 constexpr int ilog2c(int x) { int r = 0; while((1 << r) < x) r++; return r; }
 
-template<int N_, int V_>
+// RM is the radix of the main passes, V by default; with V = 2 * RM every lane
+// runs two groups of each main pass (the 32-values-per-lane conv, wide.hip).
+template<int N_, int V_, int RM_ = V_>
 struct Plan {
-   static constexpr int N = N_, V = V_;
-   static constexpr int LOGN = ilog2c(N), LOGV = ilog2c(V);
-   static constexpr int NR   = LOGN / LOGV;
-   static constexpr int LEAD = 1 << (LOGN % LOGV);
+   static constexpr int N = N_, V = V_, RM = RM_;
+   static constexpr int LOGN = ilog2c(N), LOGV = ilog2c(V), LOGR = ilog2c(RM);
+   static constexpr int NR   = LOGN / LOGR;
+   static constexpr int LEAD = 1 << (LOGN % LOGR);
    static constexpr int NP   = NR + (LEAD > 1 ? 1 : 0);
    static constexpr int T    = N / V;
-   static_assert((1 << LOGN) == N && (1 << LOGV) == V, "power-of-two sizes only");
-   static_assert(NR >= 1, "N must hold at least one radix-V pass");
+   static_assert((1 << LOGN) == N && (1 << LOGV) == V && (1 << LOGR) == RM, "power-of-two sizes only");
+   static_assert(NR >= 1, "N must hold at least one main pass");
+   static_assert(V % RM == 0 && V % LEAD == 0, "whole groups per lane");
 
-   static constexpr int radix(int p) { return (LEAD > 1 && p == 0) ? LEAD : V; }
+   static constexpr int radix(int p) { return (LEAD > 1 && p == 0) ? LEAD : RM; }
    static constexpr int stride(int p)
    {
       int M = N;

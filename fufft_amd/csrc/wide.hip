@@ -1,0 +1,231 @@
+// Fused cyclic convolution at N = 32768 in one launch (gfx950).
+//
+// The reference runs a single-block conv up to N = 4096 and goes four-step
+// beyond (run_large, bench_fufft.cu:357-492: 56 bytes per point over HBM).  A
+// CU of MI355X holds 512 KiB of VGPRs, so one workgroup of 1024 lanes keeps a
+// whole 32768-point transform in registers, 32 values per lane, and the conv
+// becomes the radix-16 plan of the single-launch kernels, LEAD 8 then three
+// radix-16 passes (the plan fufft_pipeline_v16 would run at this N,
+// fufft.cuh:722-800), with each lane doing the work of two radix-16 lanes:
+// groups L and L + T of every radix-16 pass (T = 1024 lanes), four groups of
+// the radix-8 lead pass.  The arithmetic per group is the radix-16 kernels'
+// own (compute_pass, the reference's butterflies and twiddle chains), so the
+// result is bit for bit that plan's and the filter is the radix-16 plan's: in
+// digit order, lane-major pairs or bperm, as fufft_plan_filter_f32 writes them
+// for (32768, FUFFT_V16).  The signal crosses HBM twice (16 bytes per point),
+// the filter once per launch when shared.
+//
+// The exchanges.  A complex exchange of 32768 points needs 256 KiB, beyond
+// the CU's 160 KiB of LDS.  Each exchange therefore runs in two rounds through
+// one float buffer of N + N/16 slots (136 KiB, one spare slot after every 16):
+// every lane writes the real parts of its outgoing values, barrier, reads the
+// real parts of its incoming ones, barrier, the same for the imaginary parts.
+// A lane's register keeps the component it has not yet exchanged, so no
+// register is spent on staging.  Slot of position i: i + i/16.  Every pass's
+// accesses are conflict free under gfx950's 4-byte bank rule: consecutive
+// positions for the M >= 64 passes, 272 / 17 float slots per 16 / 1 lane steps
+// at M = 16 / 1, all distinct modulo 64 within a wavefront.
+//
+// Races.  Within a pass a lane writes the positions it read (same layout on
+// both sides), so the next exchange's first write needs no barrier after the
+// last read; the three barriers separate write from read within a round and
+// the two rounds from each other.  Every wavefront of the workgroup reaches
+// every barrier (one transform per workgroup, the whole group leaves
+// together).
+//
+// Resources: 128 VGPRs with no scratch (16 wavefronts of 1024 lanes, 4 per
+// SIMD), 136 KiB of LDS: one workgroup per CU.  Measured against the
+// four-step at 2^27 points on one MI355X: 137.7 Gpt/s four-step (48 bytes per
+// point over HBM and the Infinity Cache), 173 Gpt/s with the digit-order
+// filter, 190 with the lane-major filter.
+#include "fufft_device.hpp"
+#include "fufft_plan.hpp"
+#include "fufft_internal.hpp"
+
+namespace fufft {
+
+namespace {
+
+using WPlan = Plan<CONV_WIDE_N, 32, 16>;
+using FloatPad = Lds<16, LAYOUT_PAD>;        // float slot of position i: i + i/16
+
+// one component (C = 0 real, 1 imaginary) of the lane's values out to pass P's
+// positions, or in from them
+template<class PL, int P, int C>
+__device__ __forceinline__ void scatter_part(const float2 (&r)[PL::V], float* A, int L)
+{
+   constexpr int R = PL::radix(P), G = PL::V / R, M = PL::stride(P);
+#pragma unroll
+   for(int g = 0; g < G; g++) {
+      const int bp = FloatPad::phys(tap_pos<PL, P>(L, g, 0));
+#pragma unroll
+      for(int k = 0; k < R; k++) A[bp + FloatPad::cphys(k * M)] = C ? r[g + k * G].y : r[g + k * G].x;
+   }
+}
+
+template<class PL, int P, int C>
+__device__ __forceinline__ void gather_part(float2 (&r)[PL::V], const float* A, int L)
+{
+   constexpr int R = PL::radix(P), G = PL::V / R, M = PL::stride(P);
+#pragma unroll
+   for(int g = 0; g < G; g++) {
+      const int bp = FloatPad::phys(tap_pos<PL, P>(L, g, 0));
+#pragma unroll
+      for(int k = 0; k < R; k++) {
+         if constexpr(C) r[g + k * G].y = A[bp + FloatPad::cphys(k * M)];
+         else            r[g + k * G].x = A[bp + FloatPad::cphys(k * M)];
+      }
+   }
+}
+
+// pass PS's values out, pass PG's values in: real round, then imaginary round
+template<class PL, int PS, int PG>
+__device__ __forceinline__ void split_exchange(float2 (&r)[PL::V], float* A, int L)
+{
+   scatter_part<PL, PS, 0>(r, A, L);
+   __syncthreads();
+   gather_part<PL, PG, 0>(r, A, L);
+   __syncthreads();
+   scatter_part<PL, PS, 1>(r, A, L);
+   __syncthreads();
+   gather_part<PL, PG, 1>(r, A, L);
+}
+
+// The mid operation.  After the forward DIF register g + 2k of lane L holds
+// digit-order slot (L + g*T)*16 + k, i.e. slot 16*L' + k of radix-16 lane
+// L' = L + g*T (of T16 = N/16), so the filter is read where the radix-16
+// plan's lane L' reads it: 16 contiguous slots in digit order, pairs at
+// 2(L' + m*T16) lane-major, slot 16L' + k at L' + k*T16 in bperm.  The layout
+// is a template parameter: a run-time branch kept both sides' registers live
+// and spilled.
+template<class PL, int MID, int FLT>
+__device__ __forceinline__ void wide_mid(float2 (&r)[PL::V], const Buf& fb, uint32_t fb0, int L)
+{
+   using Op = MidOf<MID>;
+   constexpr int T = PL::T, G = 2, T16 = PL::N / 16;
+#pragma unroll
+   for(int g = 0; g < G; g++) {
+      const uint32_t l16 = (uint32_t)(L + g * T);
+      // at most 4 slots' loads in flight (the empty asm orders each step after
+      // the last): all 16 at once pushed the kernel past 128 VGPRs into scratch
+      if constexpr(FLT == FLT_BPERM) {
+#pragma unroll
+         for(int h = 0; h < 16; h += 4) {
+            float2 f[4];
+#pragma unroll
+            for(int k = 0; k < 4; k++) f[k] = fb.ld2((fb0 + l16) * 8u, (h + k) * T16 * 8);
+#pragma unroll
+            for(int k = 0; k < 4; k++) {
+               r[g + G * (h + k)] = Op::apply(r[g + G * (h + k)], f[k]);
+               asm volatile("" :: "v"(r[g + G * (h + k)].x));
+            }
+         }
+      } else {
+         constexpr bool lane = FLT == FLT_LANE;
+         const uint32_t so = lane ? fb0 * 8u + l16 * 16u : (fb0 + l16 * 16u) * 8u;
+         constexpr uint32_t ms = lane ? (uint32_t)T16 * 16u : 16u;
+#pragma unroll
+         for(int h = 0; h < 8; h += 2) {
+            float4 q[2];
+#pragma unroll
+            for(int m = 0; m < 2; m++) q[m] = fb.ld4(so, (h + m) * ms);
+#pragma unroll
+            for(int m = 0; m < 2; m++) {
+               const int a = g + G * (2 * (h + m)), b = g + G * (2 * (h + m) + 1);
+               r[a] = Op::apply(r[a], make_float2(q[m].x, q[m].y));
+               r[b] = Op::apply(r[b], make_float2(q[m].z, q[m].w));
+               asm volatile("" :: "v"(r[a].x), "v"(r[b].x));
+            }
+         }
+      }
+   }
+}
+
+template<int MID, int FLT>
+__global__ void __launch_bounds__(WPlan::T)
+conv_wide_kernel(const Conv1dParams p)
+{
+   using PL = WPlan;
+   constexpr int N = PL::N, T = PL::T, V = PL::V;
+   extern __shared__ float ldsf[];
+   const int L = threadIdx.x;
+   const uint32_t t = blockIdx.x;            // one transform per workgroup
+   Twiddles<PL> tw;
+   tw.load(p.tw, L);
+   // the base twiddles held from here (an empty asm that may change them):
+   // left free, the scheduler's placement of their loads and uses cost 28-72
+   // bytes of scratch per lane; held, the kernel fits 128 VGPRs with none
+#pragma unroll
+   for(int i = 0; i < Twiddles<PL>::COUNT; i++) asm volatile("" : "+v"(tw.w[i].x), "+v"(tw.w[i].y));
+   KeptChain<PL> kc;                         // not kept: two groups per lane
+   float2 r[V];
+   // the signal read and the result written once: streamed past the caches
+   const Buf xb(static_cast<const char*>(p.in0) + (size_t)t * N * 8, N * 8);
+#pragma unroll
+   for(int q = 0; q < V; q++) r[q] = xb.ld2<POL_NT>((uint32_t)L * 8u, q * T * 8);
+   static_for<PL::NP>([&](auto pi) {
+      constexpr int P = decltype(pi)::value;
+      if constexpr(P > 0) split_exchange<PL, P - 1, P>(r, ldsf, L);
+      compute_pass<PL, P, -1, false, KEEP_NONE>(r, tw, kc);
+   });
+   if constexpr(mid_reads_filter<MID>) {
+      const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
+      wide_mid<PL, MID, FLT>(r, fb, modulo_count(t, p.fcount) * N, L);
+   }
+   static_for<PL::NP>([&](auto qi) {
+      constexpr int P = PL::NP - 1 - decltype(qi)::value;
+      compute_pass<PL, P, +1, true, KEEP_NONE>(r, tw, kc);
+      if constexpr(P > 0) split_exchange<PL, P, P - 1>(r, ldsf, L);
+   });
+   const Buf ob(static_cast<char*>(p.out0) + (size_t)t * N * 8, N * 8);
+#pragma unroll
+   for(int q = 0; q < V; q++) ob.st2<POL_NT>(r[q], (uint32_t)L * 8u, q * T * 8);
+}
+
+template<int MID, int FLT>
+hipError_t launch_wide_mid(const Conv1dParams& p, hipStream_t s)
+{
+   const void* k = reinterpret_cast<const void*>(&conv_wide_kernel<MID, FLT>);
+   constexpr size_t shm = (size_t)FloatPad::size(CONV_WIDE_N) * sizeof(float);
+   static std::atomic<uint64_t> lds_ok{};
+   if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
+   Conv1dParams arg = p;
+   void* argv[] = { &arg };
+   return hipLaunchKernel(k, dim3(p.ntrans), dim3(WPlan::T), argv, shm, s);
+}
+
+}  // namespace
+
+// Per-signal filters address with 32-bit byte offsets: beyond 4 GiB of them
+// the launch is split into chunks of transforms (signal, result and filter
+// advance together).
+hipError_t launch_conv_wide(const Conv1dParams& p, hipStream_t s)
+{
+   if(p.ntrans == 0) return hipSuccess;
+   if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
+   if(p.fl != FLT_DR && p.fl != FLT_LANE && p.fl != FLT_BPERM) return hipErrorInvalidValue;
+   auto one = [&](const Conv1dParams& q) {
+      return with_mid(q.mid, [&](auto m) {
+         constexpr int MID = decltype(m)::value;
+         if constexpr(!mid_reads_filter<MID>) return launch_wide_mid<MID, FLT_DR>(q, s);
+         else return q.fl == FLT_LANE ? launch_wide_mid<MID, FLT_LANE>(q, s)
+                   : q.fl == FLT_BPERM ? launch_wide_mid<MID, FLT_BPERM>(q, s) : launch_wide_mid<MID, FLT_DR>(q, s);
+      });
+   };
+   constexpr uint64_t bytes = (uint64_t)CONV_WIDE_N * 8;
+   if((uint64_t)p.fcount * bytes <= 0xffffffffull) return one(p);
+   if(p.fcount != p.ntrans) return hipErrorInvalidValue;
+   const uint32_t step = (uint32_t)(0xffffffffull / bytes) & ~255u;
+   for(uint32_t t0 = 0; t0 < p.ntrans; t0 += step) {
+      Conv1dParams q = p;
+      q.ntrans = p.ntrans - t0 < step ? p.ntrans - t0 : step;
+      q.fcount = q.ntrans;
+      q.in0  = static_cast<const char*>(p.in0) + (size_t)t0 * bytes;
+      q.out0 = static_cast<char*>(p.out0) + (size_t)t0 * bytes;
+      q.filt = static_cast<const char*>(p.filt) + (size_t)t0 * bytes;
+      if(const hipError_t e = one(q); e != hipSuccess) return e;
+   }
+   return hipSuccess;
+}
+
+}  // namespace fufft

@@ -25,8 +25,9 @@
  *     (one filter shared by the batch) or n (one filter per signal).
  *
  * Supported sizes (fufft_supported): single-launch N = 2^k with
- * 256 <= N <= 16384 for FUFFT_V16 and 512 <= N <= 8192 for FUFFT_R8; the
- * four-step path takes N = 16^L * MID up to 2^20.
+ * 256 <= N <= 16384 for FUFFT_V16 and 512 <= N <= 8192 for FUFFT_R8, and the
+ * fused conv (fufft_conv_f32) also at N = 32768 for FUFFT_V16; the four-step
+ * path takes N = 16^L * MID up to 2^20.
  */
 #ifndef FUFFT_FUFFT_H
 #define FUFFT_FUFFT_H
@@ -106,13 +107,15 @@ int fufft_abi_version(void);
 /* Upload the twiddle table to `device` (idempotent, thread-safe). */
 int fufft_init(int device);
 const char* fufft_status_string(int status);
-/* 1 if a single-launch kernel exists for (n, variant), else 0 */
+/* 1 if a single-launch kernel exists for (n, variant), else 0.  At
+ * n = 32768 (FUFFT_V16) that is the fused conv, fufft_conv_f32, alone; the
+ * other 1D calls return FUFFT_ERR_UNSUPPORTED there. */
 int fufft_supported(int64_t n, int variant);
 /* The faster variant (FUFFT_R8 or FUFFT_V16) for an n-point conv whose filter
  * is in `layout`, as measured on MI355X for the fp32 and the BFP conv alike;
  * FUFFT_AUTO is this for FUFFT_LAYOUT_DR.  With FUFFT_LAYOUT_LANE it is
  * FUFFT_R8 at n = 512 and FUFFT_V16 at every other n, the fastest plan of
- * this library at n = 1024 .. 16384.  Plan the filter and launch with the
+ * this library at n = 1024 .. 32768.  Plan the filter and launch with the
  * variant it returns.  No reference counterpart (the reference's caller
  * picks the kernel template). */
 int fufft_fastest_variant(int64_t n, int layout);
@@ -174,7 +177,12 @@ int fufft_twiddle_table_host_source(int log_max, int source, float* out);
 
 /* ---- fp32 fused convolution ------------------------------------------------
  * out = IDFT(DFT(in) mid filt) for batch signals of n points, one launch,
- * three HBM passes.  in == out is allowed.
+ * three HBM passes.  in == out is allowed.  At n = 32768 (FUFFT_V16 or
+ * FUFFT_AUTO) one workgroup holds a transform, 32 values per lane, with the
+ * radix-16 plan's arithmetic and filter: the filter is the one
+ * fufft_plan_filter_f32 writes for (32768, FUFFT_V16) in any of the three
+ * layouts, and the result equals that plan bit for bit.  (The four-step call,
+ * fufft_conv_large_f32, is the reference's run_large chain at that size.)
  * Replaces fufft_pipeline_v16<N,LEAD,NRV,CPB> (fufft.cuh:1518-1534),
  * fufft_pipeline_v16f (fufft.cuh:1499-1516) and
  * fufft_pipeline_ip<N,LEAD,NR8,CPB,Mid> (fufft.cuh:1757-1772), launched by

@@ -131,7 +131,7 @@ def test_gpu_equals_reference_on_golden_fixture(ref_tw, name):
         raise AssertionError(kind)
 
 
-SIZES = [("v16", n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384)] + \
+SIZES = [("v16", n) for n in (256, 512, 1024, 2048, 4096, 8192, 16384, 32768)] + \
         [("r8", n) for n in (512, 1024, 2048, 4096, 8192)]
 V = {"v16": 16, "r8": 8}
 

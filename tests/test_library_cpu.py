@@ -63,9 +63,32 @@ def test_auto_variant_rule():
         # with the lane-major filter radix 16 wins from n = 1024 on
         assert ff.fastest_variant(n, "lane") == ("r8" if n == 512 else "v16")
         assert ff.supported(n, ff.fastest_variant(n, "lane"))
-    for bad in (100, 128, 32768):
+    # N = 32768: the fused conv alone, radix 16 (wide.hip)
+    assert ff.fastest_variant(32768, "lane") == ff.fastest_variant(32768, "dr") == "v16"
+    assert ff.resolve_variant(32768, "auto") == "v16"
+    assert ff.supported(32768, "v16") and ff.supported(32768, "auto") and not ff.supported(32768, "r8")
+    for bad in (100, 128, 65536):
         with pytest.raises(ff.FufftError):
             ff.fastest_variant(bad, "lane")
+
+
+def test_n32768_is_the_fused_conv_only():
+    """At N = 32768 every 1D call but the fused conv refuses the size before
+    touching a device (fake addresses, never used)."""
+    import fufft_amd as ff
+    L, A, n = ff.lib, 1 << 32, 32768
+    B = A + (1 << 24)
+    assert L.fufft_fwd_f32(A, B, n, 1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_apply_f32(A, n, B, 0, B + (1 << 22), n, 1, 0, 0, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_c2c_f32(A, B, n, 1, -1, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_r2_f32(A, A + (1 << 20), B, 0, B + (1 << 20), B + (1 << 21), n, 1, 0, 0, None) \
+        == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_bfp16(A, A + (1 << 20), B, 0, B + (1 << 20), B + (1 << 21), n, 1, 64, 0, 0, 0, None) \
+        == ff.ERR_UNSUPPORTED
+    assert L.fufft_conv_timed_f32(A, B, 0, B + (1 << 20), n, 1, 0, 0, 0, None, 0, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter_device_f32(A, B, n, 1, 0, 0, 1, 1, None) == ff.ERR_UNSUPPORTED
+    # the radix-8 plan has no N = 32768 kernel, the fused conv included
+    assert L.fufft_conv_f32(A, B, 0, B + (1 << 20), n, 1, 0, 1, 0, None) == ff.ERR_UNSUPPORTED
 
 
 def run_large_chain_order(n, lout, mid):
