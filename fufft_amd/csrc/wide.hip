@@ -78,16 +78,37 @@ __device__ __forceinline__ void gather_part(float2 (&r)[PL::V], const float* A, 
    }
 }
 
+// An exchange between passes P and P + 1 stays inside each wavefront when
+// both run at M <= 64 with the same radix R: for every group g, wavefront w's
+// 64 lanes then own positions [(64w + g*T)*R, (64w + g*T + 64)*R) on both
+// sides, and the float slots of those positions (a monotonic map) no other
+// wavefront's.  Here: the exchange between the last two radix-16 passes (M =
+// 16 and 1).  It takes wavefront fences instead of workgroup barriers, 6 of
+// the 18 barriers of a transform.
+template<class PL, int P>
+constexpr bool exchange_private()
+{
+   return PL::stride(P) <= 64 && PL::stride(P + 1) <= 64 && PL::radix(P) == PL::radix(P + 1);
+}
+
+template<bool PRIVATE>
+__device__ __forceinline__ void exchange_fence()
+{
+   if constexpr(PRIVATE) pass_barrier<64>();
+   else                  __syncthreads();
+}
+
 // pass PS's values out, pass PG's values in: real round, then imaginary round
 template<class PL, int PS, int PG>
 __device__ __forceinline__ void split_exchange(float2 (&r)[PL::V], float* A, int L)
 {
+   constexpr bool PRIVATE = exchange_private<PL, (PS < PG ? PS : PG)>();
    scatter_part<PL, PS, 0>(r, A, L);
-   __syncthreads();
+   exchange_fence<PRIVATE>();
    gather_part<PL, PG, 0>(r, A, L);
-   __syncthreads();
+   exchange_fence<PRIVATE>();
    scatter_part<PL, PS, 1>(r, A, L);
-   __syncthreads();
+   exchange_fence<PRIVATE>();
    gather_part<PL, PG, 1>(r, A, L);
 }
 
