@@ -17,14 +17,12 @@
 //
 // The exchanges.  A complex exchange of 32768 points needs 256 KiB, beyond
 // the CU's 160 KiB of LDS.  Each exchange therefore runs in two rounds through
-// one float buffer of N + N/16 slots (136 KiB, one spare slot after every 16):
-// every lane writes the real parts of its outgoing values, barrier, reads the
-// real parts of its incoming ones, barrier, the same for the imaginary parts.
-// A lane's register keeps the component it has not yet exchanged, so no
-// register is spent on staging.  Slot of position i: i + i/16.  Every pass's
-// accesses are conflict free under gfx950's 4-byte bank rule: consecutive
-// positions for the M >= 64 passes, 272 / 17 float slots per 16 / 1 lane steps
-// at M = 16 / 1, all distinct modulo 64 within a wavefront.
+// one float buffer of N + N/16 slots (136 KiB): every lane writes the real
+// parts of its outgoing values, barrier, reads the real parts of its incoming
+// ones, barrier, the same for the imaginary parts.  A lane's register keeps
+// the component it has not yet exchanged, so no register is spent on staging.
+// The slot layouts (Pad16, Pad256 below) keep every access free of bank
+// conflicts.
 //
 // Races.  Within a pass a lane writes the positions it read (same layout on
 // both sides), so the next exchange's first write needs no barrier after the
@@ -47,33 +45,63 @@ namespace fufft {
 namespace {
 
 using WPlan = Plan<CONV_WIDE_N, 32, 16>;
-using FloatPad = Lds<16, LAYOUT_PAD>;        // float slot of position i: i + i/16
+
+// Float slot layouts.  gfx950 serves the 4-byte LDS forms 32 lanes at a time
+// over 32 banks (bank = slot mod 32), each access of a paired form
+// (ds_read2_b32, ds_write2st64_b32) like a single one; a group costs the
+// largest number of distinct slots sharing a bank, minus one, in cycles
+// (measured with a probe: stride 2 / 4 / 16 cost 2 / 6 / 30 cycles per
+// wavefront instruction, strides 17 and 33 nothing).
+//  - Pad16, i + i/16: 17 slots per lane at M = 1 and 272 per 16 lanes at
+//    M = 16, both conflict free; a run of 32 consecutive positions (the
+//    M >= 64 passes) spans 34 slots and costs 2 cycles per access, 768 per
+//    wavefront over a transform (the counter's reading).
+//  - Pad256, i + 16*(i/256): 32-runs stay contiguous, and the M = 16 pass's
+//    two 16-runs per half-wavefront land 16 banks apart: conflict free for
+//    the passes at M >= 16, not at M = 1.
+// Each exchange takes the layout its two passes need (Pad256 for the ones
+// between the M >= 16 passes, Pad16 for the private one into M = 1).  Both put
+// the 1024-aligned block c of positions inside slots [1088c, 1088c + 1088),
+// so a private pass that reads one layout and writes the other stays inside
+// its wavefront's own slot range; both are additive over every pass's taps
+// (base + k*M).
+struct Pad16 {
+   __device__ __forceinline__ static int phys(int i) { return i + (i >> 4); }
+   static constexpr int cphys(int i) { return i + (i >> 4); }
+   static constexpr int size(int n) { return n + n / 16; }
+};
+struct Pad256 {
+   __device__ __forceinline__ static int phys(int i) { return i + ((i >> 8) << 4); }
+   static constexpr int cphys(int i) { return i + ((i >> 8) << 4); }
+   static constexpr int size(int n) { return n + n / 16; }
+};
+static_assert(Pad16::size(CONV_WIDE_N) == Pad256::size(CONV_WIDE_N), "one buffer for both layouts");
 
 // one component (C = 0 real, 1 imaginary) of the lane's values out to pass P's
 // positions, or in from them
-template<class PL, int P, int C>
+template<class PL, int P, int C, class FL>
 __device__ __forceinline__ void scatter_part(const float2 (&r)[PL::V], float* A, int L)
 {
    constexpr int R = PL::radix(P), G = PL::V / R, M = PL::stride(P);
 #pragma unroll
    for(int g = 0; g < G; g++) {
-      const int bp = FloatPad::phys(tap_pos<PL, P>(L, g, 0));
+      const int bp = FL::phys(tap_pos<PL, P>(L, g, 0));
 #pragma unroll
-      for(int k = 0; k < R; k++) A[bp + FloatPad::cphys(k * M)] = C ? r[g + k * G].y : r[g + k * G].x;
+      for(int k = 0; k < R; k++) A[bp + FL::cphys(k * M)] = C ? r[g + k * G].y : r[g + k * G].x;
    }
 }
 
-template<class PL, int P, int C>
+template<class PL, int P, int C, class FL>
 __device__ __forceinline__ void gather_part(float2 (&r)[PL::V], const float* A, int L)
 {
    constexpr int R = PL::radix(P), G = PL::V / R, M = PL::stride(P);
 #pragma unroll
    for(int g = 0; g < G; g++) {
-      const int bp = FloatPad::phys(tap_pos<PL, P>(L, g, 0));
+      const int bp = FL::phys(tap_pos<PL, P>(L, g, 0));
 #pragma unroll
       for(int k = 0; k < R; k++) {
-         if constexpr(C) r[g + k * G].y = A[bp + FloatPad::cphys(k * M)];
-         else            r[g + k * G].x = A[bp + FloatPad::cphys(k * M)];
+         if constexpr(C) r[g + k * G].y = A[bp + FL::cphys(k * M)];
+         else            r[g + k * G].x = A[bp + FL::cphys(k * M)];
       }
    }
 }
@@ -103,13 +131,14 @@ template<class PL, int PS, int PG>
 __device__ __forceinline__ void split_exchange(float2 (&r)[PL::V], float* A, int L)
 {
    constexpr bool PRIVATE = exchange_private<PL, (PS < PG ? PS : PG)>();
-   scatter_part<PL, PS, 0>(r, A, L);
+   using FL = typename std::conditional<PRIVATE, Pad16, Pad256>::type;
+   scatter_part<PL, PS, 0, FL>(r, A, L);
    exchange_fence<PRIVATE>();
-   gather_part<PL, PG, 0>(r, A, L);
+   gather_part<PL, PG, 0, FL>(r, A, L);
    exchange_fence<PRIVATE>();
-   scatter_part<PL, PS, 1>(r, A, L);
+   scatter_part<PL, PS, 1, FL>(r, A, L);
    exchange_fence<PRIVATE>();
-   gather_part<PL, PG, 1>(r, A, L);
+   gather_part<PL, PG, 1, FL>(r, A, L);
 }
 
 // The mid operation.  After the forward DIF register g + 2k of lane L holds
@@ -207,7 +236,7 @@ template<int MID, int FLT>
 hipError_t launch_wide_mid(const Conv1dParams& p, hipStream_t s)
 {
    const void* k = reinterpret_cast<const void*>(&conv_wide_kernel<MID, FLT>);
-   constexpr size_t shm = (size_t)FloatPad::size(CONV_WIDE_N) * sizeof(float);
+   constexpr size_t shm = (size_t)Pad16::size(CONV_WIDE_N) * sizeof(float);
    static std::atomic<uint64_t> lds_ok{};
    if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    Conv1dParams arg = p;
