@@ -66,7 +66,8 @@ __device__ __forceinline__ void static_for(F&& f)
 
 // ---- LDS layouts ------------------------------------------------------------------
 // phys(i) maps logical position i of a transform to its float2 slot.  gfx950
-// LDS bank model, measured with SQ_LDS_BANK_CONFLICT (fufft_amd/lds_probe.py):
+// LDS bank model, measured with SQ_LDS_BANK_CONFLICT on a one-off probe kernel
+// (restated with the measurements in tests/lds_bank_model.py):
 // ds_read_b64 is serviced 32 lanes at a time, so lanes of an aligned
 // half-wavefront conflict when their slots agree modulo 32; ds_write_b64 and
 // each 8-byte access of the paired forms the exchanges compile to

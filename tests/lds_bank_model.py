@@ -64,3 +64,60 @@ def conflict_cycles(slots, form: str) -> int:
                 banks.setdefault(s % mod, set()).add(s)
             total += max(len(x) for x in banks.values()) - 1
     return total
+
+
+# ---- 4-byte forms ----------------------------------------------------------------
+# The N = 32768 conv (wide.hip) exchanges one float component at a time
+# (ds_read_b32 / ds_write_b32 and their paired and st64 forms).  Slots here
+# are float indices (byte address / 4).  Measured the same way as the 8-byte
+# forms (a one-off probe: one 64-lane workgroup per pattern and form, 256
+# repetitions, rocprofv3 --pmc SQ_LDS_BANK_CONFLICT SQ_INSTS_LDS SQ_WAVES):
+#
+# - every 4-byte form is serviced 32 lanes at a time over 32 banks; two lanes
+#   of a half-wavefront conflict when their slots differ but agree modulo 32;
+# - a paired form (ds_read2_b32, ds_write2_b32, ds_read2st64_b32,
+#   ds_write2st64_b32) costs its two accesses separately.
+
+FORMS32 = ("read_b32", "write_b32", "read2_b32", "write2_b32", "read2st64_b32", "write2st64_b32")
+# second access of the paired forms as the probe issued them, in float slots
+SECOND32 = {"read2_b32": 1, "write2_b32": 1, "read2st64_b32": 64, "write2st64_b32": 64}
+
+
+def _patterns32() -> dict:
+    lane = range(64)
+    p = {"contiguous": [l for l in lane]}
+    for s in (2, 4, 8, 16, 32, 64, 17, 33):
+        p[f"stride {s}"] = [s * l for l in lane]
+    p["padded by 16 (i + i/16)"] = [l + l // 16 for l in lane]
+    p["272 (l/16) + l%16"] = [272 * (l // 16) + l % 16 for l in lane]
+    p["16 l + 16 (l/16)"] = [16 * l + 16 * (l // 16) for l in lane]
+    p["16 l + l%16 + 16 (l/16)"] = [16 * l + l % 16 + 16 * (l // 16) for l in lane]
+    p["two runs of 32, 64 apart"] = [l + 64 * (l // 32) for l in lane]
+    return p
+
+
+PATTERNS32 = _patterns32()
+
+# SQ_LDS_BANK_CONFLICT per instruction of the single forms (read_b32 and
+# write_b32 measured alike); the paired forms measured exactly twice these,
+# with a second access 1 or 17 floats away, or 64 (st64)
+MEASURED32 = {
+    "contiguous": 0, "stride 2": 2, "stride 4": 6, "stride 8": 14, "stride 16": 30, "stride 32": 62,
+    "stride 64": 62, "stride 17": 0, "stride 33": 0, "padded by 16 (i + i/16)": 2, "272 (l/16) + l%16": 0,
+    "16 l + 16 (l/16)": 30, "16 l + l%16 + 16 (l/16)": 0, "two runs of 32, 64 apart": 0,
+}
+
+
+def conflict_cycles32(slots, form: str) -> int:
+    """Extra cycles of one 4-byte instruction of `form` whose lanes access `slots`."""
+    accesses = [list(slots)]
+    if form in SECOND32:
+        accesses.append([s + SECOND32[form] for s in slots])
+    total = 0
+    for acc in accesses:
+        for h in range(0, len(acc), 32):
+            banks: dict = {}
+            for s in acc[h:h + 32]:
+                banks.setdefault(s % 32, set()).add(s)
+            total += max(len(x) for x in banks.values()) - 1
+    return total

@@ -29,6 +29,7 @@ from pathlib import Path
 
 import pytest
 
+from tests import lds_bank_model as M
 from tests.lds_bank_model import PATTERNS, FORMS, conflict_cycles
 
 ROOT = Path(__file__).resolve().parent.parent
@@ -453,3 +454,113 @@ def test_outer2_exchange_conflict_free():
     # without the 16-slot skew per k1 block the half-wavefront rule fails
     flat = [(tid >> 4) * 256 + q * 16 + (tid & 15) for q in (0,) for tid in range(64)]
     assert conflict_cycles(flat, "read_b64") > 0
+
+
+# ---- the N = 32768 conv's float exchanges (wide.hip) ---------------------------------
+
+def test_b32_model_reproduces_the_probe():
+    """The 4-byte rule (32 lanes, 32 banks, paired forms per access) gives
+    every measured count of the probe."""
+    for name, slots in M.PATTERNS32.items():
+        for form in M.FORMS32:
+            want = M.MEASURED32[name] * (2 if form in M.SECOND32 else 1)
+            assert M.conflict_cycles32(slots, form) == want, (name, form)
+
+
+WIDE_N, WIDE_V = 32768, 32
+WIDE_T = WIDE_N // WIDE_V
+WIDE_RADICES = [8, 16, 16, 16]          # LEAD 8, then radix 16 at two groups per lane
+
+
+def _wide_stride(p):
+    m = WIDE_N
+    for r in WIDE_RADICES[:p + 1]:
+        m //= r
+    return m
+
+
+def _wide_taps(p, lane, g):
+    """positions of group g of pass p for `lane` (gidx = L + g T, taps b R M + j + k M)"""
+    r, m = WIDE_RADICES[p], _wide_stride(p)
+    gidx = lane + g * WIDE_T
+    return [(gidx // m) * r * m + gidx % m + k * m for k in range(r)]
+
+
+def _pad16(i):
+    return i + (i >> 4)
+
+
+def _pad256(i):
+    return i + ((i >> 8) << 4)
+
+
+def _wide_private(p):
+    """the kernel's rule: both passes at M <= 64 with the same radix"""
+    return _wide_stride(p) <= 64 and _wide_stride(p + 1) <= 64 and WIDE_RADICES[p] == WIDE_RADICES[p + 1]
+
+
+def test_wide_private_exchange_rule_matches_brute_force():
+    for p in range(len(WIDE_RADICES) - 1):
+        private = True
+        for w in range(WIDE_T // 64):
+            a = {x for lane in range(64 * w, 64 * w + 64) for g in range(WIDE_V // WIDE_RADICES[p])
+                 for x in _wide_taps(p, lane, g)}
+            b = {x for lane in range(64 * w, 64 * w + 64) for g in range(WIDE_V // WIDE_RADICES[p + 1])
+                 for x in _wide_taps(p + 1, lane, g)}
+            private &= a == b
+        assert private == _wide_private(p), p
+
+
+def _wide_conflicts(layout_of):
+    """conflict cycles per wavefront over a transform: every exchange, both
+    sides, both components, forward and inverse (single 4-byte accesses)"""
+    total = 0
+    for p in range(len(WIDE_RADICES) - 1):
+        lay = layout_of(p)
+        for side in (p, p + 1):
+            for g in range(WIDE_V // WIDE_RADICES[side]):
+                for k in range(WIDE_RADICES[side]):
+                    for w in (0, 5, WIDE_T // 64 - 1):          # every wavefront has the same pattern
+                        slots = [lay(_wide_taps(side, lane, g)[k]) for lane in range(64 * w, 64 * w + 64)]
+                        c = M.conflict_cycles32(slots, "read_b32")
+                        if w == 0:
+                            first = c
+                        assert c == first
+                    total += first * 2 * 2
+    return total
+
+
+def test_wide_layouts_conflict_free_and_old_layout_matches_counter():
+    """Pad256 on the cross-wavefront exchanges, Pad16 on the private one: no
+    conflict cycle.  Pad16 everywhere (the first build) gives the 768 cycles
+    per wavefront that rocprofv3 counted on it."""
+    assert _wide_conflicts(lambda p: _pad16 if _wide_private(p) else _pad256) == 0
+    assert _wide_conflicts(lambda p: _pad16) == 768
+
+
+def test_wide_layouts_keep_wavefront_ranges():
+    """Both layouts put the 1024-aligned block c of positions inside slots
+    [1088c, 1088c + 1088): a private pass that reads one layout and writes the
+    other never reaches another wavefront's slots; and both fit the buffer."""
+    size = WIDE_N + WIDE_N // 16
+    for c in range(WIDE_N // 1024):
+        for lay in (_pad16, _pad256):
+            s = [lay(i) for i in range(1024 * c, 1024 * c + 1024)]
+            assert len(set(s)) == 1024 and min(s) >= 1088 * c and max(s) < 1088 * (c + 1) <= size
+    # every wavefront's positions of the private passes form whole 1024-blocks
+    for w in range(WIDE_T // 64):
+        pos = {x for lane in range(64 * w, 64 * w + 64) for g in range(2) for x in _wide_taps(3, lane, g)}
+        blocks = {x // 1024 for x in pos}
+        assert len(pos) == 1024 * len(blocks)
+
+
+def test_wide_layouts_additive():
+    """the kernel addresses a tap as layout(base) + layout(k M)"""
+    for p in range(len(WIDE_RADICES) - 1):
+        lay = _pad16 if _wide_private(p) else _pad256
+        for side in (p, p + 1):
+            m = _wide_stride(side)
+            for lane in (0, 1, 17, 63, 64, 515, WIDE_T - 1):
+                for g in range(WIDE_V // WIDE_RADICES[side]):
+                    taps = _wide_taps(side, lane, g)
+                    assert all(lay(t) == lay(taps[0]) + lay(k * m) for k, t in enumerate(taps))
