@@ -45,6 +45,7 @@ KINDS = {0: "conv", 1: "conv_r2", 2: "fwd", 3: "apply", 4: "fwd_r2", 5: "apply_r
          11: "conv_psf"}
 MIDS = {0: "mul", 1: "conj", 2: "none"}
 LAYOUTS = {0: "xor", 1: "pad", 2: "xchg"}
+FILTERS = {0: "dr", 1: "lane", 2: "bperm"}
 
 FP32_ARITH = re.compile(r"^v_(add|sub|subrev|mul|fma|fmac|fmaak|fmamk)_f32")
 # bytes moved per lane by each LDS data instruction
@@ -148,6 +149,12 @@ def decode_name(name: str) -> dict | None:
         # big: blocks of more than 64 points (LDS rendezvous of the block maxima)
         return {"family": "bfp", "n": n, "v": v, "layout": LAYOUTS[lay],
                 "kind": "conv_blocks" if big else "conv", "mid": MIDS[mid]}
+    # the N = 32768 conv (wide.hip): 32 values per lane, float exchanges
+    m = re.search(r"conv_wide_kernelILi(\d+)ELi(\d+)E", name)
+    if m:
+        mid, flt = map(int, m.groups())
+        return {"family": "wide", "n": 32768, "v": 32, "layout": "split", "kind": "conv", "mid": MIDS[mid],
+                "filter": FILTERS[flt]}
     return None
 
 
@@ -232,6 +239,26 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
             "vmem_stores_per_wave": stores, "untaken_branch": untaken, "passes": ps}
 
 
+def model_wide(mid: str = "mul", filt: str = "lane", n: int = 32768, v: int = 32) -> dict:
+    """The N = 32768 conv (wide.hip): the radix-16 plan with V/R groups per lane
+    in every pass (4 in the radix-8 lead, 2 in the radix-16 passes), no kept
+    chain; each exchange writes and reads both float components of the lane's
+    V values (V 8-byte equivalents each way); the filter as V/2 16-byte loads
+    (V 8-byte ones in bperm)."""
+    ps = plan(n, 16)
+    one_dir = sum((v // r) * (DFT_OPS[r] + (4 * (2 * r - 3) if M > 1 else 0)) for r, M in ps)
+    arith = 2 * one_dir + (4 * v if mid != "none" else 0)
+    lds = 2 * v * (len(ps) - 1) * 2
+    # a pass with M <= T gives both of a lane's groups the same base twiddle
+    # index ((L + g T) mod M = L mod M), and the compiler merges those loads
+    t = n // v
+    loads = v + sum((v // r) if M > t else 1 for r, M in ps if M > 1)
+    if mid != "none":
+        loads += v if filt == "bperm" else v // 2
+    return {"fp32_arith_per_lane": arith, "lds_access_8B_per_lane": lds, "vmem_loads_per_wave": loads,
+            "vmem_stores_per_wave": v, "untaken_branch": {"loads": 0, "stores": 0}, "passes": ps}
+
+
 # ---- occupancy ---------------------------------------------------------------------------
 
 def occupancy(vgpr: int, agpr: int, lds_bytes: int, waves_per_wg: int) -> dict:
@@ -250,6 +277,8 @@ def default_layout(n: int, v: int, family: str = "conv1d") -> str:
     plan (bfp_lds_layout in bfp.hip)."""
     if family == "bfp":
         return "xchg"
+    if family == "wide":
+        return "split"
     return "pad" if (v == 8 and n > 4096) else "xchg"
 
 
@@ -269,9 +298,11 @@ def conv_rows(rows=None) -> list:
         n, v = d["n"], d["v"]
         t = n // v
         threads = t if t >= 128 else 256
-        lds = lds_bytes_conv(n, v, d["layout"])
+        # the wide kernel's float buffer: N + N/16 slots of 4 bytes
+        lds = (n + n // 16) * 4 if d["family"] == "wide" else lds_bytes_conv(n, v, d["layout"])
         occ = occupancy(r["meta"]["vgpr_count"], r["meta"].get("agpr_count", 0), lds, threads // 64)
-        mod = model_conv(n, v, d["kind"], d["mid"]) if d["family"] == "conv1d" else None
+        mod = model_conv(n, v, d["kind"], d["mid"]) if d["family"] == "conv1d" else \
+            model_wide(d["mid"], d["filter"]) if d["family"] == "wide" else None
         out.append({**d, "vgpr": r["meta"]["vgpr_count"], "sgpr": r["meta"]["sgpr_count"],
                     "scratch": r["meta"].get("private_segment_fixed_size", 0),
                     "spills": r["meta"].get("vgpr_spill_count", 0) + r["meta"].get("sgpr_spill_count", 0),
@@ -306,7 +337,8 @@ def main() -> None:
         vm = (f"{r['vmem_load']}+{r['vmem_store']} / {m['vmem_loads_per_wave'] + m['untaken_branch']['loads']}"
               f"+{m['vmem_stores_per_wave'] + m['untaken_branch']['stores']}") if m else \
             f"{r['vmem_load']}+{r['vmem_store']} / —"
-        print(f"| {r['family']} {r['kind']} | {r['n']} | {r['v']} | {r['vgpr']} | {r['scratch']} | "
+        label = f"{r['family']} {r['kind']}" + (f" ({r['filter']} filter)" if r["family"] == "wide" else "")
+        print(f"| {label} | {r['n']} | {r['v']} | {r['vgpr']} | {r['scratch']} | "
               f"{r['waves_per_simd']} ({r['limited_by']}) | {r['valu']} | {ar} | {ld} | {vm} |")
 
 
