@@ -24,18 +24,20 @@
 // The slot layouts (Pad16, Pad256 below) keep every access free of bank
 // conflicts.
 //
-// Races.  Within a pass a lane writes the positions it read (same layout on
-// both sides), so the next exchange's first write needs no barrier after the
-// last read; the three barriers separate write from read within a round and
-// the two rounds from each other.  Every wavefront of the workgroup reaches
-// every barrier (one transform per workgroup, the whole group leaves
-// together).
+// Races.  Within a pass a lane writes the positions it read, so the next
+// exchange's first write needs no barrier after the last read: a pass that
+// spans wavefronts reads and writes the same layout (the same slots), a pass
+// inside each wavefront may switch layouts but stays in its wavefront's own
+// slot range (the layouts below).  The three barriers of an exchange separate
+// write from read within a round and the two rounds from each other.  Every
+// wavefront of the workgroup reaches every barrier (one transform per
+// workgroup, the whole group leaves together).
 //
 // Resources: 128 VGPRs with no scratch (16 wavefronts of 1024 lanes, 4 per
-// SIMD), 136 KiB of LDS: one workgroup per CU.  Measured against the
-// four-step at 2^27 points on one MI355X: 137.7 Gpt/s four-step (48 bytes per
-// point over HBM and the Infinity Cache), 173 Gpt/s with the digit-order
-// filter, 190 with the lane-major filter.
+// SIMD), 136 KiB of LDS: one workgroup per CU.  Measured at 2^27 points on one
+// MI355X: 199-207 Gpt/s with the lane-major filter, 187-195 with the
+// digit-order one, against 135-138 for the four-step chain at the same N (48
+// bytes per point over HBM and the Infinity Cache).
 #include "fufft_device.hpp"
 #include "fufft_plan.hpp"
 #include "fufft_internal.hpp"
