@@ -330,6 +330,44 @@ def bench_c2c(torch, ff, dev, n, pts, steps, warmup, stream, seed):
             "speedup_vs_rocfft": round(t_vendor / t_ours, 3)}
 
 
+def bench_r2(torch, ff, dev, n, pts, steps, warmup, stream, seed):
+    """Real two-for-one 1D conv (fufft_conv_r2_f32): pts complex points are
+    2 pts real samples, x and y U[0,1) each convolved with one shared real
+    filter (taps U[0,1), planned as a spectrum) and written to u and v; 4 bytes
+    per real sample read and written, 16 per complex point."""
+    batch = pts // n
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    x = torch.rand(pts, device=dev, generator=gen)
+    y = torch.rand(pts, device=dev, generator=gen)
+    u, v = torch.empty_like(x), torch.empty_like(y)
+    rng = np.random.default_rng(seed)
+    taps = rng.uniform(0, 1, n).astype(np.complex64)
+    layout = "lane"
+    var = ff.fastest_variant(n, layout)
+    filt = torch.from_numpy(ff.plan_filter(taps, n, variant=var, layout=layout, kind=ff.FILTER_TAPS)).to(dev)
+
+    def step():
+        ff.conv_r2(x, y, filt, u, v, n=n, batch=batch, variant=var, layout=layout, stream=stream)
+
+    step()
+    torch.cuda.synchronize()
+    idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
+    spec = np.fft.fft(taps.real.astype(np.float64))
+    got, want = [], []
+    for a, b in ((x, u), (y, v)):
+        xs = a.view(batch, n)[idx].cpu().numpy().astype(np.float64)
+        want.append(np.fft.ifft(np.fft.fft(xs, axis=1) * spec[None, :], axis=1).real)
+        got.append(b.view(batch, n)[idx].cpu().numpy())
+    rel = rel_l2(np.stack(got), np.stack(want))
+    secs = time_launches(torch, step, steps, warmup, stream, SETTLE_S) / steps
+    del x, y, u, v, filt
+    return {"n": n, "batch": batch, "variant": var, "filter_layout": layout,
+            "gsamples_s": round(2 * pts / secs / 1e9, 3), "gpoints_s": round(pts / secs / 1e9, 3),
+            "ms": round(secs * 1e3, 5), "bytes_per_sample": 8, "frac": frac(16.0 * pts + 8.0 * n, secs),
+            "rel_l2": rel}
+
+
 def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="auto"):
     """Four-step conv: batch pts/n of U[-1,1) signals, one
     shared filter in the chain order of the middle `variant` ("auto" = "v16",
@@ -927,6 +965,12 @@ def main():
         line["large"] = large
 
     if not args.no_c2c:
+        # the real two-for-one 1D conv at the headline N (two real signals per complex transform)
+        r2 = bench_r2(torch, ff, dev, n, pts, args.sweep_steps, 3, stream, 23)
+        if not r2["rel_l2"] <= 2e-6:
+            print(json.dumps({"error": f"r2 accuracy check failed: rel L2 {r2['rel_l2']:.3e}"}))
+            sys.exit(1)
+        line["real_two_for_one"] = r2
         c2c = bench_c2c(torch, ff, dev, n, pts, args.sweep_steps, 3, stream, 21)
         if not c2c["rel_l2"] <= 2e-6:
             print(json.dumps({"error": f"C2C accuracy check failed: rel L2 {c2c['rel_l2']:.3e}"}))
