@@ -717,7 +717,9 @@ int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t c
                                  int layout, int filter_kind, int fold_inv_n, void* stream)
 {
    int v = 0;
-   int st = check_1d(n, count, variant, FUFFT_MID_NONE, layout, &v);
+   // a spectrum is only permuted, so the fused conv's N = 32768 plan takes it
+   // too; taps need the forward transform, which exists up to N = 16384
+   int st = check_1d(n, count, variant, FUFFT_MID_NONE, layout, &v, filter_kind == FUFFT_FILTER_SPECTRUM);
    if(st != FUFFT_OK) return st;
    if((st = check_plan_kind(filter_kind)) != FUFFT_OK) return st;
    if(!in || !out || (filter_kind == FUFFT_FILTER_SPECTRUM && in == out)) return FUFFT_ERR_INVALID;

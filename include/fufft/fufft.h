@@ -268,7 +268,9 @@ int fufft_c2c_f32(const void* in, void* out, int64_t n, int64_t batch,
  *   FUFFT_FILTER_TAPS: the conv kernels' own forward transform in fp32
  *     (times 1/n, exact since n is a power of two).  The host planner takes
  *     this DFT in fp64 instead, so the two agree to fp32 transform rounding
- *     (rel L2 ~3e-7), not bit for bit.  in == out is allowed. */
+ *     (rel L2 ~3e-7), not bit for bit.  in == out is allowed.
+ * In 1D, spectra are planned for every n the fused conv takes (n = 32768
+ * included), taps up to n = 16384 (FUFFT_ERR_UNSUPPORTED beyond). */
 int fufft_plan_filter_device_f32(const void* in, void* out, int64_t n, int64_t count,
                                  int variant, int layout, int filter_kind,
                                  int fold_inv_n, void* stream);

@@ -15,8 +15,9 @@
 //   - the plan objects of include/fufft/plan.hpp (Conv1d with the lane-major
 //     filter at the fastest variant and with the reference's digit order,
 //     Conv1d::from_device, the BFP conv through a Conv1d, ConvLarge with the
-//     reference's V=16 middle, Conv2d) bit for bit against the C calls with
-//     filters planned by hand, and their argument errors as fufft::Error.
+//     reference's V=16 middle, Conv2d, and a Conv1d at N = 32768, the
+//     single-launch 32-values-per-lane conv) bit for bit against the C calls
+//     with filters planned by hand, and their argument errors as fufft::Error.
 // Built by fufft_amd/build.py into tests/cpp/_build/abi_gpu_check and run by
 // tests/test_gpu_cpp_caller.py.  Prints "ok ..." and returns 0 on success.
 #include "fufft/fufft.hpp"
@@ -334,6 +335,35 @@ int main()
          CHECK_HIP(hipMemcpy(b1.data(), d_o, np * nimg * 8, hipMemcpyDeviceToHost));
          CHECK_HIP(hipMemcpy(b2.data(), d_o2, np * nimg * 8, hipMemcpyDeviceToHost));
          if(!same_bits(b1, b2)) { std::fprintf(stderr, "Conv2d differs from the C call\n"); return 28; }
+         plans++;
+      }
+      // (g) N = 32768 in one launch: a Conv1d at its fastest plan (lane-major
+      //     filter) against the C call with the digit-order filter, bit for
+      //     bit (the same plan and arithmetic, another filter layout)
+      {
+         const int64_t nw = 32768, bw = 3;
+         std::vector<float> xw(2 * nw * bw), tw(2 * nw), fw(2 * nw), w1(2 * nw * bw), w2(2 * nw * bw);
+         for(auto& v : xw) v = rng.next();
+         for(auto& v : tw) v = rng.next();
+         fufft::Conv1d<fufft::MidMultiply> wide(nw, tw.data());
+         if(wide.variant() != fufft::Variant::V16 || wide.layout() != FUFFT_LAYOUT_LANE) {
+            std::fprintf(stderr, "Conv1d plan at N = 32768\n");
+            return 30;
+         }
+         CHECK_FU(fufft::plan_filter(tw.data(), fw.data(), nw, fufft::Variant::V16, FUFFT_FILTER_TAPS, FUFFT_LAYOUT_DR));
+         void* d_w = nullptr; void* d_wf = nullptr; void* d_wo = nullptr;
+         CHECK_HIP(hipMalloc(&d_w, (size_t)nw * bw * 8)); CHECK_HIP(hipMalloc(&d_wf, (size_t)nw * 8));
+         CHECK_HIP(hipMalloc(&d_wo, (size_t)nw * bw * 8));
+         CHECK_HIP(hipMemcpy(d_w, xw.data(), (size_t)nw * bw * 8, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_wf, fw.data(), (size_t)nw * 8, hipMemcpyHostToDevice));
+         CHECK_FU(fufft_conv_f32(d_w, d_wf, 0, d_wo, nw, bw, FUFFT_MID_MUL, FUFFT_V16, FUFFT_LAYOUT_DR, s));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(w1.data(), d_wo, (size_t)nw * bw * 8, hipMemcpyDeviceToHost));
+         wide(d_w, d_wo, bw, s);
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(w2.data(), d_wo, (size_t)nw * bw * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipFree(d_w)); CHECK_HIP(hipFree(d_wf)); CHECK_HIP(hipFree(d_wo));
+         if(!same_bits(w1, w2)) { std::fprintf(stderr, "Conv1d at N = 32768 differs from the C call\n"); return 31; }
          plans++;
       }
    } catch(const fufft::Error& e) {

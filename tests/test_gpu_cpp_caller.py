@@ -9,8 +9,9 @@ conv in the reference's own format bit for bit against dequantise -> fp32 conv
 -> quantise; a 64 x 64 image (one fused launch) against an fp64 direct 2D
 cyclic convolution; and the plan objects of include/fufft/plan.hpp (Conv1d
 lane-major / digit order / planned on the device / BFP, ConvLarge with the
-reference's V=16 middle, Conv2d) bit for bit against the C calls with filters
-planned by hand, a per-signal plan refusing a mismatched batch.
+reference's V=16 middle, Conv2d, a Conv1d at N = 32768) bit for bit against
+the C calls with filters planned by hand, a per-signal plan refusing a
+mismatched batch.
 """
 import subprocess
 from pathlib import Path

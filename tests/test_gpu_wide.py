@@ -120,3 +120,26 @@ def test_wide_per_signal_filters_beyond_4gib(dev):
     want = O.conv(a_s, f_s, N, O.kernel_plan(N, 16), filt_stride=N).reshape(len(idx), N)
     assert bits_equal(got, want)
     del x, f, out
+
+
+@pytest.mark.parametrize("layout", ["dr", "lane", "bperm"])
+def test_wide_device_planned_spectra(dev, layout):
+    """Natural-order spectra planned on the device at N = 32768 (a gather:
+    bit-identical to the host planner) drive the fused conv as the host's do;
+    taps are refused at this size (the forward transform exists up to 16384)."""
+    import torch
+    import fufft_amd as ff
+    rng = np.random.default_rng(50 + ["dr", "lane", "bperm"].index(layout))
+    count = 3
+    specs = crandn(rng, count * N)
+    host = np.concatenate([ff.plan_filter(specs[i * N:(i + 1) * N], N, variant="v16", layout=layout)
+                           for i in range(count)])
+    print(f"case wide device planning n={N} layout={layout}", flush=True)
+    d_spec = _dt(specs, dev)
+    out = torch.empty_like(d_spec)
+    ff.plan_filter_device(d_spec, out, N, count=count, variant="v16", layout=layout)
+    torch.cuda.synchronize()
+    assert bits_equal(out.cpu().numpy(), host)
+    with pytest.raises(ff.FufftError):
+        ff.plan_filter_device(d_spec, out, N, count=count, variant="v16", layout=layout, kind=ff.FILTER_TAPS)
+

@@ -86,7 +86,9 @@ def test_n32768_is_the_fused_conv_only():
     assert L.fufft_conv_bfp16(A, A + (1 << 20), B, 0, B + (1 << 20), B + (1 << 21), n, 1, 64, 0, 0, 0, None) \
         == ff.ERR_UNSUPPORTED
     assert L.fufft_conv_timed_f32(A, B, 0, B + (1 << 20), n, 1, 0, 0, 0, None, 0, None) == ff.ERR_UNSUPPORTED
+    # taps need the forward transform (not built at this size); spectra are only permuted
     assert L.fufft_plan_filter_device_f32(A, B, n, 1, 0, 0, 1, 1, None) == ff.ERR_UNSUPPORTED
+    assert L.fufft_plan_filter_device_f32(A, A + 8, n, 1, 0, 0, 0, 1, None) == ff.ERR_ALIGN
     # the radix-8 plan has no N = 32768 kernel, the fused conv included
     assert L.fufft_conv_f32(A, B, 0, B + (1 << 20), n, 1, 0, 1, 0, None) == ff.ERR_UNSUPPORTED
 
