@@ -4,7 +4,8 @@
   they compute one after the other (the calls are stateless).
 - Four host threads on four streams call four entry points concurrently, with
   the same results.
-- fufft_conv_f32, the four-step chain and the 2D conv captured in a graph
+- fufft_conv_f32 (N = 4096 and the single-launch N = 32768), the four-step
+  chain and the 2D conv captured in a graph
   (torch.cuda.CUDAGraph drives hipStreamBeginCapture) replay bit-identically
   to the eager call, replay after replay, with eager work in between.  None
   of these paths issues a memset or allocates, so they capture as plain
@@ -74,6 +75,19 @@ def test_graph_capture_conv(dev, rng):
     f = torch.from_numpy(ff.plan_filter(crandn(rng, n), n, "auto", kind=ff.FILTER_TAPS)).to(dev)
     out = torch.empty_like(a)
     _graph_matches_eager(lambda s: ff.conv(a, f, out, n=n, batch=batch, variant="auto", stream=s), out)
+
+
+def test_graph_capture_conv_n32768(dev, rng):
+    """the single-launch conv at N = 32768 (136 KiB of dynamic LDS) captured and replayed"""
+    import torch
+    import fufft_amd as ff
+    n, batch = 32768, 8
+    print("case graph conv n=32768", flush=True)
+    a = torch.from_numpy(crandn(rng, (batch, n))).to(dev)
+    f = torch.from_numpy(ff.plan_filter(crandn(rng, n), n, "v16", layout="lane", kind=ff.FILTER_TAPS)).to(dev)
+    out = torch.empty_like(a)
+    _graph_matches_eager(lambda s: ff.conv(a, f, out, n=n, batch=batch, variant="v16", layout="lane", stream=s),
+                         out)
 
 
 def test_graph_capture_fourstep_and_2d(dev, rng):
