@@ -292,9 +292,10 @@ struct Buf {
    {
       return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, POL));
    }
+   template<int POL = POL_DEFAULT>
    __device__ __forceinline__ float4 ld4(uint32_t voff, uint32_t soff) const
    {
-      return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+      return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, POL));
    }
    template<int POL = POL_DEFAULT>
    __device__ __forceinline__ uint32_t ldu(uint32_t voff, uint32_t soff) const
