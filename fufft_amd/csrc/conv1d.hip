@@ -184,7 +184,8 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
          // and with a shared (cache-resident) filter -0.4% for the kept chain
          // it gives up, so it is this plan's per-signal kernel only.  Each
          // filter is read once: NT, as the signal (a property of this kernel,
-         // no runtime choice): 246.0 -> 253.8 Gpt/s, same box, bit-identical
+         // no runtime choice): bit-identical, +1.5% in bench.py's per-signal
+         // leg and +3.2% in 100-launch rounds, same box
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
          const uint32_t so = modulo_count(t, p.fcount) * N * 8u + L * 16u;
 #pragma unroll
