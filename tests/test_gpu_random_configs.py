@@ -22,7 +22,10 @@ def draw(seed):
     rng = np.random.default_rng(seed)
     op = OPS[seed % len(OPS)]
     variant = ["r8", "v16"][rng.integers(2)]
-    n = int(rng.choice(BFP_SIZES[variant] if op == "bfp" else SIZES[variant]))   # bfp_scaled: every size
+    sizes = BFP_SIZES[variant] if op == "bfp" else SIZES[variant]               # bfp_scaled: every size
+    if op == "conv" and variant == "v16":
+        sizes = sizes + [32768]                 # the fused conv alone runs N = 32768 in one launch
+    n = int(rng.choice(sizes))
     batch = int(rng.integers(1, max(2, min(37, (1 << 19) // n))))
     return dict(op=op, variant=variant, n=n, batch=batch,
                 mid=["mul", "conj", "none"][rng.integers(3)],
