@@ -11,6 +11,10 @@
    correlation by brute force, linearity, digit order by naive DFT.
 5. The fp64 references themselves against numpy and a naive DFT.
 """
+import subprocess
+import sys
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -135,11 +139,17 @@ def test_conv_r2_libm_matches_reference_bitwise(n, rng):
 
 
 @needs_ref
-def test_reference_self_tests_pass_here():
-    """The reference's own CPU suites (verify_kernel, cpu_mixed, cpu_inplace)."""
-    assert REF.ref_vk_main() == 0
-    assert REF.ref_mixed_main() == 0
-    assert REF.ref_inplace_main() == 0
+@pytest.mark.parametrize("entry", ["ref_vk_main", "ref_mixed_main", "ref_inplace_main"])
+def test_reference_self_tests_pass_here(entry):
+    """The reference's own CPU suites (verify_kernel, cpu_mixed, cpu_inplace),
+    each in a child process: their reports go through C stdio, which would
+    otherwise reach the terminal only when pytest exits."""
+    code = ("import sys; sys.path.insert(0, sys.argv[1]); from oracle import oracle as O; "
+            f"sys.exit(O.load_ref().{entry}())")
+    root = str(Path(__file__).resolve().parent.parent)
+    p = subprocess.run([sys.executable, "-c", code, root], capture_output=True, text=True, timeout=600)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert "FAIL" not in p.stdout.replace("ALL PASS", "")
 
 
 @needs_ref
