@@ -12,14 +12,16 @@ GRID = ((1, 0), (2, 0), (4, 0), (3, 0), (1, 7), (1, 1024))
 POLICY = ((0, 0), (2, 2), (2, 0), (0, 2), (1, 1), (3, 3))
 
 
-@pytest.mark.parametrize("lanes", (64, 256, 1024))
-@pytest.mark.parametrize("width", (8, 16))
-@pytest.mark.parametrize("loads", LOADS)
+# every shape of the copy: a workgroup tile of at most 256 KiB (1024 lanes of
+# 512 bytes in flight would spill registers and is refused)
+SHAPES = [(lanes, width, loads) for lanes in (64, 256, 1024) for width in (8, 16) for loads in LOADS
+          if lanes * width * loads <= 256 * 1024]
+
+
+@pytest.mark.parametrize("lanes,width,loads", SHAPES)
 def test_stream_shapes_copy_exactly(dev, loads, width, lanes):
     import torch
     import fufft_amd as ff
-    if lanes * width * loads > 256 * 1024:
-        pytest.skip("not a shape of the copy: 1024 lanes of 512 bytes in flight would spill registers")
     # 1 MiB + 3 KiB + 16 B: several tiles of every size and a partial last one
     nbytes = (1 << 20) + 3 * 1024 + 16
     gen = torch.Generator(device=dev)
