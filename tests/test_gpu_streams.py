@@ -5,7 +5,7 @@
 - Four host threads on four streams call four entry points concurrently, with
   the same results.
 - fufft_conv_f32 (N = 4096 and the single-launch N = 32768), the four-step
-  chain and the 2D conv captured in a graph
+  chain, the 2D conv and both BFP formats captured in a graph
   (torch.cuda.CUDAGraph drives hipStreamBeginCapture) replay bit-identically
   to the eager call, replay after replay, with eager work in between.  None
   of these paths issues a memset or allocates, so they capture as plain
@@ -43,26 +43,32 @@ def test_two_streams_concurrently(dev, rng):
 
 
 def _graph_matches_eager(run, out, reps=3):
-    """capture run() (writing out), replay reps times with eager work between
-    replays, every replay equal to the eager result"""
+    """capture run() (writing out, a tensor or a tuple of them), replay reps
+    times with eager work between replays, every replay equal to the eager
+    result"""
     import torch
+    outs = out if isinstance(out, tuple) else (out,)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         run(s)                                     # warm-up on the capture stream
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    want = out.clone()
+    want = [o.clone() for o in outs]
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         run(s)
     for i in range(reps):
-        out.zero_()
-        scratch = torch.randn(1 << 20, device=out.device)      # eager work between replays
+        for o in outs:
+            o.zero_()
+        scratch = torch.randn(1 << 20, device=outs[0].device)  # eager work between replays
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), f"replay {i}"
+        for o, w in zip(outs, want):
+            if o.is_floating_point() or o.is_complex():          # bit for bit, not value for value
+                o, w = o.view(torch.int32), w.view(torch.int32)
+            assert torch.equal(o, w), f"replay {i}"
         del scratch
 
 
@@ -109,6 +115,33 @@ def test_graph_capture_fourstep_and_2d(dev, rng):
     f2 = torch.from_numpy(ff.plan_filter2d(crandn(rng, (h, w)), h, w, kind=ff.FILTER_TAPS)).to(dev)
     out2 = torch.empty_like(img)
     _graph_matches_eager(lambda s: ff.conv2d(img, f2, out2, h, w, batch=2, stream=s), out2)
+
+
+def test_graph_capture_bfp(dev, rng):
+    """both int16-BFP formats captured and replayed: 64-point blocks, whole-
+    signal blocks (the LDS rendezvous of the block maxima) and the reference's
+    fp32-scale format with its int16 filter"""
+    import torch
+    import fufft_amd as ff
+    n, batch = 4096, 64
+    x = crandn(rng, (batch, n))
+    taps = crandn(rng, n)
+    f = torch.from_numpy(ff.plan_filter(taps, n, "v16", layout="lane", kind=ff.FILTER_TAPS)).to(dev)
+    for block in (64, n):
+        print(f"case graph bfp block={block}", flush=True)
+        q, e = ff.bfp_quantize(x, block=block)
+        dq, de = torch.from_numpy(q).to(dev), torch.from_numpy(e).to(dev)
+        qo, eo = torch.empty_like(dq), torch.empty_like(de)
+        _graph_matches_eager(lambda s: ff.conv_bfp16(dq, de, f, qo, eo, n=n, batch=batch, variant="v16",
+                                                     layout="lane", stream=s, block=block), (qo, eo))
+    print("case graph bfp scaled", flush=True)
+    q, sc = ff.bfp_scaled_quantize(x, n)
+    fq, fs = ff.bfp_scaled_quantize(ff.plan_filter(taps, n, variant="v16", kind=ff.FILTER_TAPS), n)
+    dq, ds = torch.from_numpy(q).to(dev), torch.from_numpy(sc).to(dev)
+    dfq, dfs = torch.from_numpy(fq).to(dev), torch.from_numpy(fs).to(dev)
+    qo, so = torch.empty_like(dq), torch.empty_like(ds)
+    _graph_matches_eager(lambda s: ff.conv_bfp16_scaled(dq, ds, dfq, dfs, qo, so, n=n, batch=batch,
+                                                        variant="v16", stream=s), (qo, so))
 
 
 def test_host_threads_call_concurrently(dev, rng):
