@@ -264,14 +264,18 @@ def bench_fp32(torch, ff, dev, n, pts, variant, steps, warmup, stream, seed, set
     return secs / steps, rel
 
 
-def bench_vendor_chain(torch, dev, n, pts, steps, warmup, stream, seed):
+def bench_vendor_chain(torch, dev, n, pts, steps, warmup, stream, seed, uniform=False):
     """The vendor-library chain the reference compares against (cuFFT fwd ->
-    pointwise -> inv, bench_fufft.cu:201-213), on MI355X: torch.fft, which
-    calls rocFFT, forward -> multiply -> inverse on the same workload."""
+    pointwise -> inv, bench_fufft.cu:201-213, and beside the four-step at
+    453-478), on MI355X: torch.fft, which calls rocFFT, forward -> multiply ->
+    inverse on the same workload (Re/Im N(0,1), or U[-1,1) with uniform)."""
     batch = pts // n
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
-    x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen).view(batch, n)
+    if uniform:
+        x = (torch.rand(2 * pts, device=dev, generator=gen) * 2 - 1).view(torch.complex64).view(batch, n)
+    else:
+        x = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen).view(batch, n)
     rng = np.random.default_rng(seed)
     taps = (rng.standard_normal(n) + 1j * rng.standard_normal(n)).astype(np.complex64)
     spec = torch.fft.fft(torch.from_numpy(taps).to(dev))
@@ -943,6 +947,14 @@ def main():
                         "rel_l2": r}
         # the default middle (the reference's) with the radix-8 one beside it
         large[str(s)] = {**legs["v16"], "variant": "v16", "r8_middle": legs["r8"]}
+        if not args.no_vendor:
+            # the reference times its four-step against the cuFFT chain at this N
+            # (bench_fufft.cu:453-478); here rocFFT through torch.fft, same batch
+            vt, vrel = bench_vendor_chain(torch, dev, s, pts, args.sweep_steps, 3, stream, 1234 + s, uniform=True)
+            large[str(s)]["rocfft_chain"] = {"what": "torch.fft (rocFFT) forward -> multiply -> inverse, same batch",
+                                             "gpoints_s": round(pts / vt / 1e9, 3), "ms": round(vt * 1e3, 5),
+                                             "rel_l2": vrel}
+            large[str(s)]["speedup_vs_rocfft"] = round(vt * 1e3 / legs["v16"]["ms"], 3)
         if ff.supported(s, "v16"):
             # the same size as one fused conv (N = 32768: a workgroup per
             # transform, 32 values per lane), 16 B/pt, both filter layouts
@@ -961,6 +973,9 @@ def main():
                         "(not the reference's four-step chain); N(0,1) signals, one shared filter",
                 **single["lane"], "filter_layout": "lane", "dr_filter": single["dr"],
                 "speedup_vs_fourstep": round(legs["v16"]["ms"] / single["lane"]["ms"], 3)}
+            if "rocfft_chain" in large[str(s)]:
+                large[str(s)]["single_launch"]["speedup_vs_rocfft"] = round(
+                    large[str(s)]["rocfft_chain"]["ms"] / single["lane"]["ms"], 3)
     if large:
         line["large"] = large
 
