@@ -845,8 +845,12 @@ def main():
                      "filter_layout": args.layout, "bytes_per_point": 24,
                      "achieved_gbs": round(24.0 * pts / a / 1e9, 1), "frac": frac(24.0 * pts, a), "rel_l2": r}}
 
+    # seconds per call of the rocFFT chain by N: the reference's published
+    # ratios are against the vendor chain (README.md:12-13, bench_fufft.cu:201-246)
+    chain_s = {}
     if not args.no_vendor:
         vt, vrel = bench_vendor_chain(torch, dev, n, pts, args.sweep_steps, 3, stream, 1234)
+        chain_s[n] = vt
         line["vendor_chain"] = {"what": "torch.fft (rocFFT) forward -> multiply -> inverse, same workload",
                                 "gpoints_s": round(pts / vt / 1e9, 3), "ms": round(vt * 1e3, 5),
                                 "rel_l2": vrel, "fused_speedup": round(vt / avg, 3)}
@@ -865,6 +869,12 @@ def main():
         if not r <= 2e-6:
             print(json.dumps({"error": f"fp32 accuracy check failed at N={s}: rel L2 {r:.3e}"}))
             sys.exit(1)
+        if not args.no_vendor:
+            vt_s, vrel_s = bench_vendor_chain(torch, dev, s, pts, args.sweep_steps, 3, stream, 1234 + s)
+            chain_s[s] = vt_s
+            sweep[str(s)]["rocfft_chain"] = {"gpoints_s": round(pts / vt_s / 1e9, 3), "ms": round(vt_s * 1e3, 5),
+                                             "rel_l2": vrel_s}
+            sweep[str(s)]["speedup_vs_rocfft"] = round(vt_s / a, 3)
     if sweep:
         line["sweep"] = sweep
 
@@ -886,6 +896,9 @@ def main():
                            "frac": frac(bb, a), "model_frac_12B": round(12.0 * pts / a / 1e9 / HBM_PEAK_GBS, 4),
                            "rel_l2_vs_fp64_unquantised": r, "worst_signal_rel_l2": worst,
                            "variant": bv, "filter_layout": args.layout}
+            if s in chain_s:
+                # against the fp32 rocFFT chain at this N (the reference: 4.3-4.5x against cuFFT's)
+                bfp[str(s)]["speedup_vs_rocfft"] = round(chain_s[s] / a, 3)
             if s == n:
                 # both legs timed the same way: check, SETTLE_S, --warmup, --steps
                 bfp[str(s)]["speedup_vs_fp32"] = round(g / gpts, 3)
