@@ -17,7 +17,11 @@
 //     Conv1d::from_device, the BFP conv through a Conv1d, ConvLarge with the
 //     reference's V=16 middle, Conv2d, and a Conv1d at N = 32768, the
 //     single-launch 32-values-per-lane conv) bit for bit against the C calls
-//     with filters planned by hand, and their argument errors as fufft::Error.
+//     with filters planned by hand, and their argument errors as fufft::Error;
+//   - the reference's launch surface by name (fufft::ref: fufft_pipeline_v16,
+//     _ip, _v16f, _fwd / _apply, _v16_bfp, run_large) with one filter per
+//     transform, bit for bit against the C calls, and run_large refusing a
+//     split the library does not run.
 // Built by fufft_amd/build.py into tests/cpp/_build/abi_gpu_check and run by
 // tests/test_gpu_cpp_caller.py.  Prints "ok ..." and returns 0 on success.
 #include "fufft/fufft.hpp"
@@ -371,11 +375,122 @@ int main()
       return 29;
    }
 
+   // 9. the reference's launch surface by name (fufft::ref), one filter per
+   //    transform as its kernels read them, against the C calls
+   int refs = 0;
+   {
+      std::vector<float> x(2 * pts), tb(2 * pts), f16(2 * pts), f8(2 * pts), fbp(2 * pts), want(2 * pts), got(2 * pts);
+      for(auto& v : x) v = rng.next();
+      for(auto& v : tb) v = rng.next();
+      for(int64_t t = 0; t < batch; t++) {
+         CHECK_FU(fufft::plan_filter(tb.data() + 2 * t * n, f16.data() + 2 * t * n, n, fufft::Variant::V16));
+         CHECK_FU(fufft::plan_filter(tb.data() + 2 * t * n, f8.data() + 2 * t * n, n, fufft::Variant::R8));
+         CHECK_FU(fufft::plan_filter(tb.data() + 2 * t * n, fbp.data() + 2 * t * n, n, fufft::Variant::V16,
+                                     FUFFT_FILTER_TAPS, FUFFT_LAYOUT_BPERM));
+      }
+      void *d_f16 = nullptr, *d_f8 = nullptr, *d_fbp = nullptr;
+      CHECK_HIP(hipMalloc(&d_f16, pts * 8)); CHECK_HIP(hipMalloc(&d_f8, pts * 8)); CHECK_HIP(hipMalloc(&d_fbp, pts * 8));
+      CHECK_HIP(hipMemcpy(d_a, x.data(), pts * 8, hipMemcpyHostToDevice));
+      CHECK_HIP(hipMemcpy(d_f16, f16.data(), pts * 8, hipMemcpyHostToDevice));
+      CHECK_HIP(hipMemcpy(d_f8, f8.data(), pts * 8, hipMemcpyHostToDevice));
+      CHECK_HIP(hipMemcpy(d_fbp, fbp.data(), pts * 8, hipMemcpyHostToDevice));
+      // 0 when d_o and d_o2 hold the same bits, else `code` (10 on a HIP error)
+      auto compare = [&](const char* what, int code) -> int {
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(want.data(), d_o, pts * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(got.data(), d_o2, pts * 8, hipMemcpyDeviceToHost));
+         if(!same_bits(want, got)) { std::fprintf(stderr, "fufft::ref::%s differs from the C call\n", what); return code; }
+         refs++;
+         return 0;
+      };
+      // fufft_pipeline_v16<N, LEAD, NRV, CPB> with MidMultiply{b}
+      CHECK_FU(fufft_conv_f32(d_a, d_f16, n, d_o, n, batch, FUFFT_MID_MUL, FUFFT_V16, FUFFT_LAYOUT_DR, s));
+      CHECK_FU((fufft::ref::fufft_pipeline_v16<4096, 1, 3, 1>(d_a, d_o2, fufft::MidMultiply{d_f16}, batch, s)));
+      if(const int r = compare("fufft_pipeline_v16", 40)) return r;
+      // fufft_pipeline_ip<N, LEAD, NR8, CPB, Mid> with a correlation
+      CHECK_FU(fufft_conv_f32(d_a, d_f8, n, d_o, n, batch, FUFFT_MID_CONJ, FUFFT_R8, FUFFT_LAYOUT_DR, s));
+      CHECK_FU((fufft::ref::fufft_pipeline_ip<4096, 1, 4, 8, fufft::MidConjMultiply>(
+         d_a, d_o2, fufft::MidConjMultiply{d_f8}, batch, s)));
+      if(const int r = compare("fufft_pipeline_ip", 41)) return r;
+      // fufft_pipeline_v16f<N, LEAD, NRV, CPB> with the bperm filter: the same
+      // results as fufft_pipeline_v16 with the digit-order one
+      CHECK_FU(fufft_conv_f32(d_a, d_f16, n, d_o, n, batch, FUFFT_MID_MUL, FUFFT_V16, FUFFT_LAYOUT_DR, s));
+      CHECK_FU((fufft::ref::fufft_pipeline_v16f<4096, 1, 3, 1>(d_a, d_fbp, d_o2, batch, s)));
+      if(const int r = compare("fufft_pipeline_v16f", 42)) return r;
+      // fufft_pipeline_fwd + fufft_pipeline_apply (radix 8) against fufft_pipeline_ip
+      CHECK_FU((fufft::ref::fufft_pipeline_ip<4096, 1, 4, 8, fufft::MidMultiply>(
+         d_a, d_o, fufft::MidMultiply{d_f8}, batch, s)));
+      CHECK_FU((fufft::ref::fufft_pipeline_fwd<4096, 1, 4, 8>(d_a, d_spec, batch, s)));
+      CHECK_FU((fufft::ref::fufft_pipeline_apply<4096, 1, 4, 8>(d_spec, d_f8, d_o2, batch, s)));
+      if(const int r = compare("fufft_pipeline_fwd / _apply", 43)) return r;
+      // fufft_pipeline_v16_bfp<N, LEAD, NRV, CPB>: int16 filter and scale per transform
+      {
+         std::vector<int16_t> q(2 * pts), fq(2 * pts), q1(2 * pts), q2(2 * pts);
+         std::vector<float> sc(batch), fs(batch), s1(batch), s2(batch);
+         CHECK_FU(fufft_bfp_scaled_quantize(x.data(), n, batch, q.data(), sc.data()));
+         CHECK_FU(fufft_bfp_scaled_quantize(f16.data(), n, batch, fq.data(), fs.data()));
+         void *d_q = nullptr, *d_fq = nullptr, *d_qo = nullptr;
+         float *d_s = nullptr, *d_fs = nullptr, *d_so = nullptr;
+         CHECK_HIP(hipMalloc(&d_q, pts * 4)); CHECK_HIP(hipMalloc(&d_fq, pts * 4)); CHECK_HIP(hipMalloc(&d_qo, pts * 4));
+         CHECK_HIP(hipMalloc(&d_s, batch * 4)); CHECK_HIP(hipMalloc(&d_fs, batch * 4)); CHECK_HIP(hipMalloc(&d_so, batch * 4));
+         CHECK_HIP(hipMemcpy(d_q, q.data(), pts * 4, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_fq, fq.data(), pts * 4, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_s, sc.data(), batch * 4, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_fs, fs.data(), batch * 4, hipMemcpyHostToDevice));
+         CHECK_FU(fufft_conv_bfp16_scaled(d_q, d_s, d_fq, d_fs, n, d_qo, d_so, n, batch, FUFFT_MID_MUL, FUFFT_V16,
+                                          FUFFT_LAYOUT_DR, s));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(q1.data(), d_qo, pts * 4, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(s1.data(), d_so, batch * 4, hipMemcpyDeviceToHost));
+         CHECK_FU((fufft::ref::fufft_pipeline_v16_bfp<4096, 1, 3, 1>(d_q, d_s, d_fq, d_fs, d_qo, d_so, batch, s)));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(q2.data(), d_qo, pts * 4, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(s2.data(), d_so, batch * 4, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipFree(d_q)); CHECK_HIP(hipFree(d_fq)); CHECK_HIP(hipFree(d_qo));
+         CHECK_HIP(hipFree(d_s)); CHECK_HIP(hipFree(d_fs)); CHECK_HIP(hipFree(d_so));
+         if(std::memcmp(q1.data(), q2.data(), q1.size() * 2) != 0 || std::memcmp(s1.data(), s2.data(), s1.size() * 4) != 0) {
+            std::fprintf(stderr, "fufft::ref::fufft_pipeline_v16_bfp differs from the C call\n");
+            return 44;
+         }
+         refs++;
+      }
+      // run_large<N, LOUT, ROUT, MID, MLEAD, MNRV>: the reference bench's own
+      // configuration, one chained filter per transform; a split the library
+      // does not run is refused before any launch
+      {
+         const int64_t nl = 32768, bl = 2;
+         std::vector<float> tl(2 * nl * bl), fl2(2 * nl * bl), xl(2 * nl * bl), a1(2 * nl * bl), a2(2 * nl * bl);
+         for(auto& v : tl) v = rng.next();
+         for(auto& v : xl) v = rng.next();
+         for(int64_t t = 0; t < bl; t++)
+            CHECK_FU(fufft_plan_filter_large_f32(nl, FUFFT_V16, FUFFT_FILTER_TAPS, 1, tl.data() + 2 * t * nl,
+                                                 fl2.data() + 2 * t * nl));
+         void* d_l = nullptr; void* d_lf = nullptr;
+         CHECK_HIP(hipMalloc(&d_l, (size_t)nl * bl * 8)); CHECK_HIP(hipMalloc(&d_lf, (size_t)nl * bl * 8));
+         CHECK_HIP(hipMemcpy(d_lf, fl2.data(), (size_t)nl * bl * 8, hipMemcpyHostToDevice));
+         CHECK_HIP(hipMemcpy(d_l, xl.data(), (size_t)nl * bl * 8, hipMemcpyHostToDevice));
+         CHECK_FU(fufft_conv_large_f32(d_l, d_lf, nl, nl, bl, FUFFT_MID_MUL, FUFFT_V16, s));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(a1.data(), d_l, (size_t)nl * bl * 8, hipMemcpyDeviceToHost));
+         CHECK_HIP(hipMemcpy(d_l, xl.data(), (size_t)nl * bl * 8, hipMemcpyHostToDevice));
+         CHECK_FU((fufft::ref::run_large<32768, 1, 16, 2048, 8, 2>(d_l, d_lf, bl, s)));
+         CHECK_HIP(hipStreamSynchronize(s));
+         CHECK_HIP(hipMemcpy(a2.data(), d_l, (size_t)nl * bl * 8, hipMemcpyDeviceToHost));
+         const int refused = fufft::ref::run_large<32768, 2, 16, 128, 8, 1>(d_l, d_lf, bl, s);
+         CHECK_HIP(hipFree(d_l)); CHECK_HIP(hipFree(d_lf));
+         if(!same_bits(a1, a2)) { std::fprintf(stderr, "fufft::ref::run_large differs from the C call\n"); return 45; }
+         if(refused != FUFFT_ERR_UNSUPPORTED) { std::fprintf(stderr, "run_large ran a split the library does not\n"); return 46; }
+         refs++;
+      }
+      CHECK_HIP(hipFree(d_f16)); CHECK_HIP(hipFree(d_f8)); CHECK_HIP(hipFree(d_fbp));
+   }
+
    CHECK_HIP(hipFree(d_a)); CHECK_HIP(hipFree(d_f)); CHECK_HIP(hipFree(d_o));
    CHECK_HIP(hipFree(d_o2)); CHECK_HIP(hipFree(d_spec));
    CHECK_HIP(hipStreamDestroy(s));
    std::printf("ok C++ caller: n=%lld batch=%lld, template == C entry == split == in place, rel L2 vs fp64 direct %.2e; "
-               "reference-format BFP == its definition; 64x64 2D rel L2 %.2e; %d plan objects == their C calls\n",
-               (long long)n, (long long)batch, rel, rel2, plans);
+               "reference-format BFP == its definition; 64x64 2D rel L2 %.2e; %d plan objects == their C calls; "
+               "%d reference-named launches == their C calls\n",
+               (long long)n, (long long)batch, rel, rel2, plans, refs);
    return 0;
 }

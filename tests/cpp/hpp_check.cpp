@@ -42,6 +42,21 @@ int main()
    if(fufft::plan_filter_large_device(nullptr, nullptr, 4096) != FUFFT_ERR_UNSUPPORTED) return 11;
    if(fufft::plan_filter2d_device(nullptr, nullptr, 512, 512) != FUFFT_ERR_INVALID) return 12;
    if(fufft_transforms_per_workgroup(4096, FUFFT_R8) != 1 || fufft_transforms_per_workgroup(512, FUFFT_R8) != 4) return 13;
+   // the reference's launch surface by name: argument errors before any device
+   // call, and a four-step split the library does not run refused as such
+   {
+      namespace R = fufft::ref;
+      if((R::fufft_pipeline_v16<4096, 1, 3, 1>(nullptr, nullptr, fufft::MidMultiply{}, 1)) != FUFFT_ERR_INVALID) return 19;
+      if((R::fufft_pipeline_ip<4096, 1, 4, 8, fufft::MidConjMultiply>(nullptr, nullptr, fufft::MidConjMultiply{}, 1)) !=
+         FUFFT_ERR_INVALID) return 20;
+      if((R::fufft_pipeline_v16_bfp<512, 2, 2, 16>(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1)) !=
+         FUFFT_ERR_INVALID) return 21;
+      if((R::fufft_c2c<512, 3, 1>(nullptr, nullptr, 1)) != FUFFT_ERR_INVALID) return 22;
+      if((R::fufft_conv2d<64, 64, 1>(nullptr, nullptr, fufft::MidMultiply{}, 1)) != FUFFT_ERR_INVALID) return 23;
+      if((R::run_large<32768, 1, 16, 2048, 8, 2>(nullptr, nullptr, 1)) != FUFFT_ERR_INVALID) return 24;
+      if((R::run_large<32768, 2, 16, 128, 8, 1>(nullptr, nullptr, 1)) != FUFFT_ERR_UNSUPPORTED) return 25;
+      if((R::run_large<65536, 1, 16, 4096, 1, 3>(nullptr, nullptr, 1)) != FUFFT_ERR_INVALID) return 26;
+   }
    std::printf("ok %s\n", fufft::status_string(FUFFT_OK));
    return 0;
 }

@@ -370,6 +370,47 @@ def test_cpp_mirror_header_builds_and_runs(tmp_path):
     assert out.stdout.startswith("ok")
 
 
+# fufft::ref (the reference's launch surface by name): a template whose
+# parameters do not spell a plan the library runs must not compile.  Each case
+# is a call that compiles with the first template arguments and fails with the
+# second, with the static_assert's text.
+REF_TEMPLATE_CASES = [
+    ("fufft_pipeline_v16<4096, 1, 3, 1>", "fufft_pipeline_v16<4096, 2, 3, 1>",
+     "(nullptr, nullptr, fufft::MidMultiply{}, 1)", "N must be LEAD * 16^NRV"),
+    ("fufft_pipeline_v16f<2048, 8, 2, 1>", "fufft_pipeline_v16f<2048, 16, 1, 1>",
+     "(nullptr, nullptr, nullptr, 1)", "N must be LEAD * 16^NRV"),
+    ("fufft_pipeline_ip<1024, 2, 3, 4, fufft::MidNothing>", "fufft_pipeline_ip<4096, 8, 3, 4, fufft::MidNothing>",
+     "(nullptr, nullptr, fufft::MidNothing{}, 1)", "N must be LEAD * 8^NR8"),
+    ("fufft_pipeline_v16_bfp<4096, 1, 3, 16>", "fufft_pipeline_v16_bfp<4096, 1, 3, 32>",
+     "(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 1)", "1 <= CPB <= 16"),
+    ("fufft_c2c<4096, 4, 1>", "fufft_c2c<4096, 3, 1>", "(nullptr, nullptr, 1)", "N must be 8^LOG8N"),
+    ("run_large<32768, 1, 16, 2048, 8, 2>", "run_large<32768, 1, 8, 4096, 1, 4>", "(nullptr, nullptr, 1)",
+     "the outer levels are radix 16"),
+    ("run_large<65536, 1, 16, 4096, 1, 3>", "run_large<65536, 1, 16, 4096, 2, 3>", "(nullptr, nullptr, 1)",
+     "N must be 16^LOUT * MID"),
+]
+
+
+@pytest.mark.parametrize("good,bad,args,message", REF_TEMPLATE_CASES)
+def test_cpp_reference_templates_checked_at_compile_time(tmp_path, good, bad, args, message):
+    import shutil
+    import subprocess
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+
+    def compile_call(call):
+        src = tmp_path / "ref_case.cpp"
+        src.write_text('#include "fufft/fufft.hpp"\nint f() { return fufft::ref::' + call + args + '; }\n')
+        return subprocess.run(["g++", "-std=c++17", "-fsyntax-only", f"-I{ROOT / 'include'}", str(src)],
+                              capture_output=True, text=True)
+
+    ok = compile_call(good)
+    assert ok.returncode == 0, ok.stderr
+    refused = compile_call(bad)
+    assert refused.returncode != 0
+    assert message in refused.stderr, refused.stderr[-2000:]
+
+
 def test_cpp_plan_objects_build_and_reject_bad_arguments(tmp_path):
     """include/fufft/plan.hpp (plan objects that own their device filter)
     compiles with g++ against the HIP headers, and each plan object throws
