@@ -844,6 +844,20 @@ def main():
             "fp32": {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": var,
                      "filter_layout": args.layout, "bytes_per_point": 24,
                      "achieved_gbs": round(24.0 * pts / a / 1e9, 1), "frac": frac(24.0 * pts, a), "rel_l2": r}}
+        # the same protocol in the reference's own format as well: its plan
+        # (fufft_pipeline_v16) and its digit-order filters, what
+        # fufft::ref::fufft_pipeline_v16 runs (bench_fufft.cu:166-169, 218-219)
+        a, r = bench_fp32(torch, ff, dev, n, pts, "v16", args.sweep_steps, 3, stream, 4322, SETTLE_S,
+                          layout="dr", per_signal=True)
+        if not r <= 2e-6:
+            print(json.dumps({"error": f"fp32 per-signal digit-order accuracy check failed at N={n}: "
+                                       f"rel L2 {r:.3e}"}))
+            sys.exit(1)
+        line["per_signal_filter"]["fp32_reference_plan"] = {
+            "what": "the reference's plan and digit-order filters, one per signal",
+            "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": "v16", "filter_layout": "dr",
+            "bytes_per_point": 24, "achieved_gbs": round(24.0 * pts / a / 1e9, 1), "frac": frac(24.0 * pts, a),
+            "rel_l2": r}
 
     # seconds per call of the rocFFT chain by N: the reference's published
     # ratios are against the vendor chain (README.md:12-13, bench_fufft.cu:201-246)
@@ -934,6 +948,20 @@ def main():
                 line.setdefault("per_signal_filter", {})["bfp_reference_format"] = {
                     "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": bv,
                     "filter_layout": args.layout, "bytes_per_point": 12,
+                    "achieved_gbs": round(12.0 * pts / a / 1e9, 1), "frac": frac(12.0 * pts, a),
+                    "rel_l2_vs_fp64_unquantised": r}
+                # and the reference's own call: its plan and digit-order int16 filters
+                # (fufft_pipeline_v16_bfp, bench_fufft.cu:172-178, 220-221)
+                a, r = bench_bfp_scaled(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 399 + s, variant="v16",
+                                        layout="dr", per_signal=True)
+                if not r <= 1e-4:
+                    print(json.dumps({"error": f"BFP (reference call, filter per signal) accuracy check failed "
+                                               f"at N={s}: rel L2 {r:.3e}"}))
+                    sys.exit(1)
+                line["per_signal_filter"]["bfp_reference_plan"] = {
+                    "what": "the reference's plan and digit-order int16 filters, one per signal",
+                    "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": "v16",
+                    "filter_layout": "dr", "bytes_per_point": 12,
                     "achieved_gbs": round(12.0 * pts / a / 1e9, 1), "frac": frac(12.0 * pts, a),
                     "rel_l2_vs_fp64_unquantised": r}
         line["bfp"] = bfp
