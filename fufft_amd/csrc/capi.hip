@@ -565,11 +565,13 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
    // N = 32768: one workgroup per transform, 32 values per lane
    if(conv_wide_plan(n, v)) return status_of(launch_conv_wide(p, static_cast<hipStream_t>(stream)));
-   // one lane-major filter per signal at radix 16, N = 4096: the kernel that
-   // loads each signal's filter with the signal (K_CONV_PSF)
-   const bool psf = conv_psf_plan((int)n, v) && layout == FUFFT_LAYOUT_LANE && filt_stride == n &&
-                    mid_needs_filter(mid);
-   return run_conv1d(psf ? K_CONV_PSF : K_CONV, (int)n, v, p, stream);
+   // one filter per signal at radix 16, N = 4096: the kernels that load each
+   // signal's filter with the signal (K_CONV_PSF lane-major, K_CONV_PSF_DR the
+   // reference's digit order)
+   const bool psf = conv_psf_plan((int)n, v) && filt_stride == n && mid_needs_filter(mid) &&
+                    (layout == FUFFT_LAYOUT_LANE || layout == FUFFT_LAYOUT_DR);
+   const int kind = !psf ? K_CONV : layout == FUFFT_LAYOUT_LANE ? K_CONV_PSF : K_CONV_PSF_DR;
+   return run_conv1d(kind, (int)n, v, p, stream);
 }
 
 static_assert(TIMER_STRIDE == FUFFT_TIMER_STRIDE, "timer record layout");

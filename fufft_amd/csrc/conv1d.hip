@@ -77,12 +77,15 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
    constexpr bool C2C_INV   = KIND == K_C2C_INV;
    constexpr bool PLAN      = KIND == K_PLAN_TAPS;
    constexpr bool TIMED     = KIND == K_CONV_TIMED;
-   // one lane-major filter per signal: its loads go out with the signal's
-   constexpr bool PSF       = KIND == K_CONV_PSF && mid_reads_filter<MID>;
+   // one filter per signal: its loads go out with the signal's (lane-major
+   // pairs, or digit order handed to the lanes through LDS at the mid)
+   constexpr bool PSF       = (KIND == K_CONV_PSF || KIND == K_CONV_PSF_DR) && mid_reads_filter<MID>;
+   constexpr bool PSF_DR    = PSF && KIND == K_CONV_PSF_DR;
    // the signal read and the result written once per launch stream past the
    // caches in the single-launch conv and C2C; the four-step middle, the split
    // and 2D row kernels keep the default policy
-   constexpr int  IO_POL    = (KIND == K_CONV || KIND == K_CONV_PSF || TIMED || C2C_FWD || C2C_INV) ? POL_NT
+   constexpr int  IO_POL    = (KIND == K_CONV || KIND == K_CONV_PSF || KIND == K_CONV_PSF_DR || TIMED || C2C_FWD ||
+                               C2C_INV) ? POL_NT
                                                                                               : POL_DEFAULT;
    constexpr int  EL_IN     = REAL_IN ? 4 : 8;
    constexpr int  EL_OUT    = REAL_OUT ? 4 : 8;
@@ -187,9 +190,13 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
          // no runtime choice): bit-identical, +1.5% in bench.py's per-signal
          // leg and +3.2% in 100-launch rounds, same box
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
-         const uint32_t so = modulo_count(t, p.fcount) * N * 8u + L * 16u;
+         if constexpr(PSF_DR) {
+            dr_runs_load<PL, POL_NT>(pf, fb, modulo_count(t, p.fcount) * N, L);
+         } else {
+            const uint32_t so = modulo_count(t, p.fcount) * N * 8u + L * 16u;
 #pragma unroll
-         for(int m = 0; m < V / 2; m++) pf[m] = fb.ld4<POL_NT>(so, m * T * 16);
+            for(int m = 0; m < V / 2; m++) pf[m] = fb.ld4<POL_NT>(so, m * T * 16);
+         }
       }
       stamp(1);
       if constexpr(C2C_INV) natural_to_digit<PL, LD, LANES, true>(r, A, L);
@@ -226,7 +233,13 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
          const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
          const uint32_t fb0 = modulo_count(t, p.fcount) * N;
          // a uniform branch on the filter layout: each side computes only its own offset
-         if constexpr(PSF) {
+         if constexpr(PSF_DR) {
+            using Op = MidOf<MID>;
+            float2 b[V];
+            dr_runs_stage<PL, typename LD::template at<PL, PL::NP - 2>>(b, pf, A, L);
+#pragma unroll
+            for(int k = 0; k < V; k++) r[k] = Op::apply(r[k], b[k]);
+         } else if constexpr(PSF) {
             using Op = MidOf<MID>;
 #pragma unroll
             for(int m = 0; m < V / 2; m++) {
@@ -356,6 +369,13 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
          // lane-major filters only (the launcher's choice)
          if constexpr(conv_psf_plan(N, V)) {
             return p.fl == FLT_LANE ? launch_mid<N, V, LAYOUT, K_CONV_PSF>(p, s) : hipErrorInvalidValue;
+         } else {
+            return hipErrorInvalidValue;
+         }
+      case K_CONV_PSF_DR:
+         // digit-order filters only (the launcher's choice)
+         if constexpr(conv_psf_plan(N, V)) {
+            return p.fl == FLT_DR ? launch_mid<N, V, LAYOUT, K_CONV_PSF_DR>(p, s) : hipErrorInvalidValue;
          } else {
             return hipErrorInvalidValue;
          }

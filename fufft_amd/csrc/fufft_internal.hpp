@@ -57,11 +57,15 @@ __host__ __device__ constexpr uint32_t lane_position(uint32_t slot, uint32_t tlo
 // K_CONV_PSF: K_CONV for one lane-major filter per signal at radix 16,
 // N = 4096: the filter loads go out with the signal loads (without the kept
 // twiddle chain, for the registers they hold through the forward DIF).
+// K_CONV_PSF_DR: the same for one digit-order filter per signal (the
+// reference's own per-signal format): the loads of each wavefront's 1 KiB
+// filter runs go out with the signal loads, the hand-off to the lanes goes
+// through LDS at the mid operation.
 enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_R2 = 5,
        K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9, K_CONV_MID = 10,
-       K_CONV_PSF = 11 };
+       K_CONV_PSF = 11, K_CONV_PSF_DR = 12 };
 
-// the plans K_CONV_PSF is built for
+// the plans K_CONV_PSF and K_CONV_PSF_DR are built for
 constexpr bool conv_psf_plan(int n, int v) { return n == 4096 && v == 16; }
 
 // phase timer record of one workgroup (K_CONV_TIMED), TIMER_STRIDE words:

@@ -610,6 +610,39 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
    }
 }
 
+// The two halves of load_dr_staged, for a caller that issues the loads early
+// (the per-signal kernel, K_CONV_PSF_DR): the wavefront's V*64 contiguous
+// slots from fslot0 + its first slot, 1 KiB per 16-byte load (POL: cache
+// policy) ...
+template<class PL, int POL = POL_DEFAULT>
+__device__ __forceinline__ void dr_runs_load(float4 (&q)[PL::V / 2], const Buf& f, uint32_t fslot0, int L)
+{
+   constexpr int V = PL::V;
+   static_assert(PL::T >= 64, "whole wavefronts per transform");
+   const int wl = L & 63, w0 = (L & ~63) * V;      // lane in the wavefront, the wavefront's first slot
+#pragma unroll
+   for(int m = 0; m < V / 2; m++) q[m] = f.ld4<POL>((fslot0 + (uint32_t)w0) * 8u + (uint32_t)wl * 16u, m * 1024);
+}
+
+// ... and the hand-off to the lanes that hold those slots, through the LDS
+// positions they hold in the last pass (layout LDL), which no other wavefront
+// touches until this one's inverse reuses them (a wavefront fence)
+template<class PL, class LDL>
+__device__ __forceinline__ void dr_runs_stage(float2 (&b)[PL::V], const float4 (&q)[PL::V / 2], float2* A, int L)
+{
+   constexpr int V = PL::V;
+   const int wl = L & 63, w0 = (L & ~63) * V;
+#pragma unroll
+   for(int m = 0; m < V / 2; m++) {
+      const int s = w0 + m * 128 + 2 * wl;
+      A[LDL::phys(s)]     = make_float2(q[m].x, q[m].y);
+      A[LDL::phys(s + 1)] = make_float2(q[m].z, q[m].w);
+   }
+   pass_barrier<64>();
+#pragma unroll
+   for(int k = 0; k < V; k++) b[k] = A[LDL::phys(L * V + k)];
+}
+
 // The lane's V digit-order filter values, slots L*V .. L*V + V - 1 from
 // fslot0, passed through LDS.  Read in place they are V/2 16-byte loads 16*V
 // bytes apart, so a wavefront instruction touches 64 (V = 16) cache lines.
@@ -621,21 +654,9 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
 template<class PL, class LDL>
 __device__ __forceinline__ void load_dr_staged(float2 (&b)[PL::V], const Buf& f, uint32_t fslot0, float2* A, int L)
 {
-   constexpr int V = PL::V;
-   static_assert(PL::T >= 64, "whole wavefronts per transform");
-   const int wl = L & 63, w0 = (L & ~63) * V;      // lane in the wavefront, the wavefront's first slot
-   float4 q[V / 2];
-#pragma unroll
-   for(int m = 0; m < V / 2; m++) q[m] = f.ld4((fslot0 + (uint32_t)w0) * 8u + (uint32_t)wl * 16u, m * 1024);
-#pragma unroll
-   for(int m = 0; m < V / 2; m++) {
-      const int s = w0 + m * 128 + 2 * wl;
-      A[LDL::phys(s)]     = make_float2(q[m].x, q[m].y);
-      A[LDL::phys(s + 1)] = make_float2(q[m].z, q[m].w);
-   }
-   pass_barrier<64>();
-#pragma unroll
-   for(int k = 0; k < V; k++) b[k] = A[LDL::phys(L * V + k)];
+   float4 q[PL::V / 2];
+   dr_runs_load<PL>(q, f, fslot0, L);
+   dr_runs_stage<PL, LDL>(b, q, A, L);
 }
 
 template<class PL, class LDL, int MID>

@@ -42,7 +42,7 @@ TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
 
 KINDS = {0: "conv", 1: "conv_r2", 2: "fwd", 3: "apply", 4: "fwd_r2", 5: "apply_r2",
          6: "c2c_fwd", 7: "c2c_inv", 8: "plan_taps", 9: "conv_timed", 10: "conv_mid",
-         11: "conv_psf"}
+         11: "conv_psf", 12: "conv_psf_dr"}
 MIDS = {0: "mul", 1: "conj", 2: "none"}
 LAYOUTS = {0: "xor", 1: "pad", 2: "xchg"}
 FILTERS = {0: "dr", 1: "lane", 2: "bperm"}
@@ -200,29 +200,30 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
     one_dir =sum((v // r) * (DFT_OPS[r] + (4 * (2 * r - 3) if M > 1 else 0)) for r, M in ps)
     exchanges = len(ps) - 1
     twiddle_slots = sum(v // r for r, M in ps if M > 1)
-    two = kind in ("conv", "conv_r2", "conv_timed", "conv_psf")
+    two = kind in ("conv", "conv_r2", "conv_timed", "conv_psf", "conv_psf_dr")
     arith = one_dir * (2 if two else 1)
     # the forward's last twiddled pass hands its chain to the inverse when that
     # pass has one group per lane and the registers allow it (KeptChain): pure
     # powers of the radix, and radix 16 up to N = 2048 behind a lead pass;
     # R - 2 fewer complex products per lane, 6 at radix 8 and 14 at radix 16
-    # (the per-signal kernel conv_psf holds its filter in those registers instead)
-    if two and kind != "conv_psf" and len(ps) >= 2 and ps[-2][0] == v and ps[-2][1] > 1 and \
+    # (the per-signal kernels conv_psf / conv_psf_dr hold their filter in those registers instead)
+    if two and kind not in ("conv_psf", "conv_psf_dr") and len(ps) >= 2 and ps[-2][0] == v and ps[-2][1] > 1 and \
             (all(r == v for r, _ in ps) or (v == 16 and n // v <= 128)):
         arith -= 4 * (v - 2)
-    if kind in ("conv", "conv_r2", "conv_timed", "conv_psf", "apply", "apply_r2") and mid != "none":
+    if kind in ("conv", "conv_r2", "conv_timed", "conv_psf", "conv_psf_dr", "apply", "apply_r2") and mid != "none":
         arith += 4 * v
     if kind == "plan_taps":
         arith += 2 * v                   # the 1/N scale
     lds = 2 * v * exchanges * (2 if two else 1)
     if kind in ("c2c_fwd", "c2c_inv"):
         lds += 2 * v                     # the digit <-> natural exchange
-    if kind in ("conv", "conv_r2", "conv_timed", "apply", "apply_r2") and mid != "none" and v == 16 and n >= 2048:
-        lds += 2 * v                     # the digit-order filter handed over through LDS (mid_op_dr_staged)
-    loads = {"conv": v, "conv_timed": v, "conv_psf": v, "conv_r2": 2 * v, "fwd": v, "fwd_r2": 2 * v, "apply": v // 2,
+    if kind in ("conv", "conv_r2", "conv_timed", "conv_psf_dr", "apply", "apply_r2") and mid != "none" and \
+            v == 16 and n >= 2048:
+        lds += 2 * v                     # the digit-order filter handed over through LDS (dr_runs_stage)
+    loads = {"conv": v, "conv_timed": v, "conv_psf": v, "conv_psf_dr": v, "conv_r2": 2 * v, "fwd": v, "fwd_r2": 2 * v, "apply": v // 2,
              "apply_r2": v // 2, "c2c_fwd": v, "c2c_inv": v, "plan_taps": v}[kind]
     loads += twiddle_slots
-    if kind in ("conv", "conv_r2", "conv_timed", "conv_psf", "apply", "apply_r2") and mid != "none":
+    if kind in ("conv", "conv_r2", "conv_timed", "conv_psf", "conv_psf_dr", "apply", "apply_r2") and mid != "none":
         loads += v // 2
     stores = {"conv_r2": 2 * v, "apply_r2": 2 * v, "fwd": v // 2, "fwd_r2": v // 2,
               "plan_taps": v // 2}.get(kind, v)

@@ -74,12 +74,15 @@ def test_per_signal_filter_and_lane_layout(dev, variant, n, rng):
 
 @pytest.mark.parametrize("mid", ["mul", "conj"])
 @pytest.mark.parametrize("inplace", [False, True])
-def test_per_signal_lane_filters_n4096_full_batch(dev, mid, inplace):
-    """One lane-major filter per signal at N = 4096, radix 16 (the reference
-    bench's protocol): the library runs the kernel that issues each signal's
-    filter loads with its signal loads.  2^27 points, filters planned on the
-    device from random spectra; 16 signals across the batch bit-identical to
-    the oracle, which reads the same filters planned in digit order."""
+@pytest.mark.parametrize("layout", ["lane", "dr"])
+def test_per_signal_filters_n4096_full_batch(dev, mid, inplace, layout):
+    """One filter per signal at N = 4096, radix 16 (the reference bench's
+    protocol; with the digit-order filter, its exact call): the library runs
+    the kernels that issue each signal's filter loads with its signal loads
+    (lane-major pairs, or the digit order's 1 KiB runs handed to the lanes
+    through LDS).  2^27 points, filters planned on the device from random
+    spectra; 16 signals across the batch bit-identical to the oracle, which
+    reads the same filters planned in digit order."""
     import torch
     import fufft_amd as ff
     n, batch = 4096, (1 << 27) // 4096
@@ -88,7 +91,7 @@ def test_per_signal_lane_filters_n4096_full_batch(dev, mid, inplace):
     x = torch.randn(batch * n, dtype=torch.complex64, device=dev, generator=gen)
     spec = torch.randn(batch * n, dtype=torch.complex64, device=dev, generator=gen)
     flane = torch.empty_like(spec)
-    ff.plan_filter_device(spec, flane, n, count=batch, variant="v16", layout="lane", kind=ff.FILTER_SPECTRUM)
+    ff.plan_filter_device(spec, flane, n, count=batch, variant="v16", layout=layout, kind=ff.FILTER_SPECTRUM)
     idx = torch.from_numpy(np.linspace(0, batch - 1, 16).astype(np.int64)).to(dev)
     a_s = x.view(batch, n)[idx].cpu().numpy()
     s_s = spec.view(batch, n)[idx].contiguous()
@@ -96,8 +99,8 @@ def test_per_signal_lane_filters_n4096_full_batch(dev, mid, inplace):
     fdr_s = torch.empty_like(s_s)
     ff.plan_filter_device(s_s, fdr_s, n, count=16, variant="v16", layout="dr", kind=ff.FILTER_SPECTRUM)
     out = x if inplace else torch.empty_like(x)
-    print(f"case per-signal lane filters n=4096 full batch mid={mid} inplace={inplace}", flush=True)
-    ff.conv(x, flane, out, n=n, batch=batch, filt_stride=n, mid=mid, variant="v16", layout="lane")
+    print(f"case per-signal {layout} filters n=4096 full batch mid={mid} inplace={inplace}", flush=True)
+    ff.conv(x, flane, out, n=n, batch=batch, filt_stride=n, mid=mid, variant="v16", layout=layout)
     torch.cuda.synchronize()
     got = out.view(batch, n)[idx].cpu().numpy().reshape(-1)
     want = O.conv(a_s, fdr_s.cpu().numpy(), n, O.kernel_plan(n, 16), filt_stride=n, mid=mid)
