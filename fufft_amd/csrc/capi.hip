@@ -565,12 +565,13 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
    // N = 32768: one workgroup per transform, 32 values per lane
    if(conv_wide_plan(n, v)) return status_of(launch_conv_wide(p, static_cast<hipStream_t>(stream)));
-   // one filter per signal at radix 16, N = 4096: the kernels that load each
-   // signal's filter with the signal (K_CONV_PSF lane-major, K_CONV_PSF_DR the
-   // reference's digit order)
-   const bool psf = conv_psf_plan((int)n, v) && filt_stride == n && mid_needs_filter(mid) &&
-                    (layout == FUFFT_LAYOUT_LANE || layout == FUFFT_LAYOUT_DR);
-   const int kind = !psf ? K_CONV : layout == FUFFT_LAYOUT_LANE ? K_CONV_PSF : K_CONV_PSF_DR;
+   // one filter per signal at radix 16: the kernels that load each signal's
+   // filter with the signal (K_CONV_PSF lane-major, N = 1024 .. 4096;
+   // K_CONV_PSF_DR the reference's digit order, N = 2048 .. 4096)
+   const bool per_signal = filt_stride == n && mid_needs_filter(mid);
+   const int kind = per_signal && layout == FUFFT_LAYOUT_LANE && conv_psf_plan((int)n, v)  ? K_CONV_PSF
+                  : per_signal && layout == FUFFT_LAYOUT_DR && conv_psf_dr_plan((int)n, v) ? K_CONV_PSF_DR
+                                                                                           : K_CONV;
    return run_conv1d(kind, (int)n, v, p, stream);
 }
 

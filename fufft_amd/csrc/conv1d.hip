@@ -374,7 +374,7 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
          }
       case K_CONV_PSF_DR:
          // digit-order filters only (the launcher's choice)
-         if constexpr(conv_psf_plan(N, V)) {
+         if constexpr(conv_psf_dr_plan(N, V)) {
             return p.fl == FLT_DR ? launch_mid<N, V, LAYOUT, K_CONV_PSF_DR>(p, s) : hipErrorInvalidValue;
          } else {
             return hipErrorInvalidValue;

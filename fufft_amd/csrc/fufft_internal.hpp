@@ -65,8 +65,16 @@ enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_
        K_C2C_FWD = 6, K_C2C_INV = 7, K_PLAN_TAPS = 8, K_CONV_TIMED = 9, K_CONV_MID = 10,
        K_CONV_PSF = 11, K_CONV_PSF_DR = 12 };
 
-// the plans K_CONV_PSF and K_CONV_PSF_DR are built for
-constexpr bool conv_psf_plan(int n, int v) { return n == 4096 && v == 16; }
+// the plans K_CONV_PSF and K_CONV_PSF_DR are built for: radix 16 with whole
+// wavefronts per transform and room for the filter's 32 VGPRs within 128
+// (N = 8192 would pass them).  Same box, 2^27 points, one filter per signal,
+// bit-identical, Gpt/s against K_CONV: lane-major N = 1024 247.1 -> 254.0,
+// 2048 258.2 -> 263.3, 4096 234.0 -> 243.4; digit order N = 2048 260.8 ->
+// 268.0, 4096 239.5 -> 247.2, but N = 1024 258.6 -> 252.4: there
+// K_CONV reads the digit-order filter in place (no LDS hand-off at T = 64),
+// which the staged early read does not beat.
+constexpr bool conv_psf_plan(int n, int v) { return v == 16 && (n == 1024 || n == 2048 || n == 4096); }
+constexpr bool conv_psf_dr_plan(int n, int v) { return v == 16 && (n == 2048 || n == 4096); }
 
 // phase timer record of one workgroup (K_CONV_TIMED), TIMER_STRIDE words:
 // [0] HW_ID, [1] XCC_ID, [2] marks, [3] s_memrealtime ticks (100 MHz) from
