@@ -82,6 +82,8 @@ def parse():
     p.add_argument("--no-2d", action="store_true")
     p.add_argument("--no-c2c", action="store_true", help="skip the natural-order C2C line")
     p.add_argument("--no-vendor", action="store_true", help="skip the rocFFT chain comparison")
+    p.add_argument("--per-signal-sizes", default="",
+                   help="comma list of further N for the one-filter-per-signal legs (both filter layouts)")
     p.add_argument("--no-per-signal", action="store_true",
                    help="skip the one-filter-per-signal legs (fp32 and reference-format BFP at N)")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -858,6 +860,25 @@ def main():
             "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": "v16", "filter_layout": "dr",
             "bytes_per_point": 24, "achieved_gbs": round(24.0 * pts / a / 1e9, 1), "frac": frac(24.0 * pts, a),
             "rel_l2": r}
+        # the same two legs at further sizes (the reference's bench runs this
+        # protocol at every N, bench_fufft.cu:156-221)
+        by_size = {}
+        for s in [int(v) for v in args.per_signal_sizes.split(",") if v.strip()]:
+            if s == n:
+                continue
+            legs = {}
+            for key, lay, sv in (("lane", "lane", ff.fastest_variant(s, "lane")), ("reference_plan", "dr", "v16")):
+                a, r = bench_fp32(torch, ff, dev, s, pts, sv, args.sweep_steps, 3, stream, 4323 + s, SETTLE_S,
+                                  layout=lay, per_signal=True)
+                if not r <= 2e-6:
+                    print(json.dumps({"error": f"fp32 per-signal accuracy check failed at N={s} ({lay}): "
+                                               f"rel L2 {r:.3e}"}))
+                    sys.exit(1)
+                legs[key] = {"gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "variant": sv,
+                             "filter_layout": lay, "frac": frac(24.0 * pts, a), "rel_l2": r}
+            by_size[str(s)] = legs
+        if by_size:
+            line["per_signal_filter"]["by_size"] = by_size
 
     # seconds per call of the rocFFT chain by N: the reference's published
     # ratios are against the vendor chain (README.md:12-13, bench_fufft.cu:201-246)
