@@ -374,33 +374,51 @@ def bench_r2(torch, ff, dev, n, pts, steps, warmup, stream, seed):
             "rel_l2": rel}
 
 
-def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="auto"):
+def bench_large(torch, ff, dev, n, pts, steps, warmup, stream, seed, variant="auto", per_transform=False):
     """Four-step conv: batch pts/n of U[-1,1) signals, one
     shared filter in the chain order of the middle `variant` ("auto" = "v16",
-    the reference's run_large middle), in place.  Returns (seconds per call,
-    rel L2 of a sample)."""
+    the reference's run_large middle), in place.  per_transform: one chained
+    filter per transform, as the reference's run_large feeds it
+    (bench_fufft.cu:410-428; fufft::ref::run_large), planned on the device from
+    random natural-order spectra.  Returns (seconds per call, rel L2 of a
+    sample)."""
     batch = pts // n
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     x = (torch.rand(2 * pts, device=dev, generator=gen) * 2 - 1).view(torch.complex64)
     rng = np.random.default_rng(seed)
-    taps = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS, variant=variant)).to(dev)
     idx = torch.from_numpy(np.linspace(0, batch - 1, 8).astype(np.int64)).to(dev)
     xs = x.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
-    ff.conv_large(x, filt, n=n, batch=batch, variant=variant, stream=stream)
+    if per_transform:
+        spec = torch.randn(pts, dtype=torch.complex64, device=dev, generator=gen)
+        filt = torch.empty_like(spec)
+        ff.plan_filter_large_device(spec, filt, n, count=batch, variant=variant, stream=stream)
+        spec_s = spec.view(batch, n)[idx].cpu().numpy().astype(np.complex128)
+        stride = n
+    else:
+        taps = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)).astype(np.complex64)
+        filt = torch.from_numpy(ff.plan_filter_large(taps, n, kind=ff.FILTER_TAPS, variant=variant)).to(dev)
+        spec_s = np.fft.fft(taps.astype(np.complex128))[None, :]
+        stride = 0
+    ff.conv_large(x, filt, n=n, batch=batch, filt_stride=stride, variant=variant, stream=stream)
     torch.cuda.synchronize()
     ys = x.view(batch, n)[idx].cpu().numpy()
-    want = np.fft.ifft(np.fft.fft(xs, axis=1) * np.fft.fft(taps.astype(np.complex128))[None, :], axis=1)
+    want = np.fft.ifft(np.fft.fft(xs, axis=1) * spec_s, axis=1)
     rel = rel_l2(ys, want)
     # the call is in place, so the timed launches re-convolve their own output;
-    # they use an all-pass filter (unit-modulus spectrum, random phase) of the
-    # same cost, which keeps the data's norm fixed over any number of launches
-    phase = np.exp(2j * np.pi * rng.uniform(0, 1, n)).astype(np.complex64)
-    filt = torch.from_numpy(ff.plan_filter_large(phase, n, kind=ff.FILTER_SPECTRUM, variant=variant)).to(dev)
-    secs = time_launches(torch, lambda: ff.conv_large(x, filt, n=n, batch=batch, variant=variant, stream=stream),
+    # they use all-pass filters (unit-modulus spectra, random phase) of the
+    # same cost, which keep the data's norm fixed over any number of launches
+    if per_transform:
+        spec = torch.polar(torch.ones(pts, device=dev), torch.rand(pts, device=dev, generator=gen) * (2 * np.pi))
+        ff.plan_filter_large_device(spec, filt, n, count=batch, variant=variant, stream=stream)
+        del spec
+    else:
+        phase = np.exp(2j * np.pi * rng.uniform(0, 1, n)).astype(np.complex64)
+        filt = torch.from_numpy(ff.plan_filter_large(phase, n, kind=ff.FILTER_SPECTRUM, variant=variant)).to(dev)
+    secs = time_launches(torch, lambda: ff.conv_large(x, filt, n=n, batch=batch, filt_stride=stride,
+                                                      variant=variant, stream=stream),
                          steps, warmup, stream, SETTLE_S)
-    del x
+    del x, filt
     return secs / steps, rel
 
 
@@ -1009,6 +1027,20 @@ def main():
                         "rel_l2": r}
         # the default middle (the reference's) with the radix-8 one beside it
         large[str(s)] = {**legs["v16"], "variant": "v16", "r8_middle": legs["r8"]}
+        if not args.no_per_signal:
+            # the reference's own run_large protocol: one chained filter per
+            # transform, a fourth 8 B/pt stream (its 56 B/pt model is then the
+            # physical bytes)
+            a, r = bench_large(torch, ff, dev, s, pts, args.sweep_steps, 3, stream, 7 + s, variant="v16",
+                               per_transform=True)
+            if not r <= 2e-6:
+                print(json.dumps({"error": f"four-step (filter per transform) accuracy check failed at N={s}: "
+                                           f"rel L2 {r:.3e}"}))
+                sys.exit(1)
+            large[str(s)]["per_transform_filter"] = {
+                "what": "one chained filter per transform, as the reference's run_large (fufft::ref::run_large)",
+                "gpoints_s": round(pts / a / 1e9, 3), "ms": round(a * 1e3, 5), "bytes_per_point": 56,
+                "frac": frac(56.0 * pts, a), "rel_l2": r}
         if not args.no_vendor:
             # the reference times its four-step against the cuFFT chain at this N
             # (bench_fufft.cu:453-478); here rocFFT through torch.fft, same batch

@@ -1075,8 +1075,14 @@ int fufft_conv_large_f32(void* buf, const void* filt, int64_t filt_stride, int64
    if(batch == 0) return FUFFT_OK;
    hipStream_t s = static_cast<hipStream_t>(stream);
    // The three stages run over sub-batches small enough for the data to stay
-   // in the last-level cache from one stage to the next.
-   const int64_t sub = subbatch_items(n * 8, batch, SUBBATCH_FOURSTEP_MB);
+   // in the last-level cache from one stage to the next.  One filter per
+   // transform streams a sub-batch's worth of filter bytes through the
+   // middle as well, so the sub-batch is halved: data and filter slices
+   // together fill the cache.  N = 32768, filter per transform, Gpt/s at
+   // 64 / 96 / 128 / 192 / 256 MiB: 106.3 / 109.0 / 115.0 / 115.7 / 101.3
+   // (a shared filter: 117.1 / 123.5 / 128.6 / 133.3 / 136.8), same box.
+   const int64_t sub = subbatch_items(n * 8 * (filt_stride == n && mid_needs_filter(mid) ? 2 : 1), batch,
+                                      SUBBATCH_FOURSTEP_MB);
    for(int64_t t0 = 0; t0 < batch; t0 += sub) {
       const int64_t nb = batch - t0 < sub ? batch - t0 : sub;
       float2* a = static_cast<float2*>(buf) + t0 * n;
