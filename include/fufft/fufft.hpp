@@ -272,11 +272,8 @@ template<class Mid> constexpr bool is_mid()
           std::is_same<Mid, MidNothing>::value;
 }
 // the filter a Mid carries (none for MidNothing) and its stride: one per transform
-template<class Mid> const void* filter_of(const Mid& m)
-{
-   if constexpr(std::is_same<Mid, MidNothing>::value) return nullptr;
-   else return m.b;
-}
+template<class Mid> inline const void* filter_of(const Mid& m) { return m.b; }
+inline const void* filter_of(const MidNothing&) { return nullptr; }
 template<class Mid> constexpr int64_t stride_of(int64_t n) { return std::is_same<Mid, MidNothing>::value ? 0 : n; }
 }  // namespace plan
 
