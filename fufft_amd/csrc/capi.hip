@@ -568,8 +568,10 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    // one filter per signal at radix 16: the kernels that load each signal's
    // filter with the signal (K_CONV_PSF lane-major, N = 1024 .. 4096;
    // K_CONV_PSF_DR the reference's digit order, N = 2048 .. 4096)
-   const bool per_signal = filt_stride == n && mid_needs_filter(mid);
-   const int kind = per_signal && layout == FUFFT_LAYOUT_LANE && conv_psf_plan((int)n, v)  ? K_CONV_PSF
+   // (the opt-in XOR LDS layout, a comparison knob, runs the plain kernel)
+   const bool per_signal = filt_stride == n && mid_needs_filter(mid) && lds_layout() != LAYOUT_XOR;
+   const int kind = per_signal && layout == FUFFT_LAYOUT_LANE &&
+                    (conv_psf_plan((int)n, v) || conv_psf_late_plan((int)n, v))             ? K_CONV_PSF
                   : per_signal && layout == FUFFT_LAYOUT_DR && conv_psf_dr_plan((int)n, v) ? K_CONV_PSF_DR
                                                                                            : K_CONV;
    return run_conv1d(kind, (int)n, v, p, stream);

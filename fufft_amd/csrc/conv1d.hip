@@ -79,8 +79,12 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
    constexpr bool TIMED     = KIND == K_CONV_TIMED;
    // one filter per signal: its loads go out with the signal's (lane-major
    // pairs, or digit order handed to the lanes through LDS at the mid)
-   constexpr bool PSF       = (KIND == K_CONV_PSF || KIND == K_CONV_PSF_DR) && mid_reads_filter<MID>;
+   constexpr bool PSF_ANY   = (KIND == K_CONV_PSF || KIND == K_CONV_PSF_DR) && mid_reads_filter<MID>;
+   constexpr bool PSF       = PSF_ANY && (KIND == K_CONV_PSF_DR || conv_psf_plan(N, V));
    constexpr bool PSF_DR    = PSF && KIND == K_CONV_PSF_DR;
+   // where the registers allow no early read: the lane-major filter read at
+   // the mid as usual, streamed past the caches
+   constexpr bool PSF_LATE  = PSF_ANY && !PSF;
    // the signal read and the result written once per launch stream past the
    // caches in the single-launch conv and C2C; the four-step middle, the split
    // and 2D row kernels keep the default policy
@@ -118,7 +122,8 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
    Twiddles<PL> tw;
    tw.load(p.tw, L);
    // both halves in this launch: the forward's last twiddled chain serves the inverse
-   constexpr int KEEP_F = (KIND == K_CONV || KIND == K_CONV_MID || KIND == K_CONV_R2 || TIMED) ? KEEP_STORE : KEEP_NONE;
+   constexpr int KEEP_F = (KIND == K_CONV || KIND == K_CONV_MID || KIND == K_CONV_R2 || TIMED || PSF_LATE) ? KEEP_STORE
+                                                                                                      : KEEP_NONE;
    constexpr int KEEP_I = KEEP_F == KEEP_STORE ? KEEP_USE : KEEP_NONE;
    KeptChain<PL> kc;
    float2 r[V];
@@ -247,6 +252,7 @@ __device__ __forceinline__ void conv1d_body(const Conv1dParams& p, const uint32_
                r[2 * m + 1] = Op::apply(r[2 * m + 1], make_float2(pf[m].z, pf[m].w));
             }
          }
+         else if constexpr(PSF_LATE) mid_op_pairs<PL, MID, POL_NT>(r, fb, fb0 * 8u + L * 16u, T * 16u);
          else if constexpr(BPERM) mid_op<PL, MID>(r, fb, (fb0 + L) * 8u, T * 8u);
          else if(p.fl == FLT_DR) {
             // radix 16 from N = 2048 (the reference's own plan and filter
@@ -366,15 +372,15 @@ static hipError_t launch_kind(int kind, const Conv1dParams& p, hipStream_t s)
    switch(kind) {
       case K_CONV:    return launch_mid<N, V, LAYOUT, K_CONV>(p, s);
       case K_CONV_PSF:
-         // lane-major filters only (the launcher's choice)
-         if constexpr(conv_psf_plan(N, V)) {
+         // lane-major filters only, default LDS layouts (the launcher's choice)
+         if constexpr((conv_psf_plan(N, V) || conv_psf_late_plan(N, V)) && LAYOUT != LAYOUT_XOR) {
             return p.fl == FLT_LANE ? launch_mid<N, V, LAYOUT, K_CONV_PSF>(p, s) : hipErrorInvalidValue;
          } else {
             return hipErrorInvalidValue;
          }
       case K_CONV_PSF_DR:
-         // digit-order filters only (the launcher's choice)
-         if constexpr(conv_psf_dr_plan(N, V)) {
+         // digit-order filters only, default LDS layouts (the launcher's choice)
+         if constexpr(conv_psf_dr_plan(N, V) && LAYOUT != LAYOUT_XOR) {
             return p.fl == FLT_DR ? launch_mid<N, V, LAYOUT, K_CONV_PSF_DR>(p, s) : hipErrorInvalidValue;
          } else {
             return hipErrorInvalidValue;

@@ -75,6 +75,13 @@ enum { K_CONV = 0, K_CONV_R2 = 1, K_FWD = 2, K_APPLY = 3, K_FWD_R2 = 4, K_APPLY_
 // which the staged early read does not beat.
 constexpr bool conv_psf_plan(int n, int v) { return v == 16 && (n == 1024 || n == 2048 || n == 4096); }
 constexpr bool conv_psf_dr_plan(int n, int v) { return v == 16 && (n == 2048 || n == 4096); }
+// the plan K_CONV_PSF runs with a late filter read, streamed past the caches
+// (NT) as each filter is read once: radix 8 at N = 512, whose 8 wavefronts
+// per SIMD leave no registers for an early read (263.7 -> 268.7 Gpt/s, same
+// box, bit-identical).  At radix 16 N = 8192 / 16384, where an early read
+// would pass 128 VGPRs, the late NT read measured 235.8 -> 215.8 and 217.0 ->
+// 213.3, so those sizes keep the plain kernel.
+constexpr bool conv_psf_late_plan(int n, int v) { return v == 8 && n == 512; }
 
 // phase timer record of one workgroup (K_CONV_TIMED), TIMER_STRIDE words:
 // [0] HW_ID, [1] XCC_ID, [2] marks, [3] s_memrealtime ticks (100 MHz) from

@@ -590,7 +590,7 @@ enum { FLT_DR = 0, FLT_LANE = 1, FLT_BPERM = 2 };
 // contiguous), 16*T lane-major.  MID is a template parameter: a runtime
 // branch between two products makes the compiler keep both results live
 // across the join.
-template<class PL, int MID>
+template<class PL, int MID, int POL = POL_DEFAULT>
 __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, uint32_t voff, uint32_t mstep)
 {
    using Op = MidOf<MID>;
@@ -598,7 +598,7 @@ __device__ __forceinline__ void mid_op_pairs(float2 (&r)[PL::V], const Buf& f, u
       float2 b[PL::V];
 #pragma unroll
       for(int m = 0; m < PL::V / 2; m++) {
-         const float4 q = f.ld4(voff, m * mstep);
+         const float4 q = f.ld4<POL>(voff, m * mstep);
          b[2 * m] = make_float2(q.x, q.y);
          b[2 * m + 1] = make_float2(q.z, q.w);
       }

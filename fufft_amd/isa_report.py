@@ -206,8 +206,11 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
     # pass has one group per lane and the registers allow it (KeptChain): pure
     # powers of the radix, and radix 16 up to N = 2048 behind a lead pass;
     # R - 2 fewer complex products per lane, 6 at radix 8 and 14 at radix 16
-    # (the per-signal kernels conv_psf / conv_psf_dr hold their filter in those registers instead)
-    if two and kind not in ("conv_psf", "conv_psf_dr") and len(ps) >= 2 and ps[-2][0] == v and ps[-2][1] > 1 and \
+    # (the per-signal kernels that read their filter early, conv_psf at radix 16 N = 1024 .. 4096 and
+    # conv_psf_dr, hold it in those registers instead; conv_psf at radix 8 N = 512 reads it late and
+    # keeps the chain)
+    early = kind == "conv_psf_dr" or (kind == "conv_psf" and v == 16 and n in (1024, 2048, 4096))
+    if two and not early and len(ps) >= 2 and ps[-2][0] == v and ps[-2][1] > 1 and \
             (all(r == v for r, _ in ps) or (v == 16 and n // v <= 128)):
         arith -= 4 * (v - 2)
     if kind in ("conv", "conv_r2", "conv_timed", "conv_psf", "conv_psf_dr", "apply", "apply_r2") and mid != "none":

@@ -56,7 +56,8 @@ def test_conv_matches_oracle_bitwise(dev, variant, n, mid, rng):
     assert O.rel_l2(got[:8 * n], truth) <= TOL_F32
 
 
-@pytest.mark.parametrize("variant,n", [("v16", 512), ("v16", 1024), ("v16", 2048), ("v16", 4096), ("r8", 1024)])
+@pytest.mark.parametrize("variant,n", [("v16", 512), ("v16", 1024), ("v16", 2048), ("v16", 4096), ("r8", 512),
+                                       ("r8", 1024)])
 def test_per_signal_filter_and_lane_layout(dev, variant, n, rng):
     batch = 64
     v = V[variant]
