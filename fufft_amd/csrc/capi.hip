@@ -432,8 +432,8 @@ int fufft_plan_chains(int64_t n, int variant, int* chains)
    const int np = fufft_plan_radices(n, variant, r);
    if(np < 0) return np;
    if(!chains) return FUFFT_ERR_INVALID;
-   // in-workgroup radix-16 passes use the even/odd chains, every other pass
-   // the single chain (tw_evenodd / tw_single, fufft_device.hpp)
+   // in-workgroup radix-16 passes use the tap-parity chains, every other pass
+   // the single chain (chain_parity / chain_one, fufft_device.hpp)
    for(int i = 0; i < np; i++) chains[i] = r[i] == 16 ? FUFFT_CHAIN_EVENODD : FUFFT_CHAIN_SINGLE;
    return np;
 }

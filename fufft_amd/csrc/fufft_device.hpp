@@ -2,14 +2,16 @@
 // complex arithmetic, radix-2/4/8/16 butterflies, stage twiddles, the LDS
 // layout and the barrier used between passes.
 //
-// Arithmetic contract.  Every operation below is written in the same order,
-// with the same explicit fmaf, as the reference's device code and its CPU
-// transcription (fufft.cuh:208-450, 504-547, 652-720; verify_kernel.cpp:31-86,
-// 1000-1011), and the library is compiled with -ffp-contract=off.  The only
-// deliberate difference is the base twiddle W^j, which is read from a
-// correctly-rounded fp32 table instead of __sincosf.  The CPU oracle
-// (oracle/oracle.c, OR_TW_TABLE) follows the same contract, so kernel and
-// oracle agree bit for bit.
+// Arithmetic contract.  Every rounded operation below (an add, a product, an
+// explicit fmaf) takes the operands the matching step of the reference's
+// device code and CPU transcription takes (fufft.cuh:208-450, 504-547,
+// 652-720; verify_kernel.cpp:31-86, 1000-1011): the same radix-2 stages, the
+// same constant rotations and the same twiddle recurrences, here written as
+// generic networks over compile-time indices.  The library is compiled with
+// -ffp-contract=off.  The only deliberate difference is the base twiddle W^j,
+// which is read from a correctly-rounded fp32 table instead of __sincosf.  The
+// CPU oracle (oracle/oracle.c, OR_TW_TABLE) follows the same contract, so
+// kernel and oracle agree bit for bit.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -40,133 +42,130 @@ __device__ __forceinline__ float2 cmul_conj(float2 x, float2 y)
                       __builtin_fmaf(x.y, y.x, -x.x * y.y));
 }
 
-// x (+-i): a swap and a sign flip, no arithmetic
-template<int SIGN>
-__device__ __forceinline__ float2 cmul_i(float2 a)
+// x * W16^E, W16 = exp(SIGN 2 pi i / 16), E = 0..7: every stage twiddle of
+// a radix-2 network of at most 16 points is one of these.  A quarter turn
+// (E = 4) is a swap and a sign; the odd eighths (E = 2, 6) are
+// sqrt(1/2) (+-1 + SIGN i), one add per component and a scale; the odd
+// sixteenths are a general product with (cos, SIGN sin)(2 pi E / 16).
+// Each rounding step has the operands of the reference's MULTIPLY forms
+// (fufft.cuh:266-340, 534-547).
+template<int E, int SIGN>
+__device__ __forceinline__ float2 rot16(float2 x)
 {
-   return SIGN < 0 ? make_float2(a.y, -a.x) : make_float2(-a.y, a.x);
-}
-
-// x W8^1 = r2 (1, SIGN): 2 add + 2 mul
-template<int SIGN>
-__device__ __forceinline__ float2 cmul_w1(float2 a)
-{
-   return SIGN < 0 ? make_float2(FUFFT_R2 * (a.x + a.y), FUFFT_R2 * (a.y - a.x))
-                   : make_float2(FUFFT_R2 * (a.x - a.y), FUFFT_R2 * (a.x + a.y));
-}
-
-// x W8^3 = r2 (-1, SIGN)
-template<int SIGN>
-__device__ __forceinline__ float2 cmul_w3(float2 a)
-{
-   return SIGN < 0 ? make_float2(FUFFT_R2 * (a.y - a.x), FUFFT_R2 * (-a.x - a.y))
-                   : make_float2(FUFFT_R2 * (-a.x - a.y), FUFFT_R2 * (a.x - a.y));
-}
-
-// x W16^K
-template<int K, int SIGN>
-__device__ __forceinline__ float2 mul_w16(float2 x)
-{
+   static_assert(E >= 0 && E < 8, "rot16: E in 0..7");
    constexpr float s = (float)SIGN;
-   if constexpr(K == 0) return x;
-   else if constexpr(K == 1) return cmul(x, make_float2( FUFFT_C16, s * FUFFT_S16));
-   else if constexpr(K == 2) return cmul_w1<SIGN>(x);
-   else if constexpr(K == 3) return cmul(x, make_float2( FUFFT_S16, s * FUFFT_C16));
-   else if constexpr(K == 4) return cmul_i<SIGN>(x);
-   else if constexpr(K == 5) return cmul(x, make_float2(-FUFFT_S16, s * FUFFT_C16));
-   else if constexpr(K == 6) return cmul_w3<SIGN>(x);
-   else                      return cmul(x, make_float2(-FUFFT_C16, s * FUFFT_S16));
+   if constexpr(E == 0) {
+      return x;
+   } else if constexpr(E == 4) {
+      return make_float2(-s * x.y, s * x.x);
+   } else if constexpr(E == 2) {
+      // sqrt(1/2) (1 + SIGN i): one add or subtract per component, then the scale
+      return SIGN < 0 ? make_float2(FUFFT_R2 * (x.x + x.y), FUFFT_R2 * (x.y - x.x))
+                      : make_float2(FUFFT_R2 * (x.x - x.y), FUFFT_R2 * (x.x + x.y));
+   } else if constexpr(E == 6) {
+      // sqrt(1/2) (-1 + SIGN i)
+      return SIGN < 0 ? make_float2(FUFFT_R2 * (x.y - x.x), FUFFT_R2 * (-x.x - x.y))
+                      : make_float2(FUFFT_R2 * (-x.x - x.y), FUFFT_R2 * (x.x - x.y));
+   } else {
+      constexpr float cs = E == 1 ? FUFFT_C16 : E == 3 ? FUFFT_S16 : E == 5 ? -FUFFT_S16 : -FUFFT_C16;
+      constexpr float sn = E == 1 ? FUFFT_S16 : E == 3 ? FUFFT_C16 : E == 5 ?  FUFFT_C16 :  FUFFT_S16;
+      return cmul(x, make_float2(cs, s * sn));
+   }
 }
 
 // ---- butterflies on a register array ---------------------------------------
-// Each takes the R taps of one group, u[k] = r[OFF + k*STRIDE], and writes the
-// natural-order outputs back to the same registers.  All indices are
-// compile-time constants, so the arrays live in VGPRs.
+// An R-point DFT (R = 2, 4, 8, 16) of the taps u[k] = r[OFF + k*STRIDE], in
+// place, as log2(R) radix-2 decimation-in-frequency stages.  The stage of
+// half-width H maps each pair (x[k], x[k+H]) of a block of 2H to
+// (x[k] + x[k+H], (x[k] - x[k+H]) W_{2H}^k), and W_{2H}^k = W16^(8k/H).
+// After the last stage position p holds frequency bitrev(p), so the values
+// go back to the taps through that reversal and leave in natural order.
+// All indices are compile-time constants: the values stay in VGPRs.
+//
+// The order the butterflies are written in is the order the compiler's
+// scheduler starts from, and it shows in registers and time (up to 1.5%,
+// same box, bit-identical results).  The order kept: a network of 16 points
+// runs its first stage pair by pair and then each half to the end before the
+// other starts; a network of up to 8 points goes stage by stage, each block's
+// sums before its differences.
 
-template<int SIGN, int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void dft2(float2 (&r)[NR])
+// one block of 2H values from B: the H sums, then the H rotated differences
+template<int SIGN, int R, int B, int H, int K = 0>
+__device__ __forceinline__ void r2_sums(const float2 (&x)[R], float2 (&s)[H])
 {
-   const float2 u0 = r[OFF], u1 = r[OFF + STRIDE];
-   r[OFF]          = cadd(u0, u1);
-   r[OFF + STRIDE] = csub(u0, u1);
+   if constexpr(K < H) {
+      s[K] = cadd(x[B + K], x[B + K + H]);
+      r2_sums<SIGN, R, B, H, K + 1>(x, s);
+   }
 }
 
-template<int SIGN, int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void dft4(float2 (&r)[NR])
+template<int SIGN, int R, int B, int H, int K = 0>
+__device__ __forceinline__ void r2_diffs(float2 (&x)[R])
 {
-   const float2 u0 = r[OFF], u1 = r[OFF + STRIDE], u2 = r[OFF + 2 * STRIDE], u3 = r[OFF + 3 * STRIDE];
-   const float2 a0 = cadd(u0, u2), a1 = cadd(u1, u3);
-   const float2 a2 = csub(u0, u2), a3 = cmul_i<SIGN>(csub(u1, u3));
-   r[OFF]              = cadd(a0, a1);
-   r[OFF + 2 * STRIDE] = csub(a0, a1);
-   r[OFF + STRIDE]     = cadd(a2, a3);
-   r[OFF + 3 * STRIDE] = csub(a2, a3);
+   if constexpr(K < H) {
+      x[B + K + H] = rot16<K * 8 / H, SIGN>(csub(x[B + K], x[B + K + H]));
+      r2_diffs<SIGN, R, B, H, K + 1>(x);
+   }
 }
 
-// radix 8 as three radix-2 stages (fufft.cuh:377-405)
-template<int SIGN>
-__device__ __forceinline__ void dft8v(const float2* u, float2* v)
+// one block, pair by pair: the sum and the rotated difference of pair K
+template<int SIGN, int R, int B, int H, int K = 0>
+__device__ __forceinline__ void r2_paired(float2 (&x)[R])
 {
-   const float2 a0 = cadd(u[0], u[4]);
-   const float2 a1 = cadd(u[1], u[5]);
-   const float2 a2 = cadd(u[2], u[6]);
-   const float2 a3 = cadd(u[3], u[7]);
-   const float2 a4 = csub(u[0], u[4]);
-   const float2 a5 = cmul_w1<SIGN>(csub(u[1], u[5]));
-   const float2 a6 = cmul_i <SIGN>(csub(u[2], u[6]));
-   const float2 a7 = cmul_w3<SIGN>(csub(u[3], u[7]));
-
-   const float2 b0 = cadd(a0, a2);
-   const float2 b1 = cadd(a1, a3);
-   const float2 b2 = csub(a0, a2);
-   const float2 b3 = cmul_i<SIGN>(csub(a1, a3));
-   const float2 b4 = cadd(a4, a6);
-   const float2 b5 = cadd(a5, a7);
-   const float2 b6 = csub(a4, a6);
-   const float2 b7 = cmul_i<SIGN>(csub(a5, a7));
-
-   v[0] = cadd(b0, b1);  v[4] = csub(b0, b1);
-   v[2] = cadd(b2, b3);  v[6] = csub(b2, b3);
-   v[1] = cadd(b4, b5);  v[5] = csub(b4, b5);
-   v[3] = cadd(b6, b7);  v[7] = csub(b6, b7);
+   if constexpr(K < H) {
+      const float2 sum = cadd(x[B + K], x[B + K + H]);
+      x[B + K + H] = rot16<K * 8 / H, SIGN>(csub(x[B + K], x[B + K + H]));
+      x[B + K] = sum;
+      r2_paired<SIGN, R, B, H, K + 1>(x);
+   }
 }
 
-template<int SIGN, int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void dft8(float2 (&r)[NR])
+// one stage of half-width H over the blocks B0, B0 + 2H, ... below B0 + SPAN
+template<int SIGN, int R, int H, int B0, int SPAN, int B = B0>
+__device__ __forceinline__ void r2_stage(float2 (&x)[R])
 {
-   float2 u[8], v[8];
+   if constexpr(B < B0 + SPAN) {
+      if constexpr(SPAN > 8) {
+         r2_paired<SIGN, R, B, H>(x);
+      } else {
+         float2 s[H];
+         r2_sums<SIGN, R, B, H>(x, s);
+         r2_diffs<SIGN, R, B, H>(x);
 #pragma unroll
-   for(int k = 0; k < 8; k++) u[k] = r[OFF + k * STRIDE];
-   dft8v<SIGN>(u, v);
-#pragma unroll
-   for(int k = 0; k < 8; k++) r[OFF + k * STRIDE] = v[k];
+         for(int k = 0; k < H; k++) x[B + k] = s[k];
+      }
+      r2_stage<SIGN, R, H, B0, SPAN, B + 2 * H>(x);
+   }
 }
 
-// radix 16 = one radix-2 stage (x W16^k) feeding two radix-8s; outputs
-// interleave even/odd (fufft.cuh:673-689)
-template<int SIGN, int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void dft16(float2 (&r)[NR])
+// the network on the SPAN values from B0
+template<int SIGN, int R, int B0 = 0, int SPAN = R, int H = SPAN / 2>
+__device__ __forceinline__ void r2_network(float2 (&x)[R])
 {
-   float2 a[8], b[8], va[8], vb[8];
-#define FUFFT_R2STEP(K)                                                             \
-   a[K] = cadd(r[OFF + (K) * STRIDE], r[OFF + ((K) + 8) * STRIDE]);                \
-   b[K] = mul_w16<K, SIGN>(csub(r[OFF + (K) * STRIDE], r[OFF + ((K) + 8) * STRIDE]));
-   FUFFT_R2STEP(0) FUFFT_R2STEP(1) FUFFT_R2STEP(2) FUFFT_R2STEP(3)
-   FUFFT_R2STEP(4) FUFFT_R2STEP(5) FUFFT_R2STEP(6) FUFFT_R2STEP(7)
-#undef FUFFT_R2STEP
-   dft8v<SIGN>(a, va);
-   dft8v<SIGN>(b, vb);
-#pragma unroll
-   for(int k = 0; k < 8; k++) { r[OFF + (2 * k) * STRIDE] = va[k]; r[OFF + (2 * k + 1) * STRIDE] = vb[k]; }
+   if constexpr(H >= 1) {
+      r2_stage<SIGN, R, H, B0, SPAN>(x);
+      if constexpr(SPAN > 8) {
+         r2_network<SIGN, R, B0, SPAN / 2>(x);
+         r2_network<SIGN, R, B0 + SPAN / 2, SPAN / 2>(x);
+      } else {
+         r2_network<SIGN, R, B0, SPAN, H / 2>(x);
+      }
+   }
 }
+
+constexpr int bitrev_of(int p, int bits) { return bits == 0 ? 0 : ((p & 1) << (bits - 1)) | bitrev_of(p >> 1, bits - 1); }
+constexpr int log2_of(int r) { return r <= 1 ? 0 : 1 + log2_of(r >> 1); }
 
 template<int R, int SIGN, int OFF, int STRIDE, int NR>
 __device__ __forceinline__ void dftR(float2 (&r)[NR])
 {
-   if constexpr(R == 2)       dft2 <SIGN, OFF, STRIDE>(r);
-   else if constexpr(R == 4)  dft4 <SIGN, OFF, STRIDE>(r);
-   else if constexpr(R == 8)  dft8 <SIGN, OFF, STRIDE>(r);
-   else                       dft16<SIGN, OFF, STRIDE>(r);
+   static_assert(R == 2 || R == 4 || R == 8 || R == 16, "dftR: radix 2, 4, 8 or 16");
+   float2 x[R];
+#pragma unroll
+   for(int k = 0; k < R; k++) x[k] = r[OFF + k * STRIDE];
+   r2_network<SIGN, R>(x);
+#pragma unroll
+   for(int p = 0; p < R; p++) r[OFF + bitrev_of(p, log2_of(R)) * STRIDE] = x[p];
 }
 
 // ---- twiddles ----------------------------------------------------------------
@@ -184,24 +183,51 @@ __device__ __forceinline__ float2 tw_load(const float2* __restrict__ tw, int idx
    return SIGN < 0 ? make_float2(w.x, -w.y) : w;
 }
 
-// single chain, W^(jk) = W^(j(k-1)) * W^j  (fufft.cuh:436-450)
+// A pass multiplies tap k of a group by W^(jk), from a recurrence on the
+// table's W^j, so each product has the reference's operands.  With KEEP the
+// chains hand back the powers they made, pw[k] = W^(jk), for a pass that
+// needs the same twiddles conjugated (tw_kept_conj); the single chain keeps
+// its state there in any case, a local array the compiler drops.
+//  - one chain, pw[k] = pw[k-1] W^j (fufft.cuh:436-450), at every radix;
+//  - inside a workgroup at radix 16, one chain per tap parity: tap 2m + q
+//    takes W^(2j) times tap 2m - 2 + q's power, from W^(2j) and W^(3j), 7
+//    steps deep instead of 14 (fufft.cuh:701-720).
+// The forms below (the single chain's state in pw, the parity chains'
+// running pair) are the ones the kernels were measured with: other forms of
+// the same recurrences schedule differently, up to 1.5% slower.
 template<int R, int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void tw_single(float2 (&r)[NR], float2 w1)
+__device__ __forceinline__ void chain_one(float2 (&r)[NR], float2 w1, float2 (&pw)[R])
 {
-   float2 w = w1;
-   r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w);
-#pragma unroll
-   for(int k = 2; k < R; k++) { w = cmul(w, w1); r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], w); }
-}
-
-// the single chain that also hands back the powers it generated, w[k] = W^(jk)
-template<int R, int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void tw_single_keep(float2 (&r)[NR], float2 w1, float2 (&w)[R])
-{
-   w[1] = w1;
+   pw[1] = w1;
    r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w1);
 #pragma unroll
-   for(int k = 2; k < R; k++) { w[k] = cmul(w[k - 1], w1); r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], w[k]); }
+   for(int k = 2; k < R; k++) {
+      pw[k] = cmul(pw[k - 1], w1);
+      r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], pw[k]);
+   }
+}
+
+template<int OFF, int STRIDE, bool KEEP, int NR>
+__device__ __forceinline__ void chain_parity(float2 (&r)[NR], float2 w1, float2 (&pw)[16])
+{
+   const float2 sq = cmul(w1, w1);
+   if constexpr(KEEP) { pw[1] = w1; pw[2] = sq; }
+   r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w1);
+   float2 run[2] = {sq, cmul(sq, w1)};   // the powers of the even and odd taps
+   if constexpr(KEEP) pw[3] = run[1];
+#pragma unroll
+   for(int m = 1; m < 8; m++) {
+#pragma unroll
+      for(int q = 0; q < 2; q++) r[OFF + (2 * m + q) * STRIDE] = cmul(r[OFF + (2 * m + q) * STRIDE], run[q]);
+      if(m < 7) {
+#pragma unroll
+         for(int q = 0; q < 2; q++) run[q] = cmul(run[q], sq);
+         if constexpr(KEEP) {
+#pragma unroll
+            for(int q = 0; q < 2; q++) pw[2 * m + 2 + q] = run[q];
+         }
+      }
+   }
 }
 
 // Multiply by the conjugates of powers a forward chain generated.  The forward
@@ -215,50 +241,17 @@ __device__ __forceinline__ void tw_kept_conj(float2 (&r)[NR], const float2 (&w)[
    for(int k = 1; k < R; k++) r[OFF + k * STRIDE] = cmul(r[OFF + k * STRIDE], make_float2(w[k].x, -w[k].y));
 }
 
-// radix 16: even outputs by (W^2)^m, odd by W (W^2)^m -- two 7-step chains
-// (fufft.cuh:701-720)
-template<int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void tw_evenodd(float2 (&r)[NR], float2 w1)
-{
-   const float2 w2 = cmul(w1, w1);
-   r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w1);
-   float2 ze = w2, zo = cmul(w2, w1);
-#pragma unroll
-   for(int m = 1; m < 8; m++) {
-      r[OFF + 2 * m * STRIDE]       = cmul(r[OFF + 2 * m * STRIDE], ze);
-      r[OFF + (2 * m + 1) * STRIDE] = cmul(r[OFF + (2 * m + 1) * STRIDE], zo);
-      if(m < 7) { ze = cmul(ze, w2); zo = cmul(zo, w2); }
-   }
-}
-
-// the even/odd chains that also hand back the powers they generated, w[k] = W^(jk)
-template<int OFF, int STRIDE, int NR>
-__device__ __forceinline__ void tw_evenodd_keep(float2 (&r)[NR], float2 w1, float2 (&w)[16])
-{
-   const float2 w2 = cmul(w1, w1);
-   w[1] = w1;
-   w[2] = w2;
-   r[OFF + STRIDE] = cmul(r[OFF + STRIDE], w1);
-   float2 ze = w2, zo = cmul(w2, w1);
-   w[3] = zo;
-#pragma unroll
-   for(int m = 1; m < 8; m++) {
-      r[OFF + 2 * m * STRIDE]       = cmul(r[OFF + 2 * m * STRIDE], ze);
-      r[OFF + (2 * m + 1) * STRIDE] = cmul(r[OFF + (2 * m + 1) * STRIDE], zo);
-      if(m < 7) { ze = cmul(ze, w2); zo = cmul(zo, w2); w[2 * m + 2] = ze; w[2 * m + 3] = zo; }
-   }
-}
-
-// chain selection: in-workgroup radix-16 passes use the even/odd chains, every
+// chain selection: in-workgroup radix-16 passes use the parity chains, every
 // other pass (lead radices, the four-step outer radix-16 level) the single
-// chain -- exactly as in the reference's kernels
+// chain, as the reference's kernels do
 enum { CHAIN_SINGLE = 0, CHAIN_EVENODD = 1 };
 
 template<int R, int CHAIN, int OFF, int STRIDE, int NR>
 __device__ __forceinline__ void twiddle_group(float2 (&r)[NR], float2 w1)
 {
-   if constexpr(R == 16 && CHAIN == CHAIN_EVENODD) tw_evenodd<OFF, STRIDE>(r, w1);
-   else                                             tw_single<R, OFF, STRIDE>(r, w1);
+   float2 pw[R];
+   if constexpr(R == 16 && CHAIN == CHAIN_EVENODD) chain_parity<OFF, STRIDE, false>(r, w1, pw);
+   else                                             chain_one<R, OFF, STRIDE>(r, w1, pw);
 }
 
 // ---- buffer-resource memory access ---------------------------------------------------

@@ -290,8 +290,8 @@ __device__ __forceinline__ void compute_pass(float2 (&r)[PL::V], const Twiddles<
          dftR<R, SIGN, g, G>(r);
          if constexpr(!DIT) {
             if constexpr(keep && KEEP == KEEP_STORE) {
-               if constexpr(R == 16) tw_evenodd_keep<g, G>(r, w1, kc.w);
-               else                  tw_single_keep<R, g, G>(r, w1, kc.w);
+               if constexpr(R == 16) chain_parity<g, G, true>(r, w1, kc.w);
+               else                  chain_one<R, g, G>(r, w1, kc.w);
             }
             else                                     twiddle_group<R, CHAIN_EVENODD, g, G>(r, w1);
          }
