@@ -563,8 +563,11 @@ int fufft_conv_f32(const void* in, const void* filt, int64_t filt_stride,
    if((st = current_table(&p.tw)) != FUFFT_OK) return st;
    p.in0 = in; p.filt = filt; p.out0 = out;
    p.ntrans = (uint32_t)batch; p.scount = 1; p.mid = mid; p.fl = layout;
-   // N = 32768: one workgroup per transform, 32 values per lane
-   if(conv_wide_plan(n, v)) return status_of(launch_conv_wide(p, static_cast<hipStream_t>(stream)));
+   // N = 32768: one workgroup per transform, 32 values per lane; N = 16384 too
+   // for a shared lane-major filter
+   if(conv_wide_plan(n, v) ||
+      (conv_wide_shared_lane_plan(n, v) && mid_needs_filter(mid) && filt_stride == 0 && layout == FUFFT_LAYOUT_LANE))
+      return status_of(launch_conv_wide(p, (int)n, static_cast<hipStream_t>(stream)));
    // one filter per signal at radix 16: the kernels that load each signal's
    // filter with the signal (K_CONV_PSF lane-major, N = 1024 .. 4096;
    // K_CONV_PSF_DR the reference's digit order, N = 2048 .. 4096)

@@ -118,7 +118,15 @@ hipError_t launch_conv1d(int kind, int n, int v, int layout, const Conv1dParams&
 // as there), results bit for bit the radix-16 plan's.
 constexpr int CONV_WIDE_N = 32768;
 constexpr bool conv_wide_plan(int64_t n, int v) { return n == CONV_WIDE_N && v == 16; }
-hipError_t launch_conv_wide(const Conv1dParams& p, hipStream_t s);
+// N = 16384 on the same kernel (512 lanes, 68 KiB of LDS: two workgroups per
+// CU, where the workgroup kernel's 128 KiB allow one) for a shared lane-major
+// filter: 227.5 -> 233.8 Gpt/s (same box, 2^27 points, 10 alternating
+// rounds, bit-identical; 229.5 with its lead twiddles held, spilled).  With
+// the digit-order filter (each lane's 128 contiguous bytes read in place) it
+// measured 223.6 -> 192.3, with one lane-major filter per signal 219.2 ->
+// 196.8, so those keep the workgroup kernel.
+constexpr bool conv_wide_shared_lane_plan(int64_t n, int v) { return n == 16384 && v == 16; }
+hipError_t launch_conv_wide(const Conv1dParams& p, int n, hipStream_t s);
 
 // ---- filter planning on the device (plan.hip) ----------------------------------------
 struct GatherDigits {

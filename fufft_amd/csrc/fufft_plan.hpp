@@ -226,18 +226,22 @@ struct Twiddles {
    static constexpr int COUNT = slots_before(PL::NP) > 0 ? slots_before(PL::NP) : 1;
    float2 w[COUNT];
 
+   // the base twiddles of pass p, W^j of each of the lane's groups
+   template<int p>
+   __device__ __forceinline__ void load_pass(const Buf& tb, int L)
+   {
+      constexpr int R = PL::radix(p), M = PL::stride(p), G = PL::V / R;
+      if constexpr(M > 1) {
+#pragma unroll
+         for(int g = 0; g < G; g++)
+            w[slots_before(p) + g] = tb.ld2((uint32_t)(((L + g * PL::T) & (M - 1)) * 8), R * M * 8);
+      }
+   }
+
    __device__ __forceinline__ void load(const float2* table, int L)
    {
       const Buf tb(table, FUFFT_TW_ENTRIES * 8u);
-      static_for<PL::NP>([&](auto pi) {
-         constexpr int p = decltype(pi)::value;
-         constexpr int R = PL::radix(p), M = PL::stride(p), G = PL::V / R;
-         if constexpr(M > 1) {
-#pragma unroll
-            for(int g = 0; g < G; g++)
-               w[slots_before(p) + g] = tb.ld2((uint32_t)(((L + g * PL::T) & (M - 1)) * 8), R * M * 8);
-         }
-      });
+      static_for<PL::NP>([&](auto pi) { load_pass<decltype(pi)::value>(tb, L); });
    }
 };
 

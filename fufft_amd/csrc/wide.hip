@@ -38,6 +38,11 @@
 // MI355X: 199-207 Gpt/s with the lane-major filter, 187-195 with the
 // digit-order one, against 135-138 for the four-step chain at the same N (48
 // bytes per point over HBM and the Infinity Cache).
+//
+// N = 16384 runs the same code with 512 lanes (LEAD 4, eight groups per lane
+// in the lead pass): 68 KiB of LDS, so two workgroups share a CU and one's
+// loads overlap the other's passes.  fufft_conv_f32 takes it for a shared
+// lane-major filter (+2.8% over the workgroup kernel, bit-identical).
 #include "fufft_device.hpp"
 #include "fufft_plan.hpp"
 #include "fufft_internal.hpp"
@@ -46,7 +51,8 @@ namespace fufft {
 
 namespace {
 
-using WPlan = Plan<CONV_WIDE_N, 32, 16>;
+template<int N>
+using WPlan = Plan<N, 32, 16>;
 
 // Float slot layouts.  gfx950 serves the 4-byte LDS forms 32 lanes at a time
 // over 32 banks (bank = slot mod 32), each access of a paired form
@@ -77,7 +83,8 @@ struct Pad256 {
    static constexpr int cphys(int i) { return i + ((i >> 8) << 4); }
    static constexpr int size(int n) { return n + n / 16; }
 };
-static_assert(Pad16::size(CONV_WIDE_N) == Pad256::size(CONV_WIDE_N), "one buffer for both layouts");
+static_assert(Pad16::size(CONV_WIDE_N) == Pad256::size(CONV_WIDE_N) && Pad16::size(16384) == Pad256::size(16384),
+              "one buffer for both layouts");
 
 // one component (C = 0 real, 1 imaginary) of the lane's values out to pass P's
 // positions, or in from them
@@ -193,11 +200,11 @@ __device__ __forceinline__ void wide_mid(float2 (&r)[PL::V], const Buf& fb, uint
    }
 }
 
-template<int MID, int FLT>
-__global__ void __launch_bounds__(WPlan::T)
+template<int N_, int MID, int FLT>
+__global__ void __launch_bounds__(WPlan<N_>::T, 4)
 conv_wide_kernel(const Conv1dParams p)
 {
-   using PL = WPlan;
+   using PL = WPlan<N_>;
    constexpr int N = PL::N, T = PL::T, V = PL::V;
    extern __shared__ float ldsf[];
    const int L = threadIdx.x;
@@ -224,8 +231,18 @@ conv_wide_kernel(const Conv1dParams p)
       const Buf fb(p.filt, p.fcount * (uint32_t)N * 8u);
       wide_mid<PL, MID, FLT>(r, fb, modulo_count(t, p.fcount) * N, L);
    }
+   // At N = 16384 the lead pass holds eight groups' base twiddles per lane;
+   // read again for the inverse's lead pass (from the cache), they are free
+   // in between, and the kernel fits 128 VGPRs with no scratch (48-68 bytes
+   // per lane when held throughout).
+   constexpr bool RELOAD_LEAD = PL::V / PL::radix(0) > 4;
    static_for<PL::NP>([&](auto qi) {
       constexpr int P = PL::NP - 1 - decltype(qi)::value;
+      if constexpr(RELOAD_LEAD && P == 0) {
+         tw.template load_pass<0>(Buf(p.tw, FUFFT_TW_ENTRIES * 8u), L);
+#pragma unroll
+         for(int i = 0; i < PL::V / PL::radix(0); i++) asm volatile("" : "+v"(tw.w[i].x), "+v"(tw.w[i].y));
+      }
       compute_pass<PL, P, +1, true, KEEP_NONE>(r, tw, kc);
       if constexpr(P > 0) split_exchange<PL, P, P - 1>(r, ldsf, L);
    });
@@ -234,16 +251,16 @@ conv_wide_kernel(const Conv1dParams p)
    for(int q = 0; q < V; q++) ob.st2<POL_NT>(r[q], (uint32_t)L * 8u, q * T * 8);
 }
 
-template<int MID, int FLT>
+template<int N, int MID, int FLT>
 hipError_t launch_wide_mid(const Conv1dParams& p, hipStream_t s)
 {
-   const void* k = reinterpret_cast<const void*>(&conv_wide_kernel<MID, FLT>);
-   constexpr size_t shm = (size_t)Pad16::size(CONV_WIDE_N) * sizeof(float);
+   const void* k = reinterpret_cast<const void*>(&conv_wide_kernel<N, MID, FLT>);
+   constexpr size_t shm = (size_t)Pad16::size(N) * sizeof(float);
    static std::atomic<uint64_t> lds_ok{};
    if(const hipError_t e = ensure_dynamic_lds(k, shm, lds_ok); e != hipSuccess) return e;
    Conv1dParams arg = p;
    void* argv[] = { &arg };
-   return hipLaunchKernel(k, dim3(p.ntrans), dim3(WPlan::T), argv, shm, s);
+   return hipLaunchKernel(k, dim3(p.ntrans), dim3(WPlan<N>::T), argv, shm, s);
 }
 
 }  // namespace
@@ -251,7 +268,8 @@ hipError_t launch_wide_mid(const Conv1dParams& p, hipStream_t s)
 // Per-signal filters address with 32-bit byte offsets: beyond 4 GiB of them
 // the launch is split into chunks of transforms (signal, result and filter
 // advance together).
-hipError_t launch_conv_wide(const Conv1dParams& p, hipStream_t s)
+template<int N>
+hipError_t launch_conv_wide_n(const Conv1dParams& p, hipStream_t s)
 {
    if(p.ntrans == 0) return hipSuccess;
    if(!modulo_count_ok(p.fcount, p.ntrans)) return hipErrorInvalidValue;
@@ -259,12 +277,12 @@ hipError_t launch_conv_wide(const Conv1dParams& p, hipStream_t s)
    auto one = [&](const Conv1dParams& q) {
       return with_mid(q.mid, [&](auto m) {
          constexpr int MID = decltype(m)::value;
-         if constexpr(!mid_reads_filter<MID>) return launch_wide_mid<MID, FLT_DR>(q, s);
-         else return q.fl == FLT_LANE ? launch_wide_mid<MID, FLT_LANE>(q, s)
-                   : q.fl == FLT_BPERM ? launch_wide_mid<MID, FLT_BPERM>(q, s) : launch_wide_mid<MID, FLT_DR>(q, s);
+         if constexpr(!mid_reads_filter<MID>) return launch_wide_mid<N, MID, FLT_DR>(q, s);
+         else return q.fl == FLT_LANE ? launch_wide_mid<N, MID, FLT_LANE>(q, s)
+                   : q.fl == FLT_BPERM ? launch_wide_mid<N, MID, FLT_BPERM>(q, s) : launch_wide_mid<N, MID, FLT_DR>(q, s);
       });
    };
-   constexpr uint64_t bytes = (uint64_t)CONV_WIDE_N * 8;
+   constexpr uint64_t bytes = (uint64_t)N * 8;
    if((uint64_t)p.fcount * bytes <= 0xffffffffull) return one(p);
    if(p.fcount != p.ntrans) return hipErrorInvalidValue;
    const uint32_t step = (uint32_t)(0xffffffffull / bytes) & ~255u;
@@ -278,6 +296,13 @@ hipError_t launch_conv_wide(const Conv1dParams& p, hipStream_t s)
       if(const hipError_t e = one(q); e != hipSuccess) return e;
    }
    return hipSuccess;
+}
+
+hipError_t launch_conv_wide(const Conv1dParams& p, int n, hipStream_t s)
+{
+   if(n == CONV_WIDE_N) return launch_conv_wide_n<CONV_WIDE_N>(p, s);
+   if(n == 16384)       return launch_conv_wide_n<16384>(p, s);
+   return hipErrorInvalidValue;
 }
 
 }  // namespace fufft

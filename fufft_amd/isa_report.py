@@ -149,11 +149,11 @@ def decode_name(name: str) -> dict | None:
         # big: blocks of more than 64 points (LDS rendezvous of the block maxima)
         return {"family": "bfp", "n": n, "v": v, "layout": LAYOUTS[lay],
                 "kind": "conv_blocks" if big else "conv", "mid": MIDS[mid]}
-    # the N = 32768 conv (wide.hip): 32 values per lane, float exchanges
-    m = re.search(r"conv_wide_kernelILi(\d+)ELi(\d+)E", name)
+    # the N = 16384 / 32768 conv (wide.hip): 32 values per lane, float exchanges
+    m = re.search(r"conv_wide_kernelILi(\d+)ELi(\d+)ELi(\d+)E", name)
     if m:
-        mid, flt = map(int, m.groups())
-        return {"family": "wide", "n": 32768, "v": 32, "layout": "split", "kind": "conv", "mid": MIDS[mid],
+        n, mid, flt = map(int, m.groups())
+        return {"family": "wide", "n": n, "v": 32, "layout": "split", "kind": "conv", "mid": MIDS[mid],
                 "filter": FILTERS[flt]}
     return None
 
@@ -244,11 +244,12 @@ def model_conv(n: int, v: int, kind: str = "conv", mid: str = "mul") -> dict:
 
 
 def model_wide(mid: str = "mul", filt: str = "lane", n: int = 32768, v: int = 32) -> dict:
-    """The N = 32768 conv (wide.hip): the radix-16 plan with V/R groups per lane
-    in every pass (4 in the radix-8 lead, 2 in the radix-16 passes), no kept
-    chain; each exchange writes and reads both float components of the lane's
-    V values (V 8-byte equivalents each way); the filter as V/2 16-byte loads
-    (V 8-byte ones in bperm)."""
+    """The N = 16384 / 32768 conv (wide.hip): the radix-16 plan with V/R groups
+    per lane in every pass (8 / 4 in the radix-4 / radix-8 lead, 2 in the
+    radix-16 passes), no kept chain; each exchange writes and reads both float
+    components of the lane's V values (V 8-byte equivalents each way); the
+    filter as V/2 16-byte loads (V 8-byte ones in bperm).  A lead pass of more
+    than 4 groups per lane reads its base twiddles again for the inverse."""
     ps = plan(n, 16)
     one_dir = sum((v // r) * (DFT_OPS[r] + (4 * (2 * r - 3) if M > 1 else 0)) for r, M in ps)
     arith = 2 * one_dir + (4 * v if mid != "none" else 0)
@@ -257,6 +258,8 @@ def model_wide(mid: str = "mul", filt: str = "lane", n: int = 32768, v: int = 32
     # index ((L + g T) mod M = L mod M), and the compiler merges those loads
     t = n // v
     loads = v + sum((v // r) if M > t else 1 for r, M in ps if M > 1)
+    if v // ps[0][0] > 4:
+        loads += v // ps[0][0]
     if mid != "none":
         loads += v if filt == "bperm" else v // 2
     return {"fp32_arith_per_lane": arith, "lds_access_8B_per_lane": lds, "vmem_loads_per_wave": loads,
@@ -306,7 +309,7 @@ def conv_rows(rows=None) -> list:
         lds = (n + n // 16) * 4 if d["family"] == "wide" else lds_bytes_conv(n, v, d["layout"])
         occ = occupancy(r["meta"]["vgpr_count"], r["meta"].get("agpr_count", 0), lds, threads // 64)
         mod = model_conv(n, v, d["kind"], d["mid"]) if d["family"] == "conv1d" else \
-            model_wide(d["mid"], d["filter"]) if d["family"] == "wide" else None
+            model_wide(d["mid"], d["filter"], n) if d["family"] == "wide" else None
         out.append({**d, "vgpr": r["meta"]["vgpr_count"], "sgpr": r["meta"]["sgpr_count"],
                     "scratch": r["meta"].get("private_segment_fixed_size", 0),
                     "spills": r["meta"].get("vgpr_spill_count", 0) + r["meta"].get("sgpr_spill_count", 0),
